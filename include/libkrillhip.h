@@ -1,0 +1,249 @@
+/*
+ * libkrillhip.h -- C ABI of the MI355X (gfx950) int8 paged KV-cache library.
+ *
+ * Drop-in for Krill's int8 KV hot path.  Each entry point names the reference
+ * interface it replaces (paths relative to the srvsngh99/Krill source tree):
+ *
+ *   pool / sequences   QuantizedKVCache state   Sources/KrillCache/QuantizedKVCache.swift:17-146
+ *                      makeQuantizedKVCaches     Sources/KrillCache/QuantizedKVCache.swift:207-210
+ *   prefix entries     PrefixCache int8 API      Sources/KrillCache/PrefixCache.swift:161-308,:369-400,:511-551
+ *   kernels            KrillKernels registry     Sources/KrillKernels/KernelRegistry.swift:13-162
+ *
+ * Conventions
+ *   - Every call returns int32_t: KRILL_OK (0) or a negative KRILL_E_* code.
+ *     The library never aborts; krill_last_error() gives a per-thread message.
+ *   - Pointers named `dev_*` or documented as device pointers are HIP device
+ *     memory; everything else is host memory.  Kernels are asynchronous on the
+ *     given stream (NULL = the pool's stream).  Block-manager calls are host
+ *     only, thread-safe (one mutex per pool) and never synchronise the device.
+ *   - Tensor layouts follow the reference: new K/V and queries are
+ *     [B][H][L][D] (QuantizedKVCache.update input, QuantizedKVCache.swift:46),
+ *     snapshots are [B][H][S][D] u8 + [B][H][S][G] f16 (QuantizedKVSnapshot,
+ *     QuantizedKVCache.swift:150-157; G = 1 in the reference's row mode).
+ */
+#ifndef LIBKRILLHIP_H
+#define LIBKRILLHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KRILL_ABI_VERSION 1
+
+/* status codes */
+#define KRILL_OK 0
+#define KRILL_E_INVAL (-1)       /* bad argument */
+#define KRILL_E_NOMEM (-2)       /* block pool exhausted after eviction, or device OOM */
+#define KRILL_E_RANGE (-3)       /* length / index outside the valid range */
+#define KRILL_E_HIP (-4)         /* a HIP runtime call failed (message in krill_last_error) */
+#define KRILL_E_STATE (-5)       /* operation not allowed in this state (frozen / freed handle) */
+#define KRILL_E_UNSUPPORTED (-6) /* shape or mode this build does not handle */
+
+/* storage (quantizer) modes */
+#define KRILL_QUANT_REF_ROW 0 /* reference rows: per (token, head) min/max over D, truncating cast,
+                                 fp16 scale + fp16 zero (QuantizedKVCache.swift:181-197) */
+#define KRILL_QUANT_AFFINE_G64 1 /* affine 8-bit in groups of 64, fp16 scale + fp16 bias
+                                    (MLX affine quantize semantics, CheckpointQuantizer.swift:255-260) */
+
+/* element types */
+#define KRILL_DTYPE_F16 0
+#define KRILL_DTYPE_BF16 1
+#define KRILL_DTYPE_F32 2
+
+/* pool flags */
+#define KRILL_POOL_HOST_ONLY 1u /* block manager only: no device memory, kernels refused */
+
+/* pool options (krill_pool_set_option) */
+#define KRILL_OPT_SPLIT_BLOCKS 1 /* blocks per attention split; 0 = automatic */
+#define KRILL_OPT_ATTN_PATH 2    /* 0 auto (VALU <= 8 query rows per KV head, else MFMA), 1 VALU, 2 MFMA */
+
+typedef struct krill_pool *krill_pool_t;
+typedef void *krill_stream_t; /* hipStream_t */
+
+typedef struct krill_pool_desc {
+  int32_t num_layers;
+  int32_t num_kv_heads;
+  int32_t head_dim;      /* 64, 128 or 256 */
+  int32_t block_tokens;  /* must be 64 */
+  int32_t num_blocks;    /* physical blocks per layer */
+  int32_t quant_mode;    /* KRILL_QUANT_* */
+  int32_t in_dtype;      /* dtype of K/V/Q handed to the kernels: KRILL_DTYPE_BF16 or _F16 */
+  uint32_t flags;        /* KRILL_POOL_* */
+  float evict_watermark; /* occupancy that triggers LRU eviction of prefix entries; 0 -> 0.9 */
+  int32_t max_prefix_entries; /* in-memory entry cap (PrefixCache maxMemoryEntries); 0 -> 8 */
+  int32_t min_prefix_len;     /* PrefixCache minPrefixLength; 0 -> 8 */
+  int64_t max_entry_bytes;    /* per-entry KV byte cap (PrefixCache maxEntryBytes); <= 0 -> none */
+  uint64_t free_list_seed;    /* 0: blocks handed out in ascending order; else a seeded shuffle */
+} krill_pool_desc;
+
+typedef struct krill_pool_stats {
+  int32_t num_blocks;
+  int32_t blocks_used;   /* refcount > 0 */
+  int32_t blocks_free;
+  int32_t blocks_shared; /* refcount > 1 */
+  int32_t live_seqs;     /* caller-owned sequences */
+  int32_t prefix_entries;
+  int64_t appended_tokens;
+  int64_t cow_copies;
+  int64_t evicted_entries;
+  int64_t evicted_blocks;
+  int64_t pending_copies; /* COW block copies queued, not yet issued to a stream */
+  int64_t device_bytes;   /* bytes of the KV slab */
+  int64_t block_bytes;    /* bytes of one (layer, block) across all KV heads */
+} krill_pool_stats;
+
+typedef struct krill_snapshot {
+  void *keys;         /* u8  [B][H][S][D] device */
+  void *values;       /* u8  [B][H][S][D] device */
+  void *key_scales;   /* f16 [B][H][S][G] device */
+  void *key_zeros;    /* f16 [B][H][S][G] device (bias in affine mode) */
+  void *value_scales; /* f16 [B][H][S][G] device */
+  void *value_zeros;  /* f16 [B][H][S][G] device */
+} krill_snapshot;
+
+/* ---------------------------------------------------------------- misc */
+
+/* Last error message of the calling thread ("" if none). */
+const char *krill_last_error(void);
+int32_t krill_abi_version(void);
+
+/* ---------------------------------------------------------------- pool */
+
+/* Replaces makeQuantizedKVCaches(numLayers:) (QuantizedKVCache.swift:207-210):
+ * one pool holds every layer's cache for every sequence. */
+int32_t krill_pool_create(const krill_pool_desc *desc, krill_stream_t stream, krill_pool_t *out);
+int32_t krill_pool_destroy(krill_pool_t pool);
+int32_t krill_pool_get_stats(krill_pool_t pool, krill_pool_stats *out);
+int32_t krill_pool_set_stream(krill_pool_t pool, krill_stream_t stream);
+int32_t krill_pool_set_option(krill_pool_t pool, int32_t option, int64_t value);
+/* Issue queued copy-on-write block copies on `stream` (kernels do this
+ * themselves before they touch the pool). */
+int32_t krill_pool_flush(krill_pool_t pool, krill_stream_t stream);
+
+/* Introspection (tests, debugging): copy the per-block reference counts of
+ * the first min(cap, num_blocks) blocks.  No counterpart in the reference
+ * (it has no block pool). */
+int32_t krill_pool_refcounts(krill_pool_t pool, int32_t *out, int32_t cap);
+
+/* ----------------------------------------------------------- sequences */
+
+/* QuantizedKVCache.init (QuantizedKVCache.swift:25) */
+int32_t krill_seq_create(krill_pool_t pool, int32_t *seq_out);
+/* New sequence sharing the first n_tokens of `src` (blocks refcounted, no
+ * copy).  Replaces restoreQuantized(_:) + truncate(to:) of a prefix hit
+ * (QuantizedKVCache.swift:122-145, InferenceEngine.swift:1395-1417). */
+int32_t krill_seq_fork(krill_pool_t pool, int32_t src, int32_t n_tokens, int32_t *seq_out);
+/* reset() (QuantizedKVCache.swift:92-99) = truncate to 0; free drops the handle. */
+int32_t krill_seq_free(krill_pool_t pool, int32_t seq);
+int32_t krill_seq_reset(krill_pool_t pool, int32_t seq);
+/* sequenceLength (QuantizedKVCache.swift:28-30) */
+int32_t krill_seq_length(krill_pool_t pool, int32_t seq, int32_t *len_out);
+/* memorySizeBytes, per layer (QuantizedKVCache.swift:33-42) */
+int32_t krill_seq_memory_bytes(krill_pool_t pool, int32_t seq, int64_t *bytes_out);
+/* truncate(to:) (QuantizedKVCache.swift:135-145): no-op when n >= length or n < 0. */
+int32_t krill_seq_truncate(krill_pool_t pool, int32_t seq, int32_t n);
+/* The bookkeeping half of update(keys:values:) (QuantizedKVCache.swift:49-61):
+ * reserve L slots at the end, copy-on-write the tail block if it is shared,
+ * LRU-evict prefix entries once occupancy passes the watermark.  Writes L
+ * physical slot ids (block * 64 + offset) to slot_mapping_out (host).
+ * KRILL_E_NOMEM leaves the sequence unchanged. */
+int32_t krill_seq_reserve_append(krill_pool_t pool, int32_t seq, int32_t L, int32_t *slot_mapping_out);
+/* Physical block ids of a sequence (host). */
+int32_t krill_seq_block_table(krill_pool_t pool, int32_t seq, int32_t *out, int32_t cap, int32_t *n_out);
+/* Host block tables [B][max_blocks] (unused entries 0) and lengths [B] for a
+ * batch; replaces the per-epoch left-padded stack (BatchedDecode.swift:96-151)
+ * as the thing the batched forward consumes. */
+int32_t krill_batch_tables(krill_pool_t pool, const int32_t *seqs, int32_t B, int32_t max_blocks,
+                           int32_t *tables_out, int32_t *lens_out);
+
+/* ------------------------------------------------------ prefix entries */
+
+/* storeQuantized (PrefixCache.swift:369-400): keep the first n tokens of
+ * `seq` as an LRU entry (a frozen fork).  stored_out = 0 when skipped
+ * (n < min_prefix_len or over max_entry_bytes), 1 when stored. */
+int32_t krill_prefix_store(krill_pool_t pool, int32_t seq, const char *model_id, const char *media_hash,
+                           const int64_t *tokens, int32_t n, int32_t *stored_out);
+/* lookupQuantized (PrefixCache.swift:161-170 via scan :273-308): exact entry
+ * for tokens[0..checkLen) with checkLen stepping down by max(1, min/2).
+ * Miss: *prefix_len_out = 0, *entry_seq_out = -1. */
+int32_t krill_prefix_lookup(krill_pool_t pool, const char *model_id, const char *media_hash,
+                            const int64_t *tokens, int32_t n, int32_t *prefix_len_out, int32_t *entry_seq_out);
+/* lookupLongestPrefixQuantized (PrefixCache.swift:235-263): entry with the
+ * longest common prefix >= min_prefix_len (ties: most recently used). */
+int32_t krill_prefix_lookup_longest(krill_pool_t pool, const char *model_id, const char *media_hash,
+                                    const int64_t *tokens, int32_t n, int32_t *prefix_len_out,
+                                    int32_t *entry_seq_out);
+int32_t krill_prefix_clear(krill_pool_t pool);
+int32_t krill_prefix_count(krill_pool_t pool, int32_t *count_out);
+/* cacheKey (PrefixCache.swift:511-532): FNV-1a 64 of schema 3 || dtype tag ||
+ * model || 0xFF || media || 0xFF || tokens (8-byte little-endian). */
+int32_t krill_prefix_key(const char *model_id, const char *media_hash, int32_t dtype_tag,
+                         const int64_t *tokens, int64_t n, uint64_t *key_out);
+
+/* ------------------------------------------------------------- kernels */
+
+/* Fused quantize + paged append: the arithmetic half of update(keys:values:)
+ * (QuantizedKVCache.swift:49-61 with quantizePerHead :181-197, or the affine
+ * group-64 quantizer).  dev_k/dev_v: [B][Hkv][L][D] in the pool's in_dtype;
+ * dev_slot_mapping: [B][L] int32 (from krill_seq_reserve_append; < 0 skips). */
+int32_t krill_quantize_append(krill_pool_t pool, int32_t layer, const void *dev_k, const void *dev_v,
+                              const int32_t *dev_slot_mapping, int32_t B, int32_t L, krill_stream_t stream);
+/* Same with element strides (b, h, l) of K and V (d contiguous), e.g. a
+ * projection output [B][L][Hkv][D]: (L*Hkv*D, D, Hkv*D). */
+int32_t krill_quantize_append_strided(krill_pool_t pool, int32_t layer, const void *dev_k,
+                                      const void *dev_v, int64_t stride_b, int64_t stride_h,
+                                      int64_t stride_l, const int32_t *dev_slot_mapping, int32_t B,
+                                      int32_t L, krill_stream_t stream);
+
+/* Paged -> contiguous snapshot.  left_pad = 0: quantizedSnapshot()
+ * (QuantizedKVCache.swift:106-115), tokens at [0, len), zeros after;
+ * left_pad = 1: stackCachesLeftPaddedQuantized (BatchedDecode.swift:96-151),
+ * tokens at [S_out - len, S_out), u8/f16 zeros before. */
+int32_t krill_gather(krill_pool_t pool, int32_t layer, const int32_t *dev_block_tables,
+                     const int32_t *dev_seq_lens, int32_t B, int32_t max_blocks, int32_t S_out,
+                     int32_t left_pad, const krill_snapshot *out, krill_stream_t stream);
+/* Paged -> dequantized fp16 K/V [B][H][S_out][D]: snapshot()
+ * (QuantizedKVCache.swift:82-89, dequantize :200-204). */
+int32_t krill_gather_dequant(krill_pool_t pool, int32_t layer, const int32_t *dev_block_tables,
+                             const int32_t *dev_seq_lens, int32_t B, int32_t max_blocks, int32_t S_out,
+                             int32_t left_pad, void *dev_k_out, void *dev_v_out, krill_stream_t stream);
+/* Contiguous snapshot -> paged: restoreQuantized(_:) (QuantizedKVCache.swift
+ * :122-129) and the int8 scatterBack slice (ContinuousBatcher.swift:743-801).
+ * Row b copies snapshot tokens [dev_src_start[b], +L) to dev_slot_mapping[b][0..L). */
+int32_t krill_scatter(krill_pool_t pool, int32_t layer, const krill_snapshot *in, int32_t B, int32_t S_in,
+                      const int32_t *dev_src_start, const int32_t *dev_slot_mapping, int32_t L,
+                      krill_stream_t stream);
+/* Copy whole blocks in every layer: dev_src_dst = n pairs (src, dst). */
+int32_t krill_copy_blocks(krill_pool_t pool, const int32_t *dev_src_dst, int32_t n, krill_stream_t stream);
+
+/* Workspace bytes for krill_decode_attention / krill_verify_attention. */
+int32_t krill_attention_workspace_size(krill_pool_t pool, int32_t B, int32_t Hq, int32_t Lq,
+                                       int32_t max_seq_len, size_t *bytes_out);
+/* Paged int8 decode attention, o = softmax(scale q K^T) V over each
+ * sequence's cached tokens (MLXFast.scaledDotProductAttention at
+ * Gemma4Model.swift:516-517 / Attention.swift:95-98 with the left-pad mask of
+ * BatchedDecode.swift:277-287).  dev_q: [B][Hq][1][D] in_dtype;
+ * dev_seq_lens include the token appended this step; out: [B][Hq][1][D]
+ * in out_dtype (F32, F16 or BF16).  max_seq_len: host bound on seq_lens. */
+int32_t krill_decode_attention(krill_pool_t pool, int32_t layer, const void *dev_q,
+                               const int32_t *dev_block_tables, const int32_t *dev_seq_lens, int32_t B,
+                               int32_t max_blocks, int32_t max_seq_len, int32_t Hq, float scale,
+                               void *dev_out, int32_t out_dtype, void *dev_ws, size_t ws_bytes,
+                               krill_stream_t stream);
+/* Speculative-verify / chunked-prefill attention: Lq new query rows per
+ * sequence, already appended, causal inside the window (row j sees tokens
+ * [0, len - Lq + j]; BatchedDecode.swift:299-312, LlamaModel.swift:186-202).
+ * dev_q / dev_out: [B][Hq][Lq][D]. */
+int32_t krill_verify_attention(krill_pool_t pool, int32_t layer, const void *dev_q, int32_t Lq,
+                               const int32_t *dev_block_tables, const int32_t *dev_seq_lens, int32_t B,
+                               int32_t max_blocks, int32_t max_seq_len, int32_t Hq, float scale,
+                               void *dev_out, int32_t out_dtype, void *dev_ws, size_t ws_bytes,
+                               krill_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LIBKRILLHIP_H */

@@ -1,0 +1,224 @@
+"""Reference-shaped cache API over a KVPool.
+
+Mirrors the Swift surfaces the Krill batcher calls, with the reference's
+names and argument meaning:
+
+* ``QuantizedKVSnapshot``      Sources/KrillCache/QuantizedKVCache.swift:150-173
+* ``PagedQuantizedKVCache``    QuantizedKVCache (QuantizedKVCache.swift:17-146):
+  update / snapshot / reset / sequence_length / memory_size_bytes /
+  quantized_snapshot / restore_quantized / truncate
+* ``make_quantized_kv_caches`` makeQuantizedKVCaches (QuantizedKVCache.swift:207-210)
+* ``PrefixCache``              the int8 half of PrefixCache
+  (PrefixCache.swift:161-308, :369-400, :511-551)
+
+The caches of one sequence share one block table, so all layers of a
+sequence hold the same token positions: a layer may append only the
+positions the sequence's other layers are also appending, and truncate /
+reset / restore apply to the whole sequence (the engine always does these to
+every layer together, InferenceEngine.swift:1402-1417).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from .pool import KVPool
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+@dataclass
+class QuantizedKVSnapshot:
+    """Six tensors of one layer: u8 keys/values [B,H,S,D], f16 scales/zeros [B,H,S,G]."""
+
+    keys: object
+    values: object
+    key_scales: object
+    key_zeros: object
+    value_scales: object
+    value_zeros: object
+
+    @property
+    def sequence_length(self) -> int:
+        return int(self.keys.shape[2])
+
+    @classmethod
+    def from_dict(cls, d: dict) -> "QuantizedKVSnapshot":
+        return cls(d["keys"], d["values"], d["key_scales"], d["key_zeros"], d["value_scales"], d["value_zeros"])
+
+    def as_dict(self) -> dict:
+        return {"keys": self.keys, "values": self.values, "key_scales": self.key_scales,
+                "key_zeros": self.key_zeros, "value_scales": self.value_scales, "value_zeros": self.value_zeros}
+
+
+class SequenceKV:
+    """One sequence of a KVPool; the per-layer caches are views of it."""
+
+    def __init__(self, pool: KVPool, seq: int | None = None):
+        self.pool = pool
+        self.seq = pool.seq_create() if seq is None else seq
+        self.layer_len = [0] * pool.num_layers
+        if seq is not None:
+            n = pool.seq_length(seq)
+            self.layer_len = [n] * pool.num_layers
+
+    @property
+    def length(self) -> int:
+        return self.pool.seq_length(self.seq)
+
+    def slots_for(self, layer: int, n: int) -> np.ndarray:
+        """Physical slots of positions [layer_len, layer_len + n) of `layer`,
+        reserving them when this layer is the first to reach them."""
+        start = self.layer_len[layer]
+        have = self.length
+        if start + n > have:
+            if start != have:
+                raise RuntimeError(f"layer {layer} appends at {start} while the sequence holds {have}")
+            self.pool.reserve_append(self.seq, n)
+        table = self.pool.block_table(self.seq)
+        pos = np.arange(start, start + n)
+        return (table[pos // 64] * 64 + pos % 64).astype(np.int32)
+
+    def truncate(self, n: int):
+        """QuantizedKVCache.truncate semantics (no-op unless 0 <= n < length)."""
+        if 0 <= n < self.length:
+            self.pool.seq_truncate(self.seq, n)
+            self.layer_len = [min(x, n) for x in self.layer_len]
+
+    def reset(self):
+        self.pool.seq_reset(self.seq)
+        self.layer_len = [0] * self.pool.num_layers
+
+    def free(self):
+        self.pool.seq_free(self.seq)
+
+    def tables(self, device="cuda"):
+        torch = _torch()
+        n = self.length
+        table = self.pool.block_table(self.seq)
+        t = torch.as_tensor(table.reshape(1, -1) if table.size else np.zeros((1, 1), np.int32), device=device)
+        return t.to(torch.int32), torch.tensor([n], dtype=torch.int32, device=device)
+
+
+class PagedQuantizedKVCache:
+    """One layer of one sequence (QuantizedKVCache.swift:17-146)."""
+
+    def __init__(self, seqkv: SequenceKV, layer: int):
+        self.s = seqkv
+        self.layer = layer
+
+    @property
+    def sequence_length(self) -> int:
+        return self.s.layer_len[self.layer]
+
+    @property
+    def memory_size_bytes(self) -> int:
+        """memorySizeBytes (QuantizedKVCache.swift:33-42) for this layer."""
+        n = self.sequence_length
+        p = self.s.pool
+        return 2 * n * p.num_kv_heads * p.head_dim + 4 * n * p.num_kv_heads * p.groups * 2
+
+    def append(self, keys, values):
+        """Quantize + append [1, Hkv, L, D] without dequantizing the cache."""
+        torch = _torch()
+        L = int(keys.shape[2])
+        slots = self.s.slots_for(self.layer, L)
+        sm = torch.as_tensor(slots.reshape(1, L), device=keys.device)
+        self.s.pool.quantize_append(self.layer, keys.contiguous(), values.contiguous(), sm)
+        self.s.layer_len[self.layer] += L
+
+    def update(self, keys, values):
+        """update(keys:values:) (QuantizedKVCache.swift:49-75): append, then
+        return the whole cache dequantized to fp16 [1, Hkv, T, D]."""
+        self.append(keys, values)
+        return self.snapshot()
+
+    def snapshot(self):
+        """snapshot() (QuantizedKVCache.swift:82-89): dequantized fp16 K/V or None."""
+        n = self.sequence_length
+        if n == 0:
+            return None
+        tables, lens = self._tables(n)
+        return self.s.pool.gather_dequant(self.layer, tables, lens, n)
+
+    def quantized_snapshot(self):
+        """quantizedSnapshot() (QuantizedKVCache.swift:106-115)."""
+        n = self.sequence_length
+        if n == 0:
+            return None
+        tables, lens = self._tables(n)
+        return QuantizedKVSnapshot.from_dict(self.s.pool.gather(self.layer, tables, lens, n))
+
+    def restore_quantized(self, snap: QuantizedKVSnapshot):
+        """restoreQuantized(_:) (QuantizedKVCache.swift:122-129) into fresh blocks."""
+        torch = _torch()
+        S = snap.sequence_length
+        if self.s.layer_len[self.layer] != 0:
+            if any(x != 0 for x in self.s.layer_len) and self.s.length > 0:
+                self.s.reset()
+        slots = self.s.slots_for(self.layer, S)
+        dev = snap.keys.device
+        self.s.pool.scatter(self.layer, snap.as_dict(), torch.zeros(1, dtype=torch.int32, device=dev),
+                            torch.as_tensor(slots.reshape(1, S), device=dev))
+        self.s.layer_len[self.layer] = S
+
+    def truncate(self, n: int):
+        self.s.truncate(n)
+
+    def reset(self):
+        self.s.reset()
+
+    def _tables(self, n: int):
+        torch = _torch()
+        table = self.s.pool.block_table(self.s.seq)
+        dev = "cuda"
+        return (torch.as_tensor(table.reshape(1, -1), device=dev).to(torch.int32),
+                torch.tensor([n], dtype=torch.int32, device=dev))
+
+
+def make_quantized_kv_caches(pool: KVPool, seq: int | None = None):
+    """makeQuantizedKVCaches(numLayers:) (QuantizedKVCache.swift:207-210)."""
+    s = SequenceKV(pool, seq)
+    return [PagedQuantizedKVCache(s, layer) for layer in range(pool.num_layers)]
+
+
+class PrefixCache:
+    """int8 prefix entries of one pool (PrefixCache.swift int8 API).
+
+    Entries are frozen forks of a sequence: storing shares its blocks
+    (refcounted, no copy) and a hit forks a new sequence from the entry."""
+
+    def __init__(self, pool: KVPool, model_id: str = ""):
+        self.pool = pool
+        self.model_id = model_id
+
+    @staticmethod
+    def common_prefix_length(a, b) -> int:
+        """PrefixCache.commonPrefixLength (PrefixCache.swift:266-271)."""
+        n = min(len(a), len(b))
+        i = 0
+        while i < n and a[i] == b[i]:
+            i += 1
+        return i
+
+    def store_quantized(self, tokens, seq: int, media_hash=None) -> bool:
+        return self.pool.prefix_store(seq, tokens, self.model_id, media_hash)
+
+    def lookup_quantized(self, tokens, media_hash=None):
+        """(prefix_len, entry_seq) of an exact entry, or (0, None)."""
+        return self.pool.prefix_lookup(tokens, self.model_id, media_hash)
+
+    def lookup_longest_prefix_quantized(self, tokens, media_hash=None):
+        return self.pool.prefix_lookup_longest(tokens, self.model_id, media_hash)
+
+    @property
+    def memory_count(self) -> int:
+        return self.pool.prefix_count()
+
+    def clear(self):
+        self.pool.prefix_clear()

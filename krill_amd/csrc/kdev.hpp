@@ -1,0 +1,142 @@
+// Device-side definitions shared by the gfx950 kernels of libkrillhip:
+// pool layout, dtype conversions and wave64 helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace krill {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+enum { DT_F16 = 0, DT_BF16 = 1, DT_F32 = 2 };
+enum { MODE_REF = 0, MODE_AFFINE = 1 };
+
+constexpr int kBlockTokens = 64;
+
+// Layout of one (layer, block, kv-head) region of the pool, D = head_dim,
+// G = scale/zero groups per token (1 in the reference's row mode, D/64 in the
+// affine group-64 mode):
+//   [0, 64*D)          K bytes, d-chunk major:  ((d/32)*64 + t)*32 + d%32
+//   [64*D, 128*D)      V bytes, token-group major, permuted inside each
+//                      32-token group:  ((t/32)*D + d)*32 + vpos(t%32)
+//   [128*D, +256*G)    K (scale, zero) fp16 pairs:  (t*G + g)*4
+//   [128*D+256*G, ..)  V (scale, zero) fp16 pairs
+// K rows of 32 consecutive d are 32-byte aligned so a 16x16x32 MFMA A
+// operand (8 d per lane) and the VALU score loop (32 d per lane) both load
+// contiguously; V stores 32 tokens of one d contiguously in the order the
+// MFMA P.V B operand produces them (lane quarter q holds tokens 4q..4q+3 and
+// 16+4q..16+4q+3), so P never has to be transposed.
+__host__ __device__ constexpr int head_region_bytes(int D, int G) { return 128 * D + 512 * G; }
+__host__ __device__ constexpr int v_offset(int D) { return 64 * D; }
+__host__ __device__ constexpr int km_offset(int D) { return 128 * D; }
+__host__ __device__ constexpr int vm_offset(int D, int G) { return 128 * D + 256 * G; }
+__host__ __device__ constexpr int k_byte(int t, int d) { return (((d >> 5) * 64 + t) << 5) + (d & 31); }
+// position of token tt (0..31) inside its 32-token group of a V row
+__host__ __device__ constexpr int vpos(int tt) {
+  return (((tt & 15) >> 2) << 3) + (tt & 3) + ((tt >> 4) << 2);
+}
+// inverse of vpos
+__host__ __device__ constexpr int vtok(int p) { return ((p >> 3) << 2) + (p & 3) + (((p >> 2) & 1) << 4); }
+__host__ __device__ constexpr int v_byte(int D, int t, int d) {
+  return 64 * D + (((t >> 5) * D + d) << 5) + vpos(t & 31);
+}
+
+// Device view of one layer of the pool.
+struct LayerView {
+  uint8_t *base;         // layer base
+  int64_t block_stride;  // bytes per block (all heads)
+  int32_t head_bytes;    // bytes per (block, head)
+  int32_t num_blocks;
+};
+
+__device__ __forceinline__ uint8_t *head_region(const LayerView &lv, int32_t block, int32_t h) {
+  return lv.base + (int64_t)block * lv.block_stride + (int64_t)h * lv.head_bytes;
+}
+
+// ---------------------------------------------------------------- dtypes
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32, round to nearest even
+}
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t x = __builtin_bit_cast(uint32_t, f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+  x += 0x7fffu + ((x >> 16) & 1u);
+  return (uint16_t)(x >> 16);
+}
+template <int DT>
+__device__ __forceinline__ float load_elem(const uint16_t *p) {
+  return DT == DT_BF16 ? bf16_bits_to_f32(*p) : f16_bits_to_f32(*p);
+}
+template <int DT>
+__device__ __forceinline__ float elem_to_f32(uint16_t v) {
+  return DT == DT_BF16 ? bf16_bits_to_f32(v) : f16_bits_to_f32(v);
+}
+// Round a binary32 value to the element dtype and back (round to nearest even).
+template <int DT>
+__device__ __forceinline__ float round_dt(float f) {
+  return DT == DT_BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(f)) : f16_bits_to_f32(f32_to_f16_bits(f));
+}
+
+__device__ __forceinline__ void store_out(void *out, int64_t idx, float v, int dt) {
+  if (dt == DT_F32)
+    reinterpret_cast<float *>(out)[idx] = v;
+  else if (dt == DT_F16)
+    reinterpret_cast<uint16_t *>(out)[idx] = f32_to_f16_bits(v);
+  else
+    reinterpret_cast<uint16_t *>(out)[idx] = f32_to_bf16_bits(v);
+}
+
+// ---------------------------------------------------------- byte unpacking
+
+// Two bytes of `w` as fp16 (1024 + byte): byte values ride in the mantissa of
+// 0x64XX, so one v_perm_b32 turns two bytes into two exact fp16 values.
+__device__ __forceinline__ half2_t bytes01_plus1024(uint32_t w) {
+  return __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u));
+}
+__device__ __forceinline__ half2_t bytes23_plus1024(uint32_t w) {
+  return __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u));
+}
+
+__device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {
+  return __builtin_amdgcn_fdot2(a, b, c, false);
+}
+
+__device__ __forceinline__ half2_t u32_as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t h2_as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// ---------------------------------------------------------- wave helpers
+
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+
+template <int FIRST, int LAST>
+__device__ __forceinline__ float wave_sum_range(float v) {
+#pragma unroll
+  for (int m = FIRST; m <= LAST; m <<= 1) v += shfl_xor(v, m);
+  return v;
+}
+template <int FIRST, int LAST>
+__device__ __forceinline__ float wave_max_range(float v) {
+#pragma unroll
+  for (int m = FIRST; m <= LAST; m <<= 1) v = fmaxf(v, shfl_xor(v, m));
+  return v;
+}
+template <int FIRST, int LAST>
+__device__ __forceinline__ float wave_min_range(float v) {
+#pragma unroll
+  for (int m = FIRST; m <= LAST; m <<= 1) v = fminf(v, shfl_xor(v, m));
+  return v;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace krill

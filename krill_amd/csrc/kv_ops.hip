@@ -1,0 +1,535 @@
+// gfx950 kernels that write and read the paged int8 pool: fused
+// quantize-append, gather (paged -> contiguous / left-padded snapshot),
+// dequantizing gather, scatter (snapshot -> paged), block copy (COW), and
+// the split-K merge of the attention kernels.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "block_manager.hpp"
+#include "kdev.hpp"
+#include "launch.hpp"
+
+namespace krill {
+
+static inline LayerView layer_view(const PoolGeometry &g, int32_t layer) {
+  LayerView lv;
+  lv.base = g.base + (int64_t)layer * g.layer_stride;
+  lv.block_stride = g.block_stride;
+  lv.head_bytes = g.head_bytes;
+  lv.num_blocks = g.num_blocks;
+  return lv;
+}
+
+// ---------------------------------------------------------------------------
+// Fused quantize + paged append.
+// Reference semantics (MODE_REF): QuantizedKVCache.quantizePerHead
+// (Sources/KrillCache/QuantizedKVCache.swift:181-197):
+//   mn, mx = min/max over D; scale = f32(dt(mx - mn)) / 255; safe = max(scale, 1e-8)
+//   q = u8(trunc(clip(f32(dt(x - mn)) / safe, 0, 255))); stores f16(safe), f16(mn)
+// Affine group-64 (MODE_AFFINE): values cast to fp16, per 64-group
+//   s = max((max-min)/255, 1e-7) signed toward the larger-magnitude edge,
+//   q0 = rint(edge/s), s = edge/q0 and bias = edge when q0 != 0 (else bias 0),
+//   q = min(rint((w - bias)/s), 255); fp16 scale/bias.
+// One wave64 per (row, K|V); each lane owns D/64 consecutive elements.
+// ---------------------------------------------------------------------------
+template <int D, int MODE, int DT>
+__global__ __launch_bounds__(256) void k_quantize_append(LayerView lv, const uint16_t *__restrict__ k,
+                                                         const uint16_t *__restrict__ v, int64_t sb,
+                                                         int64_t sh, int64_t sl,
+                                                         const int32_t *__restrict__ slots, int32_t B,
+                                                         int32_t L, int32_t Hkv) {
+  constexpr int E = D / 64;
+  constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t nrows = (int64_t)B * Hkv * L;
+  if (wave >= 2 * nrows) return;
+  const int kv = (int)(wave & 1);
+  const int64_t row = wave >> 1;
+  const int l = (int)(row % L);
+  const int h = (int)((row / L) % Hkv);
+  const int b = (int)(row / ((int64_t)L * Hkv));
+  const int slot = slots[(int64_t)b * L + l];
+  if (slot < 0) return;
+  const int blk = slot >> 6, t = slot & 63;
+  if (blk >= lv.num_blocks) return;
+  const uint16_t *src = (kv ? v : k) + (int64_t)b * sb + (int64_t)h * sh + (int64_t)l * sl;
+  const int d0 = lane * E;
+
+  float x[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) x[e] = elem_to_f32<DT>(src[d0 + e]);
+
+  uint8_t qb[E];
+  float scale, zero;
+  if constexpr (MODE == MODE_REF) {
+    float mn = x[0], mx = x[0];
+#pragma unroll
+    for (int e = 1; e < E; ++e) {
+      mn = fminf(mn, x[e]);
+      mx = fmaxf(mx, x[e]);
+    }
+    mn = wave_min_range<1, 32>(mn);
+    mx = wave_max_range<1, 32>(mx);
+    const float sc = round_dt<DT>(mx - mn) / 255.0f;
+    const float safe = sc > 1e-8f ? sc : 1e-8f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      float n = round_dt<DT>(x[e] - mn) / safe;
+      if (n < 0.0f) n = 0.0f;
+      if (n > 255.0f) n = 255.0f;
+      qb[e] = (uint8_t)(uint32_t)n;
+    }
+    scale = safe;
+    zero = mn;
+  } else {
+    constexpr int LPG = 64 / E;  // lanes per group of 64
+    float w[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) w[e] = DT == DT_F16 ? x[e] : f16_bits_to_f32(f32_to_f16_bits(x[e]));
+    float wmin = w[0], wmax = w[0];
+#pragma unroll
+    for (int e = 1; e < E; ++e) {
+      wmin = fminf(wmin, w[e]);
+      wmax = fmaxf(wmax, w[e]);
+    }
+    wmin = wave_min_range<1, LPG / 2>(wmin);
+    wmax = wave_max_range<1, LPG / 2>(wmax);
+    const bool side = fabsf(wmin) > fabsf(wmax);
+    float s = (wmax - wmin) / 255.0f;
+    if (!(s > 1e-7f)) s = 1e-7f;
+    s = side ? s : -s;
+    const float edge = side ? wmin : wmax;
+    const float q0 = rintf(edge / s);
+    float bias = 0.0f;
+    if (q0 != 0.0f) {
+      s = edge / q0;
+      bias = edge;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      float n = rintf((w[e] - bias) / s);
+      if (n > 255.0f) n = 255.0f;
+      if (n < 0.0f) n = 0.0f;
+      qb[e] = (uint8_t)(uint32_t)n;
+    }
+    scale = s;
+    zero = bias;
+  }
+
+  uint8_t *reg = head_region(lv, blk, h);
+  if (kv == 0) {
+    uint8_t *dst = reg + k_byte(t, d0);
+    if constexpr (E == 1) {
+      dst[0] = qb[0];
+    } else if constexpr (E == 2) {
+      *reinterpret_cast<uint16_t *>(dst) = (uint16_t)(qb[0] | (qb[1] << 8));
+    } else {
+      *reinterpret_cast<uint32_t *>(dst) =
+          (uint32_t)qb[0] | ((uint32_t)qb[1] << 8) | ((uint32_t)qb[2] << 16) | ((uint32_t)qb[3] << 24);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) reg[v_byte(D, t, d0 + e)] = qb[e];
+  }
+  const int g = MODE == MODE_AFFINE ? d0 / 64 : 0;
+  if ((d0 & (MODE == MODE_AFFINE ? 63 : (D - 1))) == 0) {
+    const uint32_t meta = (uint32_t)f32_to_f16_bits(scale) | ((uint32_t)f32_to_f16_bits(zero) << 16);
+    const int off = (kv ? vm_offset(D, G) : km_offset(D)) + ((t * G + g) << 2);
+    *reinterpret_cast<uint32_t *>(reg + off) = meta;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Gather: paged -> [B][H][S_out][D] u8 + [B][H][S_out][G] f16 x4.
+// left_pad = 1 reproduces stackCachesLeftPaddedQuantized
+// (Sources/KrillEngine/BatchedDecode.swift:96-151): right-aligned rows,
+// u8 0 / fp16 0 padding.  left_pad = 0 is quantizedSnapshot() with a zero tail.
+// One wave per output (b, h, s) row.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool resolve_token(const int32_t *tables, const int32_t *lens, int b,
+                                              int max_blocks, int num_blocks, int S_out, int left_pad,
+                                              int s, int *blk_out, int *t_out) {
+  const int len = lens[b];
+  const int ti = left_pad ? s - (S_out - len) : s;
+  if (ti < 0 || ti >= len || (ti >> 6) >= max_blocks) return false;
+  const int blk = tables[(int64_t)b * max_blocks + (ti >> 6)];
+  if ((unsigned)blk >= (unsigned)num_blocks) return false;
+  *blk_out = blk;
+  *t_out = ti & 63;
+  return true;
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(256) void k_gather(LayerView lv, const int32_t *__restrict__ tables,
+                                                const int32_t *__restrict__ lens, int32_t B, int32_t H,
+                                                int32_t max_blocks, int32_t S_out, int32_t left_pad,
+                                                uint8_t *keys, uint8_t *values, uint16_t *ks, uint16_t *kz,
+                                                uint16_t *vs, uint16_t *vz) {
+  constexpr int E = D / 64;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= (int64_t)B * H * S_out) return;
+  const int s = (int)(row % S_out);
+  const int h = (int)((row / S_out) % H);
+  const int b = (int)(row / ((int64_t)S_out * H));
+  int blk = 0, t = 0;
+  const bool valid = resolve_token(tables, lens, b, max_blocks, lv.num_blocks, S_out, left_pad, s, &blk, &t);
+  const uint8_t *reg = head_region(lv, blk, h);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int d = lane * E + e;
+    keys[row * D + d] = valid ? reg[k_byte(t, d)] : (uint8_t)0;
+    values[row * D + d] = valid ? reg[v_byte(D, t, d)] : (uint8_t)0;
+  }
+  if (lane < G) {
+    uint32_t km = 0, vm = 0;
+    if (valid) {
+      km = *reinterpret_cast<const uint32_t *>(reg + km_offset(D) + ((t * G + lane) << 2));
+      vm = *reinterpret_cast<const uint32_t *>(reg + vm_offset(D, G) + ((t * G + lane) << 2));
+    }
+    ks[row * G + lane] = (uint16_t)(km & 0xffffu);
+    kz[row * G + lane] = (uint16_t)(km >> 16);
+    vs[row * G + lane] = (uint16_t)(vm & 0xffffu);
+    vz[row * G + lane] = (uint16_t)(vm >> 16);
+  }
+}
+
+// Dequantizing gather: fp16 K/V [B][H][S_out][D].
+// MODE_REF: f16(f16(f16(q) * s) + z), the two roundings of
+// QuantizedKVCache.dequantize (QuantizedKVCache.swift:200-204).
+// MODE_AFFINE: f16(s*q + b) rounded once.
+template <int D, int G, int MODE>
+__global__ __launch_bounds__(256) void k_gather_dequant(LayerView lv, const int32_t *__restrict__ tables,
+                                                        const int32_t *__restrict__ lens, int32_t B,
+                                                        int32_t H, int32_t max_blocks, int32_t S_out,
+                                                        int32_t left_pad, uint16_t *k_out,
+                                                        uint16_t *v_out) {
+  constexpr int E = D / 64;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= (int64_t)B * H * S_out) return;
+  const int s = (int)(row % S_out);
+  const int h = (int)((row / S_out) % H);
+  const int b = (int)(row / ((int64_t)S_out * H));
+  int blk = 0, t = 0;
+  const bool valid = resolve_token(tables, lens, b, max_blocks, lv.num_blocks, S_out, left_pad, s, &blk, &t);
+  const uint8_t *reg = head_region(lv, blk, h);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int d = lane * E + e;
+    uint16_t ko = 0, vo = 0;
+    if (valid) {
+      const int g = d / (D / G);
+      const uint32_t km = *reinterpret_cast<const uint32_t *>(reg + km_offset(D) + ((t * G + g) << 2));
+      const uint32_t vm = *reinterpret_cast<const uint32_t *>(reg + vm_offset(D, G) + ((t * G + g) << 2));
+      const float kq = (float)reg[k_byte(t, d)], vq = (float)reg[v_byte(D, t, d)];
+      const float kss = f16_bits_to_f32((uint16_t)(km & 0xffffu)), kzz = f16_bits_to_f32((uint16_t)(km >> 16));
+      const float vss = f16_bits_to_f32((uint16_t)(vm & 0xffffu)), vzz = f16_bits_to_f32((uint16_t)(vm >> 16));
+      if constexpr (MODE == MODE_REF) {
+        ko = f32_to_f16_bits(f16_bits_to_f32(f32_to_f16_bits(kq * kss)) + kzz);
+        vo = f32_to_f16_bits(f16_bits_to_f32(f32_to_f16_bits(vq * vss)) + vzz);
+      } else {
+        ko = f32_to_f16_bits(kss * kq + kzz);
+        vo = f32_to_f16_bits(vss * vq + vzz);
+      }
+    }
+    k_out[row * D + d] = ko;
+    v_out[row * D + d] = vo;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Scatter: snapshot rows [src_start[b], +L) -> slots[b][0..L).  Inverse of the
+// gather; restoreQuantized (QuantizedKVCache.swift:122-129) and the int8
+// scatterBack slice (ContinuousBatcher.swift:743-801).
+// ---------------------------------------------------------------------------
+template <int D, int G>
+__global__ __launch_bounds__(256) void k_scatter(LayerView lv, const uint8_t *__restrict__ keys,
+                                                 const uint8_t *__restrict__ values,
+                                                 const uint16_t *__restrict__ ks, const uint16_t *__restrict__ kz,
+                                                 const uint16_t *__restrict__ vs, const uint16_t *__restrict__ vz,
+                                                 int32_t B, int32_t H, int32_t S_in,
+                                                 const int32_t *__restrict__ src_start,
+                                                 const int32_t *__restrict__ slots, int32_t L) {
+  constexpr int E = D / 64;
+  const int lane = threadIdx.x & 63;
+  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w >= (int64_t)B * L * H) return;
+  const int h = (int)(w % H);
+  const int i = (int)((w / H) % L);
+  const int b = (int)(w / ((int64_t)H * L));
+  const int slot = slots[(int64_t)b * L + i];
+  const int st = src_start[b] + i;
+  if (slot < 0 || st < 0 || st >= S_in) return;
+  const int blk = slot >> 6, t = slot & 63;
+  if (blk >= lv.num_blocks) return;
+  const int64_t row = ((int64_t)b * H + h) * S_in + st;
+  uint8_t *reg = head_region(lv, blk, h);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int d = lane * E + e;
+    reg[k_byte(t, d)] = keys[row * D + d];
+    reg[v_byte(D, t, d)] = values[row * D + d];
+  }
+  if (lane < G) {
+    const uint32_t km = (uint32_t)ks[row * G + lane] | ((uint32_t)kz[row * G + lane] << 16);
+    const uint32_t vm = (uint32_t)vs[row * G + lane] | ((uint32_t)vz[row * G + lane] << 16);
+    *reinterpret_cast<uint32_t *>(reg + km_offset(D) + ((t * G + lane) << 2)) = km;
+    *reinterpret_cast<uint32_t *>(reg + vm_offset(D, G) + ((t * G + lane) << 2)) = vm;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Whole-block copies (copy-on-write), every layer: one workgroup per
+// (pair, layer) streaming block_stride bytes with 16-byte accesses.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_copy_blocks(uint8_t *base, int64_t layer_stride, int64_t block_stride,
+                                                     int32_t num_blocks, int32_t num_layers,
+                                                     const int32_t *__restrict__ src_dst, int32_t n) {
+  const int pair = blockIdx.x / num_layers, layer = blockIdx.x % num_layers;
+  if (pair >= n) return;
+  const int src = src_dst[2 * pair], dst = src_dst[2 * pair + 1];
+  if ((unsigned)src >= (unsigned)num_blocks || (unsigned)dst >= (unsigned)num_blocks || src == dst) return;
+  const uint4 *s = reinterpret_cast<const uint4 *>(base + layer * layer_stride + src * block_stride);
+  uint4 *d = reinterpret_cast<uint4 *>(base + layer * layer_stride + dst * block_stride);
+  const int64_t n16 = block_stride >> 4;
+  for (int64_t i = threadIdx.x; i < n16; i += blockDim.x) d[i] = s[i];
+}
+
+// Same copy with up to 64 (src, dst) pairs passed by value in the kernel
+// arguments, for copy-on-write pairs queued by the host block manager.
+struct CopyPairsArg {
+  int32_t n;
+  int32_t sd[2 * 64];
+};
+__global__ __launch_bounds__(256) void k_copy_pairs(uint8_t *base, int64_t layer_stride, int64_t block_stride,
+                                                    int32_t num_blocks, int32_t num_layers, CopyPairsArg pa) {
+  const int pair = blockIdx.x / num_layers, layer = blockIdx.x % num_layers;
+  if (pair >= pa.n) return;
+  const int src = pa.sd[2 * pair], dst = pa.sd[2 * pair + 1];
+  if ((unsigned)src >= (unsigned)num_blocks || (unsigned)dst >= (unsigned)num_blocks || src == dst) return;
+  const uint4 *s = reinterpret_cast<const uint4 *>(base + layer * layer_stride + src * block_stride);
+  uint4 *d = reinterpret_cast<uint4 *>(base + layer * layer_stride + dst * block_stride);
+  const int64_t n16 = block_stride >> 4;
+  for (int64_t i = threadIdx.x; i < n16; i += blockDim.x) d[i] = s[i];
+}
+
+// ---------------------------------------------------------------------------
+// Split-K merge of attention partials (log2-domain running max m, sum l,
+// unnormalised o) into the output.  One wave per (row, kv-head, sequence).
+// Splits of one (sequence, kv-head) that saw no visible key carry m = -inf
+// and contribute nothing.  A sequence with one split was written directly by
+// the attention kernel; an empty sequence gets zeros.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void k_attn_merge(const float *__restrict__ ws_o, const float *__restrict__ ws_ml,
+                                                   const int32_t *__restrict__ lens, int32_t max_blocks,
+                                                   int32_t Hkv, int32_t NR, int32_t R, int32_t Lq, int32_t Hq,
+                                                   int32_t D, int32_t split_blocks, int32_t max_splits, void *out,
+                                                   int32_t out_dtype) {
+  const int r = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x;
+  const int len = lens[b];
+  const int nb = min(min((len + 63) >> 6, max_blocks), max_splits * split_blocks);
+  const int n_splits = (nb + split_blocks - 1) / split_blocks;
+  if (n_splits == 1) return;
+  const int hq = hk * R + r % R, j = r / R;
+  const int64_t obase = (((int64_t)b * Hq + hq) * Lq + j) * D;
+  const int64_t pbase = ((int64_t)b * Hkv + hk) * max_splits;
+  float M = -INFINITY;
+  for (int s = 0; s < n_splits; ++s) M = fmaxf(M, ws_ml[((pbase + s) * NR + r) * 2]);
+  float Lsum = 0.0f;
+  for (int s = 0; s < n_splits; ++s) {
+    const float m = ws_ml[((pbase + s) * NR + r) * 2];
+    Lsum += m == -INFINITY ? 0.0f : ws_ml[((pbase + s) * NR + r) * 2 + 1] * fast_exp2(m - M);
+  }
+  const float inv = (M == -INFINITY || !(Lsum > 0.0f)) ? 0.0f : 1.0f / Lsum;
+  for (int d = lane; d < D; d += 64) {
+    float acc = 0.0f;
+    for (int s = 0; s < n_splits; ++s) {
+      const float m = ws_ml[((pbase + s) * NR + r) * 2];
+      if (m != -INFINITY) acc += ws_o[((pbase + s) * NR + r) * (int64_t)D + d] * fast_exp2(m - M);
+    }
+    store_out(out, obase + d, acc * inv, out_dtype);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+#define KRILL_DISPATCH_D(D_, ...)                 \
+  switch (D_) {                                   \
+    case 64: {                                    \
+      constexpr int D = 64;                       \
+      __VA_ARGS__;                                \
+    } break;                                      \
+    case 128: {                                   \
+      constexpr int D = 128;                      \
+      __VA_ARGS__;                                \
+    } break;                                      \
+    case 256: {                                   \
+      constexpr int D = 256;                      \
+      __VA_ARGS__;                                \
+    } break;                                      \
+    default:                                      \
+      return hipErrorInvalidValue;                \
+  }
+
+static inline unsigned wave_blocks(int64_t waves) { return (unsigned)((waves + 3) / 4); }
+
+hipError_t launch_quantize_append(const PoolGeometry &g, int32_t layer, const void *k, const void *v,
+                                  int64_t sb, int64_t sh, int64_t sl, const int32_t *slots, int32_t B,
+                                  int32_t L, hipStream_t st) {
+  const int64_t waves = 2 * (int64_t)B * g.Hkv * L;
+  if (waves == 0) return hipSuccess;
+  const LayerView lv = layer_view(g, layer);
+  const uint16_t *kk = static_cast<const uint16_t *>(k), *vv = static_cast<const uint16_t *>(v);
+  const dim3 grid(wave_blocks(waves)), block(256);
+  KRILL_DISPATCH_D(g.D, {
+    if (g.mode == MODE_REF) {
+      if (g.in_dtype == DT_BF16)
+        k_quantize_append<D, MODE_REF, DT_BF16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, B, L, g.Hkv);
+      else
+        k_quantize_append<D, MODE_REF, DT_F16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, B, L, g.Hkv);
+    } else {
+      if (g.in_dtype == DT_BF16)
+        k_quantize_append<D, MODE_AFFINE, DT_BF16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, B, L, g.Hkv);
+      else
+        k_quantize_append<D, MODE_AFFINE, DT_F16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, B, L, g.Hkv);
+    }
+  });
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(const PoolGeometry &g, int32_t layer, const int32_t *tables, const int32_t *lens,
+                         int32_t B, int32_t max_blocks, int32_t S_out, int32_t left_pad, void *keys,
+                         void *values, void *ks, void *kz, void *vs, void *vz, hipStream_t st) {
+  const int64_t waves = (int64_t)B * g.Hkv * S_out;
+  if (waves == 0) return hipSuccess;
+  const LayerView lv = layer_view(g, layer);
+  const dim3 grid(wave_blocks(waves)), block(256);
+  auto *k8 = static_cast<uint8_t *>(keys), *v8 = static_cast<uint8_t *>(values);
+  auto *a = static_cast<uint16_t *>(ks), *bz = static_cast<uint16_t *>(kz), *c = static_cast<uint16_t *>(vs),
+       *d = static_cast<uint16_t *>(vz);
+  KRILL_DISPATCH_D(g.D, {
+    if (g.G == 1)
+      k_gather<D, 1><<<grid, block, 0, st>>>(lv, tables, lens, B, g.Hkv, max_blocks, S_out, left_pad, k8, v8, a, bz, c, d);
+    else
+      k_gather<D, D / 64><<<grid, block, 0, st>>>(lv, tables, lens, B, g.Hkv, max_blocks, S_out, left_pad, k8, v8, a, bz, c, d);
+  });
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_dequant(const PoolGeometry &g, int32_t layer, const int32_t *tables,
+                                 const int32_t *lens, int32_t B, int32_t max_blocks, int32_t S_out,
+                                 int32_t left_pad, void *k_out, void *v_out, hipStream_t st) {
+  const int64_t waves = (int64_t)B * g.Hkv * S_out;
+  if (waves == 0) return hipSuccess;
+  const LayerView lv = layer_view(g, layer);
+  const dim3 grid(wave_blocks(waves)), block(256);
+  auto *ko = static_cast<uint16_t *>(k_out), *vo = static_cast<uint16_t *>(v_out);
+  KRILL_DISPATCH_D(g.D, {
+    if (g.mode == MODE_REF)
+      k_gather_dequant<D, 1, MODE_REF><<<grid, block, 0, st>>>(lv, tables, lens, B, g.Hkv, max_blocks, S_out, left_pad, ko, vo);
+    else
+      k_gather_dequant<D, D / 64, MODE_AFFINE><<<grid, block, 0, st>>>(lv, tables, lens, B, g.Hkv, max_blocks, S_out, left_pad, ko, vo);
+  });
+  return hipGetLastError();
+}
+
+hipError_t launch_scatter(const PoolGeometry &g, int32_t layer, const void *keys, const void *values,
+                          const void *ks, const void *kz, const void *vs, const void *vz, int32_t B,
+                          int32_t S_in, const int32_t *src_start, const int32_t *slots, int32_t L,
+                          hipStream_t st) {
+  const int64_t waves = (int64_t)B * L * g.Hkv;
+  if (waves == 0) return hipSuccess;
+  const LayerView lv = layer_view(g, layer);
+  const dim3 grid(wave_blocks(waves)), block(256);
+  auto *k8 = static_cast<const uint8_t *>(keys), *v8 = static_cast<const uint8_t *>(values);
+  auto *a = static_cast<const uint16_t *>(ks), *bz = static_cast<const uint16_t *>(kz),
+       *c = static_cast<const uint16_t *>(vs), *d = static_cast<const uint16_t *>(vz);
+  KRILL_DISPATCH_D(g.D, {
+    if (g.G == 1)
+      k_scatter<D, 1><<<grid, block, 0, st>>>(lv, k8, v8, a, bz, c, d, B, g.Hkv, S_in, src_start, slots, L);
+    else
+      k_scatter<D, D / 64><<<grid, block, 0, st>>>(lv, k8, v8, a, bz, c, d, B, g.Hkv, S_in, src_start, slots, L);
+  });
+  return hipGetLastError();
+}
+
+hipError_t launch_copy_blocks(const PoolGeometry &g, const int32_t *src_dst, int32_t n, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  k_copy_blocks<<<dim3((unsigned)(n * g.num_layers)), dim3(256), 0, st>>>(
+      g.base, g.layer_stride, g.block_stride, g.num_blocks, g.num_layers, src_dst, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_copy_pairs(const PoolGeometry &g, const CopyPair *pairs, int32_t n, hipStream_t st) {
+  for (int32_t off = 0; off < n; off += 64) {
+    CopyPairsArg pa;
+    pa.n = std::min<int32_t>(64, n - off);
+    for (int32_t i = 0; i < pa.n; ++i) {
+      pa.sd[2 * i] = pairs[off + i].src;
+      pa.sd[2 * i + 1] = pairs[off + i].dst;
+    }
+    k_copy_pairs<<<dim3((unsigned)(pa.n * g.num_layers)), dim3(256), 0, st>>>(g.base, g.layer_stride, g.block_stride,
+                                                                            g.num_blocks, g.num_layers, pa);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq, int32_t max_seq_len,
+                       int32_t split_blocks, int32_t path, AttnPlan *plan) {
+  if (g.Hkv <= 0 || Hq <= 0 || Hq % g.Hkv != 0 || Lq <= 0 || B < 0 || max_seq_len < 0) return -1;
+  const int32_t R = Hq / g.Hkv;
+  AttnPlan p{};
+  p.NR = R * Lq;
+  p.use_mfma = path == 2 || (path == 0 && p.NR > 8);
+  if (!p.use_mfma && p.NR > 8) return -2;
+  // MFMA: at most 32 query rows per wave (16 for D = 256) keeps the score,
+  // output and operand tiles in registers without spilling.
+  const int32_t max_tiles = g.D >= 256 ? 1 : 2;
+  p.nrt = p.use_mfma ? std::min(max_tiles, (p.NR + 15) / 16) : 0;
+  p.row_groups = p.use_mfma ? (p.NR + 16 * p.nrt - 1) / (16 * p.nrt) : 1;
+  const int32_t nb_max = std::max(1, (max_seq_len + 63) / 64);
+  int32_t sb = split_blocks;
+  if (sb <= 0) {
+    // Aim for about 4096 workgroups over the longest sequence so the
+    // 256 CUs stay busy across ragged lengths; at least 2 blocks per split.
+    const int64_t units = (int64_t)B * g.Hkv * p.row_groups;
+    sb = (int32_t)std::max<int64_t>(2, ((int64_t)nb_max * units + 4095) / 4096);
+  }
+  sb = std::min(sb, nb_max);
+  p.split_blocks = sb;
+  p.max_splits = (nb_max + sb - 1) / sb;
+  const size_t o_bytes = (size_t)B * g.Hkv * p.max_splits * p.NR * g.D * sizeof(float);
+  const size_t ml_bytes = (size_t)B * g.Hkv * p.max_splits * p.NR * 2 * sizeof(float);
+  p.ws_bytes = ((o_bytes + 255) & ~(size_t)255) + ml_bytes;
+  *plan = p;
+  return 0;
+}
+
+hipError_t launch_attn_merge(const PoolGeometry &g, const AttnLaunch &a, const AttnPlan &p, hipStream_t st) {
+  if (p.max_splits <= 1 || a.B == 0) return hipSuccess;
+  const size_t o_bytes = (size_t)a.B * g.Hkv * p.max_splits * p.NR * g.D * sizeof(float);
+  const float *ws_o = static_cast<const float *>(a.ws);
+  const float *ws_ml = reinterpret_cast<const float *>(static_cast<const uint8_t *>(a.ws) + ((o_bytes + 255) & ~(size_t)255));
+  k_attn_merge<<<dim3((unsigned)p.NR, (unsigned)g.Hkv, (unsigned)a.B), dim3(64), 0, st>>>(
+      ws_o, ws_ml, a.lens, a.max_blocks, g.Hkv, p.NR, a.Hq / g.Hkv, a.Lq, a.Hq, g.D, p.split_blocks, p.max_splits, a.out,
+      a.out_dtype);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
+                            hipStream_t st) {
+  if (a.B == 0) return hipSuccess;
+  hipError_t e = p.use_mfma ? launch_attn_mfma(g, layer, a, p, st) : launch_attn_valu(g, layer, a, p, st);
+  if (e != hipSuccess) return e;
+  return launch_attn_merge(g, a, p, st);
+}
+
+}  // namespace krill

@@ -1,0 +1,71 @@
+// Host-side launch entry points of the gfx950 kernels (called by capi.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace krill {
+
+struct PoolGeometry {
+  uint8_t *base = nullptr;    // device slab
+  int64_t layer_stride = 0;   // bytes per layer
+  int64_t block_stride = 0;   // bytes per block (all heads)
+  int32_t head_bytes = 0;     // bytes per (block, head)
+  int32_t num_layers = 0, num_blocks = 0, Hkv = 0, D = 0, G = 1;
+  int32_t mode = 0;           // MODE_REF / MODE_AFFINE
+  int32_t in_dtype = 1;       // DT_F16 / DT_BF16
+};
+
+struct AttnLaunch {
+  const void *q;  // [B][Hq][Lq][D] in_dtype
+  const int32_t *tables;
+  const int32_t *lens;
+  int32_t B, max_blocks, max_seq_len, Hq, Lq;
+  float scale;
+  void *out;
+  int32_t out_dtype;
+  void *ws;
+  size_t ws_bytes;
+  int32_t split_blocks;  // 0 = automatic
+  int32_t path;          // 0 auto, 1 VALU, 2 MFMA
+};
+
+// Splits/rows plan shared by the workspace query and the launch.
+struct AttnPlan {
+  int32_t NR;           // query rows per KV head = (Hq/Hkv) * Lq
+  int32_t use_mfma;     // 1 when the MFMA kernel runs
+  int32_t split_blocks; // blocks per split
+  int32_t max_splits;
+  int32_t row_groups;   // MFMA: row groups of nrt 16-row tiles
+  int32_t nrt;          // MFMA: 16-row tiles per wave (register budget bound)
+  size_t ws_bytes;
+};
+
+int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq, int32_t max_seq_len,
+                       int32_t split_blocks, int32_t path, AttnPlan *plan);
+
+hipError_t launch_quantize_append(const PoolGeometry &g, int32_t layer, const void *k, const void *v,
+                                  int64_t sb, int64_t sh, int64_t sl, const int32_t *slots, int32_t B,
+                                  int32_t L, hipStream_t st);
+hipError_t launch_gather(const PoolGeometry &g, int32_t layer, const int32_t *tables, const int32_t *lens,
+                         int32_t B, int32_t max_blocks, int32_t S_out, int32_t left_pad, void *keys,
+                         void *values, void *ks, void *kz, void *vs, void *vz, hipStream_t st);
+hipError_t launch_gather_dequant(const PoolGeometry &g, int32_t layer, const int32_t *tables,
+                                 const int32_t *lens, int32_t B, int32_t max_blocks, int32_t S_out,
+                                 int32_t left_pad, void *k_out, void *v_out, hipStream_t st);
+hipError_t launch_scatter(const PoolGeometry &g, int32_t layer, const void *keys, const void *values,
+                          const void *ks, const void *kz, const void *vs, const void *vz, int32_t B,
+                          int32_t S_in, const int32_t *src_start, const int32_t *slots, int32_t L,
+                          hipStream_t st);
+hipError_t launch_copy_blocks(const PoolGeometry &g, const int32_t *src_dst, int32_t n, hipStream_t st);
+hipError_t launch_attention(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
+                            hipStream_t st);
+
+// Per-configuration kernels, defined in the attention translation units.
+hipError_t launch_attn_valu(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
+                            hipStream_t st);
+hipError_t launch_attn_mfma(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
+                            hipStream_t st);
+hipError_t launch_attn_merge(const PoolGeometry &g, const AttnLaunch &a, const AttnPlan &p, hipStream_t st);
+
+}  // namespace krill

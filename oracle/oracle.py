@@ -1,0 +1,325 @@
+"""Python face of the CPU oracle (oracle/krill_oracle.c).
+
+TEST INFRASTRUCTURE.  Only tests/, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of bench.py import this module, and only as the checker
+(or the timed CPU baseline).  The product package ``krill_amd`` never imports
+it; the GPU path fails loudly instead of falling back to anything here.
+
+How each oracle function is pinned (checked by something other than itself):
+
+==========================  ====================================================
+function                    pin
+==========================  ====================================================
+f16/bf16 conversions        exhaustive: all 65536 binary16 patterns round-trip;
+                            binary32 -> binary16 against numpy's IEEE cast on
+                            random and boundary values; bf16 against torch's
+                            CPU RNE cast (tests/test_oracle.py).
+quantize_ref (a1)           (1) tiny-input brute force with exact rational
+                            arithmetic (fractions.Fraction) of every rounding
+                            step; (2) the reference's own unit tests:
+                            Weyl-sequence tensors round-trip within 1.5 steps
+                            + 1e-3 / 1e-2 (QuantizedKVCacheUnitTests.swift
+                            :38-84); (3) closed-form special cases (constant
+                            row -> scale 0 after fp16 rounding, q = 0, zero =
+                            value; the row minimum always maps to q = 0);
+                            (4) committed golden vectors (tests/golden/).
+quantize_mlx (a1')          PARITY UNPINNED against mlx (third-party, absent).
+                            Pinned only by invariants: q in [0,255], group
+                            round-trip error <= |scale|/2 + fp16 rounding of
+                            scale/bias, the zero point exactly representable
+                            when q0 != 0, and brute force of the restated
+                            formula with Fractions on tiny groups.
+dequant_ref (a3)            exhaustive check of the two-rounding formula for
+                            every q byte against numpy float16 arithmetic.
+attention_f64 (a7/a8)       closed forms: one key -> output = that value row;
+                            equal keys -> output = mean of values; huge masked
+                            tail has no effect; brute force against an
+                            independent numpy softmax on tiny shapes.
+stack_left_padded (a5)      closed form of BatchedDecode.swift:119-147 on
+                            integer rows (tests/test_oracle.py).
+prefix_key (a10)            FNV-1a 64 published test vectors ("" and "a").
+==========================  ====================================================
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libkrill_oracle.so")
+_lib = None
+
+DT_F16 = 0
+DT_BF16 = 1
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile (gcc); returns the .so path."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.c_void_p
+        i32, i64, u64, f32, f64 = (ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64,
+                                   ctypes.c_float, ctypes.c_double)
+        L.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.oracle_f16_to_f32.restype = f32
+        L.oracle_f32_to_f16.argtypes = [f32]
+        L.oracle_f32_to_f16.restype = ctypes.c_uint16
+        L.oracle_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        L.oracle_bf16_to_f32.restype = f32
+        L.oracle_f32_to_bf16.argtypes = [f32]
+        L.oracle_f32_to_bf16.restype = ctypes.c_uint16
+        L.oracle_f16_to_f32_array.argtypes = [P, i64, P]
+        L.oracle_f32_to_f16_array.argtypes = [P, i64, P]
+        L.oracle_f32_to_bf16_array.argtypes = [P, i64, P]
+        L.oracle_quantize_ref_rows.argtypes = [P, i32, i64, i32, P, P, P]
+        L.oracle_quantize_mlx_affine.argtypes = [P, i32, i64, i32, i32, P, P, P]
+        L.oracle_dequant_ref_rows.argtypes = [P, P, P, i64, i32, P]
+        L.oracle_dequant_f64.argtypes = [P, P, P, i64, i32, i32, i32, P]
+        L.oracle_attention_f64.argtypes = [P, P, P, i32, i32, i32, P, f64, P]
+        L.oracle_stack_left_padded.argtypes = [P, P, P, P, i32, i32, i32, i32, i32, P, P, P]
+        L.oracle_fnv1a64.argtypes = [P, i64, u64]
+        L.oracle_fnv1a64.restype = u64
+        L.oracle_prefix_key.argtypes = [ctypes.c_char_p, ctypes.c_char_p, i32, P, i64]
+        L.oracle_prefix_key.restype = u64
+        L.oracle_common_prefix_length.argtypes = [P, i64, P, i64]
+        L.oracle_common_prefix_length.restype = i64
+        L.oracle_baseline_create.argtypes = [i32, i32, i32, i32, i32, P, u64]
+        L.oracle_baseline_create.restype = P
+        L.oracle_baseline_destroy.argtypes = [P]
+        L.oracle_baseline_threads.argtypes = [P]
+        L.oracle_baseline_threads.restype = i32
+        L.oracle_baseline_step.argtypes = [P, P, P, P, i32, f32, P, i32]
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# --------------------------------------------------------------------------
+# dtype helpers (bit patterns are carried as uint16 arrays)
+# --------------------------------------------------------------------------
+
+def f32_to_f16_bits(x) -> np.ndarray:
+    """numpy's IEEE RNE cast (the C conversion is tested bit-equal to it)."""
+    return np.ascontiguousarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def f16_bits_to_f32(h) -> np.ndarray:
+    return np.ascontiguousarray(h, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def c_f16_to_f32_array(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().oracle_f16_to_f32_array(_p(h), h.size, _p(out))
+    return out
+
+
+def c_f32_to_f16_array(f) -> np.ndarray:
+    f = np.ascontiguousarray(f, np.float32)
+    out = np.empty(f.shape, np.uint16)
+    lib().oracle_f32_to_f16_array(_p(f), f.size, _p(out))
+    return out
+
+
+def c_f32_to_bf16_array(f) -> np.ndarray:
+    f = np.ascontiguousarray(f, np.float32)
+    out = np.empty(f.shape, np.uint16)
+    lib().oracle_f32_to_bf16_array(_p(f), f.size, _p(out))
+    return out
+
+
+def c_f32_to_f16(v: float) -> int:
+    return int(lib().oracle_f32_to_f16(float(v)))
+
+
+def c_f16_to_f32(h: int) -> float:
+    return float(lib().oracle_f16_to_f32(int(h)))
+
+
+def f32_to_bf16_bits(x) -> np.ndarray:
+    """Vectorised RNE float32 -> bfloat16 bits (same rule as the C oracle)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
+def bf16_bits_to_f32(b) -> np.ndarray:
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def bits_to_f32(b, dt: int) -> np.ndarray:
+    if dt == DT_BF16:
+        return bf16_bits_to_f32(b)
+    return np.ascontiguousarray(b, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+# --------------------------------------------------------------------------
+# a1 / a1' / a3
+# --------------------------------------------------------------------------
+
+def quantize_ref(x_bits: np.ndarray, dt: int):
+    """Reference row quantizer over the last axis (QuantizedKVCache.swift:181-197).
+
+    Returns (q u8 [..., D], scale f16-bits [..., 1], zero f16-bits [..., 1])."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    D = x.shape[-1]
+    n = x.size // D
+    q = np.empty(x.shape, np.uint8)
+    s = np.empty(x.shape[:-1] + (1,), np.uint16)
+    z = np.empty(x.shape[:-1] + (1,), np.uint16)
+    lib().oracle_quantize_ref_rows(_p(x), dt, n, D, _p(q), _p(s), _p(z))
+    return q, s, z
+
+
+def quantize_mlx(x_bits: np.ndarray, dt: int, group: int = 64):
+    """MLX-style affine 8-bit group quantizer (parity unpinned, see header)."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    D = x.shape[-1]
+    G = D // group
+    n = x.size // D
+    q = np.empty(x.shape, np.uint8)
+    s = np.empty(x.shape[:-1] + (G,), np.uint16)
+    b = np.empty(x.shape[:-1] + (G,), np.uint16)
+    lib().oracle_quantize_mlx_affine(_p(x), dt, n, D, group, _p(q), _p(s), _p(b))
+    return q, s, b
+
+
+def quantize(x_bits: np.ndarray, dt: int, mode: int, group: int = 64):
+    """mode 0 = reference rows, mode 1 = affine groups of `group`."""
+    return quantize_ref(x_bits, dt) if mode == 0 else quantize_mlx(x_bits, dt, group)
+
+
+def dequant_ref_f16(q, s, z) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.uint8)
+    s = np.ascontiguousarray(s, np.uint16)
+    z = np.ascontiguousarray(z, np.uint16)
+    D = q.shape[-1]
+    out = np.empty(q.shape, np.uint16)
+    lib().oracle_dequant_ref_rows(_p(q), _p(s), _p(z), q.size // D, D, _p(out))
+    return out
+
+
+def dequant_f64(q, s, z, mode: int) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.uint8)
+    s = np.ascontiguousarray(s, np.uint16)
+    z = np.ascontiguousarray(z, np.uint16)
+    D = q.shape[-1]
+    G = s.shape[-1]
+    out = np.empty(q.shape, np.float64)
+    lib().oracle_dequant_f64(_p(q), _p(s), _p(z), q.size // D, D, G, mode, _p(out))
+    return out
+
+
+# --------------------------------------------------------------------------
+# a7 / a8
+# --------------------------------------------------------------------------
+
+def attention_f64(q: np.ndarray, k: np.ndarray, v: np.ndarray, limits, scale: float) -> np.ndarray:
+    """q [NR, D], k/v [T, D] (float64), row r sees keys [0, limits[r])."""
+    q = np.ascontiguousarray(q, np.float64)
+    k = np.ascontiguousarray(k, np.float64)
+    v = np.ascontiguousarray(v, np.float64)
+    NR, D = q.shape
+    T = k.shape[0]
+    lim = np.ascontiguousarray(np.broadcast_to(np.asarray(limits, np.int32), (NR,)), np.int32)
+    out = np.empty((NR, D), np.float64)
+    lib().oracle_attention_f64(_p(q), _p(k), _p(v), NR, T, D, _p(lim), float(scale), _p(out))
+    return out
+
+
+# --------------------------------------------------------------------------
+# a5
+# --------------------------------------------------------------------------
+
+def stack_left_padded(rows_q, rows_s, rows_z, lens, sMax=None):
+    """rows_*[r]: [H, L_r, D] u8 / [H, L_r, G] f16 bits -> stacked right-aligned."""
+    R = len(rows_q)
+    H, _, D = rows_q[0].shape
+    G = rows_s[0].shape[-1]
+    lens = np.ascontiguousarray(lens, np.int32)
+    if sMax is None:
+        sMax = int(lens.max()) if R else 0
+    rq = [np.ascontiguousarray(a, np.uint8) for a in rows_q]
+    rs = [np.ascontiguousarray(a, np.uint16) for a in rows_s]
+    rz = [np.ascontiguousarray(a, np.uint16) for a in rows_z]
+    pq = (ctypes.c_void_p * R)(*[a.ctypes.data for a in rq])
+    ps = (ctypes.c_void_p * R)(*[a.ctypes.data for a in rs])
+    pz = (ctypes.c_void_p * R)(*[a.ctypes.data for a in rz])
+    oq = np.empty((R, H, sMax, D), np.uint8)
+    os_ = np.empty((R, H, sMax, G), np.uint16)
+    oz = np.empty((R, H, sMax, G), np.uint16)
+    lib().oracle_stack_left_padded(pq, ps, pz, _p(lens), R, H, D, G, sMax, _p(oq), _p(os_), _p(oz))
+    return oq, os_, oz
+
+
+# --------------------------------------------------------------------------
+# a10
+# --------------------------------------------------------------------------
+
+def fnv1a64(data: bytes) -> int:
+    buf = np.frombuffer(data, np.uint8).copy() if data else np.zeros(1, np.uint8)
+    return int(lib().oracle_fnv1a64(_p(buf), len(data), 14695981039346656037))
+
+
+def prefix_key(model_id: str, media_hash: str | None, dtype_tag: int, tokens) -> int:
+    t = np.ascontiguousarray(tokens, np.int64)
+    if t.size == 0:
+        t = np.zeros(1, np.int64)
+        n = 0
+    else:
+        n = t.size
+    return int(lib().oracle_prefix_key(model_id.encode(), (media_hash or "").encode(),
+                                       dtype_tag, _p(t), n))
+
+
+def common_prefix_length(a, b) -> int:
+    na, nb = len(a), len(b)
+    a2 = np.ascontiguousarray(a, np.int64) if na else np.zeros(1, np.int64)
+    b2 = np.ascontiguousarray(b, np.int64) if nb else np.zeros(1, np.int64)
+    return int(lib().oracle_common_prefix_length(_p(a2), na, _p(b2), nb))
+
+
+# --------------------------------------------------------------------------
+# CPU baseline session (the reference's per-step algorithm, see the C file)
+# --------------------------------------------------------------------------
+
+class Baseline:
+    def __init__(self, layers, B, Hkv, Hq, D, lens, seed=0):
+        self.layers, self.B, self.Hkv, self.Hq, self.D = layers, B, Hkv, Hq, D
+        self._lens = np.ascontiguousarray(lens, np.int32)
+        self.h = lib().oracle_baseline_create(layers, B, Hkv, Hq, D, _p(self._lens), seed)
+
+    @property
+    def threads(self) -> int:
+        return int(lib().oracle_baseline_threads(self.h))
+
+    def step(self, q_bits, k_bits, v_bits, dt, scale, out, layers_to_run=0):
+        lib().oracle_baseline_step(self.h, _p(q_bits), _p(k_bits), _p(v_bits), dt,
+                                   float(scale), _p(out), layers_to_run)
+
+    def close(self):
+        if self.h:
+            lib().oracle_baseline_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,250 @@
+"""GPU parity: every kernel through the C ABI against the CPU oracle.
+
+Bit-exact for quantize-append / gather / scatter / COW (integer and byte
+work); attention within 2e-3 max-abs of the float64 oracle (fp32 output)."""
+import numpy as np
+import pytest
+
+from kvutil import DT, MODE, Filled, i32, oracle_attention, rand_bits, to_dev
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():  # pragma: no cover - CPU container
+    pytest.skip("no HIP device", allow_module_level=True)
+
+import krill_amd  # noqa: E402
+from oracle import oracle as O  # noqa: E402
+
+ATOL = 2e-3
+
+
+def make_pool(H, D, mode, dt, blocks=64, layers=1, seed=11, **kw):
+    return krill_amd.KVPool(layers, H, D, blocks, mode, dt, free_list_seed=seed, **kw)
+
+
+def gpu(t):
+    return t.cpu().numpy()
+
+
+def check_snapshot(snap, filled, layer, left_pad=False):
+    S = snap["keys"].shape[2]
+    got = {k: gpu(v) for k, v in snap.items()}
+    for b, T in enumerate(filled.lens):
+        kq, ks, kz, vq, vs, vz = filled.expected(layer, b)
+        sl = slice(S - T, S) if left_pad else slice(0, T)
+        pad = slice(0, S - T) if left_pad else slice(T, S)
+        np.testing.assert_array_equal(got["keys"][b, :, sl], kq)
+        np.testing.assert_array_equal(got["values"][b, :, sl], vq)
+        np.testing.assert_array_equal(got["key_scales"][b, :, sl].view(np.uint16), ks)
+        np.testing.assert_array_equal(got["key_zeros"][b, :, sl].view(np.uint16), kz)
+        np.testing.assert_array_equal(got["value_scales"][b, :, sl].view(np.uint16), vs)
+        np.testing.assert_array_equal(got["value_zeros"][b, :, sl].view(np.uint16), vz)
+        for name in got:
+            assert not np.any(got[name][b, :, pad].view(np.uint8)), f"{name} padding not zero"
+
+
+@pytest.mark.parametrize("mode", ["ref_row", "affine_g64"])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_quantize_append_bit_exact(mode, dt, D):
+    print(f"\ncase quantize_append mode={mode} dt={dt} D={D}", flush=True)
+    rng = np.random.default_rng(100 + D)
+    pool = make_pool(3, D, mode, dt, blocks=40)
+    f = Filled(pool, [1, 64, 137, 5], rng, dt, outlier_frac=0.05)
+    tables, lens, _ = f.tables()
+    torch.cuda.synchronize()
+    check_snapshot(pool.gather(0, tables, lens, max(f.lens)), f, 0)
+    pool.close()
+
+
+@pytest.mark.parametrize("mode", ["ref_row", "affine_g64"])
+def test_gather_left_padded_matches_reference_stack(mode):
+    print(f"\ncase gather_left_pad mode={mode}", flush=True)
+    rng = np.random.default_rng(5)
+    H, D = 2, 128
+    pool = make_pool(H, D, mode, "bf16", blocks=24)
+    f = Filled(pool, [70, 3, 128, 65], rng, "bf16")
+    tables, lens, _ = f.tables()
+    sMax = max(f.lens)
+    snap = pool.gather(0, tables, lens, sMax, left_pad=True)
+    torch.cuda.synchronize()
+    check_snapshot(snap, f, 0, left_pad=True)
+    # the reference's own stacker on the oracle rows (BatchedDecode.swift:96-151)
+    exp = [f.expected(0, b) for b in range(len(f.lens))]
+    oq, os_, oz = O.stack_left_padded([e[0] for e in exp], [e[1] for e in exp], [e[2] for e in exp], f.lens, sMax)
+    np.testing.assert_array_equal(gpu(snap["keys"]), oq)
+    np.testing.assert_array_equal(gpu(snap["key_scales"]).view(np.uint16), os_)
+    np.testing.assert_array_equal(gpu(snap["key_zeros"]).view(np.uint16), oz)
+    pool.close()
+
+
+@pytest.mark.parametrize("mode", ["ref_row", "affine_g64"])
+def test_scatter_restores_snapshot_bit_exact(mode):
+    print(f"\ncase scatter mode={mode}", flush=True)
+    rng = np.random.default_rng(8)
+    H, D = 2, 64
+    pool = make_pool(H, D, mode, "f16", blocks=32)
+    f = Filled(pool, [90, 17], rng, "f16")
+    tables, lens, _ = f.tables()
+    S = max(f.lens)
+    snap = pool.gather(0, tables, lens, S, left_pad=True)
+    # restore each row's own slice (scatterBack, ContinuousBatcher.swift:743-801) into fresh sequences
+    new = [pool.seq_create() for _ in f.lens]
+    Lmax = S
+    slots = np.full((len(f.lens), Lmax), -1, np.int32)
+    for b, T in enumerate(f.lens):
+        slots[b, :T] = pool.reserve_append(new[b], T)
+    starts = np.array([S - T for T in f.lens], np.int32)
+    pool.scatter(0, snap, i32(starts), i32(slots))
+    t2, n2 = pool.batch_tables(new, (S + 63) // 64)
+    snap2 = pool.gather(0, i32(t2), i32(n2), S)
+    torch.cuda.synchronize()
+    check_snapshot(snap2, f, 0)
+    pool.close()
+
+
+@pytest.mark.parametrize("mode", ["ref_row", "affine_g64"])
+def test_gather_dequant_matches_oracle(mode):
+    print(f"\ncase gather_dequant mode={mode}", flush=True)
+    rng = np.random.default_rng(9)
+    H, D = 2, 128
+    pool = make_pool(H, D, mode, "bf16", blocks=16)
+    f = Filled(pool, [33, 100], rng, "bf16")
+    tables, lens, _ = f.tables()
+    k, v = pool.gather_dequant(0, tables, lens, 100)
+    k, v = gpu(k).view(np.uint16), gpu(v).view(np.uint16)
+    for b, T in enumerate(f.lens):
+        kq, ks, kz, vq, vs, vz = f.expected(0, b)
+        if mode == "ref_row":
+            ek, ev = O.dequant_ref_f16(kq, ks, kz), O.dequant_ref_f16(vq, vs, vz)
+        else:
+            ek = O.f32_to_f16_bits(O.dequant_f64(kq, ks, kz, 1))
+            ev = O.f32_to_f16_bits(O.dequant_f64(vq, vs, vz, 1))
+        np.testing.assert_array_equal(k[b, :, :T], ek)
+        np.testing.assert_array_equal(v[b, :, :T], ev)
+    pool.close()
+
+
+def _attn_case(mode, D, H, R, lens, Lq=1, dt="bf16", split_blocks=0, path=0, out_dtype=None, seed=0,
+               outlier_frac=0.0, scale=None):
+    rng = np.random.default_rng(seed)
+    nb = sum((T + 63) // 64 for T in lens) + 8
+    pool = make_pool(H, D, mode, dt, blocks=nb)
+    pool.set_option(krill_amd._lib.OPT_SPLIT_BLOCKS, split_blocks)
+    pool.set_option(krill_amd._lib.OPT_ATTN_PATH, path)
+    f = Filled(pool, lens, rng, dt, outlier_frac=outlier_frac)
+    tables, tl, _ = f.tables()
+    q = rand_bits(rng, (len(lens), H * R, Lq, D), dt)
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    out = pool.attention(0, to_dev(q, dt), tables, tl, max(lens), scale, out_dtype)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    ref = oracle_attention(pool, f, 0, q, dt, scale)
+    pool.close()
+    return got, ref
+
+
+@pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
+@pytest.mark.parametrize("D,R", [(128, 5), (64, 4), (128, 8), (256, 2), (128, 1)])
+def test_decode_attention_valu(mode, D, R):
+    print(f"\ncase decode_valu mode={mode} D={D} R={R}", flush=True)
+    got, ref = _attn_case(mode, D, 2, R, [1, 63, 64, 65, 300, 700], seed=D + R)
+    err = np.abs(got - ref).max()
+    assert err <= ATOL, f"max abs error {err:.3e}"
+
+
+@pytest.mark.parametrize("split_blocks", [1, 2, 3])
+def test_decode_attention_split_merge(split_blocks):
+    print(f"\ncase decode_split sb={split_blocks}", flush=True)
+    got, ref = _attn_case("affine_g64", 128, 2, 5, [1, 200, 513, 1000], split_blocks=split_blocks, seed=3)
+    err = np.abs(got - ref).max()
+    assert err <= ATOL, f"max abs error {err:.3e}"
+
+
+@pytest.mark.parametrize("out_dtype", ["bf16", "f16"])
+def test_decode_attention_low_precision_output(out_dtype):
+    print(f"\ncase decode_out {out_dtype}", flush=True)
+    td = torch.bfloat16 if out_dtype == "bf16" else torch.float16
+    got, ref = _attn_case("affine_g64", 128, 2, 5, [77, 300], out_dtype=td, seed=4)
+    # output rounding (half an ulp of the output dtype) on top of the 2e-3 bound
+    ulp = 2.0 ** -8 if out_dtype == "bf16" else 2.0 ** -11
+    err = np.abs(got - ref) - 0.5 * ulp * np.maximum(np.abs(ref), 1e-30) * 2
+    assert err.max() <= ATOL
+
+
+@pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
+@pytest.mark.parametrize("D", [128, 64])
+def test_verify_attention_mfma_causal(mode, D):
+    print(f"\ncase verify_mfma mode={mode} D={D}", flush=True)
+    got, ref = _attn_case(mode, D, 2, 4, [9, 64, 200, 1030], Lq=8, seed=21 + D)
+    err = np.abs(got - ref).max()
+    assert err <= ATOL, f"max abs error {err:.3e}"
+
+
+def test_verify_attention_mfma_splits_and_row_groups():
+    print("\ncase verify_mfma_rowgroups", flush=True)
+    # 16 draft rows x 5 heads = 80 rows -> several row groups; small splits
+    got, ref = _attn_case("affine_g64", 128, 2, 5, [40, 300, 777], Lq=16, split_blocks=2, seed=5)
+    err = np.abs(got - ref).max()
+    assert err <= ATOL, f"max abs error {err:.3e}"
+
+
+def test_verify_attention_valu_small_rows():
+    print("\ncase verify_valu", flush=True)
+    got, ref = _attn_case("affine_g64", 128, 2, 2, [10, 130], Lq=3, seed=6)
+    err = np.abs(got - ref).max()
+    assert err <= ATOL, f"max abs error {err:.3e}"
+
+
+def test_decode_via_mfma_path_matches_valu():
+    print("\ncase decode_mfma_forced", flush=True)
+    got, ref = _attn_case("affine_g64", 128, 2, 5, [65, 400], path=2, seed=12)
+    err = np.abs(got - ref).max()
+    assert err <= ATOL, f"max abs error {err:.3e}"
+
+
+def test_copy_on_write_preserves_the_sharer():
+    print("\ncase cow", flush=True)
+    rng = np.random.default_rng(13)
+    H, D, dt = 2, 128, "bf16"
+    pool = make_pool(H, D, "affine_g64", dt, blocks=16, layers=2)
+    f = Filled(pool, [100], rng, dt, layers=(0, 1))
+    a = f.seqs[0]
+    fork = pool.seq_fork(a, 70)  # shares blocks 0 (full) and 1 (tokens 64..69 of 36 filled)
+    extra_k = rand_bits(rng, (1, H, 5, D), dt)
+    extra_v = rand_bits(rng, (1, H, 5, D), dt)
+    slots = pool.reserve_append(fork, 5)  # tail block shared -> copy-on-write
+    assert pool.stats()["cow_copies"] == 1
+    for layer in (0, 1):
+        pool.quantize_append(layer, to_dev(extra_k, dt), to_dev(extra_v, dt), i32(slots.reshape(1, 5)))
+    for layer in (0, 1):
+        # the sharer is unchanged
+        t, n = pool.batch_tables([a], 2)
+        check_snapshot(pool.gather(layer, i32(t), i32(n), 100), f, layer)
+        # the fork = first 70 tokens of a + the 5 new ones
+        t2, n2 = pool.batch_tables([fork], 2)
+        snap = pool.gather(layer, i32(t2), i32(n2), 75)
+        kq, ks, kz, vq, vs, vz = f.expected(layer, 0)
+        mode = MODE["affine_g64"]
+        nk = O.quantize(extra_k[0], DT[dt], mode)
+        np.testing.assert_array_equal(gpu(snap["keys"])[0, :, :70], kq[:, :70])
+        np.testing.assert_array_equal(gpu(snap["keys"])[0, :, 70:], nk[0])
+        np.testing.assert_array_equal(gpu(snap["key_scales"])[0, :, 70:].view(np.uint16), nk[1])
+    pool.close()
+
+
+def test_qwen3_14b_shape_decode_step():
+    """Config 2 shapes (Hq 40, Hkv 8, D 128, affine g64) on 4 ragged sequences."""
+    print("\ncase qwen3_14b_shape", flush=True)
+    got, ref = _attn_case("affine_g64", 128, 8, 5, [512, 1999, 4096, 8193], seed=20261203)
+    err = np.abs(got - ref).max()
+    assert err <= ATOL, f"max abs error {err:.3e}"
+
+
+def test_outlier_channels_long_context_shape():
+    """Config 5 flavour: Hkv 4, R 8, 1% channels x20, long context."""
+    print("\ncase outliers_long", flush=True)
+    got, ref = _attn_case("affine_g64", 128, 4, 8, [9000, 20000], seed=20261205, outlier_frac=0.01)
+    err = np.abs(got - ref).max()
+    assert err <= ATOL, f"max abs error {err:.3e}"
