@@ -1,10 +1,34 @@
-// Arguments shared by the paged attention kernels (VALU and MFMA paths).
+// Arguments and workspace layout shared by the paged attention kernels
+// (VALU and MFMA paths).
 #pragma once
 
 #include "kdev.hpp"
 #include "launch.hpp"
 
 namespace krill {
+
+// Workspace carve-up, 256-byte aligned pieces:
+//   o      float [B][Hkv][max_splits][NR][D]   unnormalised split outputs
+//   ml     float [B][Hkv][max_splits][NR][2]   (running max m in log2 units, sum l)
+//   q16    fp16  [B][Hkv][NR][D]               queries rounded to fp16 (VALU path)
+//   qsum   float [B][Hkv][NR][G]               per scale group sums of q16
+//   count  u32   [B][Hkv]                      splits finished (last one merges)
+struct WsLayout {
+  size_t o, ml, q16, qsum, count, total;
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+inline WsLayout ws_layout(int64_t B, int64_t Hkv, int64_t max_splits, int64_t NR, int64_t D, int64_t G) {
+  WsLayout w;
+  w.o = 0;
+  w.ml = align256(w.o + (size_t)(B * Hkv * max_splits * NR * D) * sizeof(float));
+  w.q16 = align256(w.ml + (size_t)(B * Hkv * max_splits * NR * 2) * sizeof(float));
+  w.qsum = align256(w.q16 + (size_t)(B * Hkv * NR * D) * sizeof(uint16_t));
+  w.count = align256(w.qsum + (size_t)(B * Hkv * NR * G) * sizeof(float));
+  w.total = align256(w.count + (size_t)(B * Hkv) * sizeof(uint32_t));
+  return w;
+}
 
 struct AttnArgs {
   LayerView lv;
@@ -16,9 +40,12 @@ struct AttnArgs {
   int32_t Hkv, R, Lq, Hq, NR;
   float scale_log2;  // softmax scale * log2(e)
   int32_t split_blocks, max_splits;
-  float *ws_o;   // [B][Hkv][max_splits][NR][D]
-  float *ws_ml;  // [B][Hkv][max_splits][NR][2] = (m, l), m in the log2 domain
-  void *out;     // [B][Hq][Lq][D]
+  float *ws_o;
+  float *ws_ml;
+  uint16_t *q16;
+  float *qsum;
+  uint32_t *count;
+  void *out;  // [B][Hq][Lq][D]
   int32_t out_dtype;
 };
 
@@ -41,9 +68,13 @@ inline AttnArgs make_attn_args(const PoolGeometry &g, int32_t layer, const AttnL
   r.scale_log2 = a.scale * 1.4426950408889634f;
   r.split_blocks = p.split_blocks;
   r.max_splits = p.max_splits;
-  const size_t o_bytes = (size_t)a.B * g.Hkv * p.max_splits * p.NR * g.D * sizeof(float);
-  r.ws_o = static_cast<float *>(a.ws);
-  r.ws_ml = reinterpret_cast<float *>(static_cast<uint8_t *>(a.ws) + ((o_bytes + 255) & ~(size_t)255));
+  const WsLayout w = ws_layout(a.B, g.Hkv, p.max_splits, p.NR, g.D, g.G);
+  uint8_t *base = static_cast<uint8_t *>(a.ws);
+  r.ws_o = reinterpret_cast<float *>(base + w.o);
+  r.ws_ml = reinterpret_cast<float *>(base + w.ml);
+  r.q16 = reinterpret_cast<uint16_t *>(base + w.q16);
+  r.qsum = reinterpret_cast<float *>(base + w.qsum);
+  r.count = reinterpret_cast<uint32_t *>(base + w.count);
   r.out = a.out;
   r.out_dtype = a.out_dtype;
   return r;
@@ -63,8 +94,8 @@ __device__ __forceinline__ float load_q(const uint16_t *p, int dt) {
   return dt == DT_BF16 ? bf16_bits_to_f32(*p) : f16_bits_to_f32(*p);
 }
 
-// Output / partial-result writers.  Rows are r = j*R + h (query position j,
-// head h inside the KV group).
+// Output / partial-result addressing.  Rows are r = j*R + h (query position
+// j, head h inside the KV group).
 __device__ __forceinline__ int64_t out_row_base(const AttnArgs &a, int b, int hk, int r, int D) {
   const int hq = hk * a.R + r % a.R, j = r / a.R;
   return (((int64_t)b * a.Hq + hq) * a.Lq + j) * D;

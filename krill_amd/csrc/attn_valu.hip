@@ -8,41 +8,97 @@
 // Sources/KrillEngine/BatchedDecode.swift:277-287 replaced by per-row lengths
 // (the -10000 mask underflows those weights to exactly zero, :22-28).
 //
-// One wave64 per (split of 64-token blocks, kv head, sequence).  Per block:
-//  * scores: NC = D/32 lanes share a token, each lane owns 32 d of K
-//    (two 16-byte loads, contiguous across lanes), bytes become fp16
-//    (1024 + q) with one v_perm_b32 per pair, v_dot2_f32_f16 against the
-//    fp16 query held in registers, then a shuffle-sum across the NC lanes.
-//    Affine mode uses linearity: q.k = s*(q.(1024+u) - 1024*sum q) + z*sum q
-//    per 64-group, so no per-element dequantisation is needed.  Reference
-//    row mode dequantises exactly (f16(f16(u*s)+z), two packed-fp16
-//    roundings, QuantizedKVCache.swift:200-204) before the dot.
-//  * online softmax in the log2 domain (wave shuffles), weights w = p*s_v
-//    written to LDS in V storage order as fp16;
-//  * P.V: each lane owns D/32 columns x 16 token positions per 32-token
-//    group; V bytes (stored token-contiguous per d) are read with 16-byte
-//    loads and reduced with v_dot2_f32_f16 over token pairs; the V zero
-//    points and the 1024 offset collapse into one per-(row, group) term.
-// Partial (m, l, o) go to the workspace for the split-K merge, or straight
-// to the output when the sequence has a single split.
+// Two launches: a prep kernel rounds the queries to fp16 once per
+// (sequence, KV head) and sums them per scale group; the main kernel runs one
+// wave64 per (split of 64-token blocks, KV head, sequence).  Per block:
+//  * scores, one token per lane: the lane reads its token's K row (D bytes,
+//    16-byte loads that are contiguous across lanes in the d-chunk-major
+//    layout), turns byte pairs into fp16 (1024 + u) with one v_perm_b32, and
+//    accumulates v_dot2c_f32_f16 against fp16 query pairs that are
+//    wave-uniform and therefore come from scalar registers (scalar loads of
+//    the prep output).  Affine mode uses linearity per 64-group:
+//      q.k = s * (q.(1024 + u) - 1024 * sum q) + z * sum q,
+//    so no element is dequantised.  Reference row mode dequantises exactly
+//    (f16(f16(u*s) + z), QuantizedKVCache.swift:200-204) before the dot.
+//  * online softmax in the log2 domain with a lazily raised running max: a
+//    block only pays for a wave reduction when some score exceeds the
+//    running max by more than 8 (a wave vote), so weights stay below 2^8;
+//  * weights w = p * s_v (fp16) go to LDS in V storage order; each lane
+//    then owns D/64 V^T rows (d values), loaded as contiguous 16-byte pieces,
+//    and reduces token pairs with v_dot2c_f32_f16.  The V zero points and the
+//    1024 offset collapse into one per-(row, group) term.
+//  * the next block's K and V are loaded as soon as the current block's
+//    registers are consumed, so loads overlap the other phase's math.
+// A sequence with one split writes the output directly; otherwise every
+// split writes (m, l, o) to the workspace and the last split to finish
+// (device-scope counter) merges them.
 #include <hip/hip_runtime.h>
 
 #include "attn_common.hpp"
 
 namespace krill {
 
+typedef __attribute__((address_space(4))) const float scalar_f32;
+
+// acc += sum_i k[i] . q_(OFF + i), i < 8, where q_n is lane n of this lane's
+// 16-lane row of `q` (v_dot2c_f32_f16 with a DPP row_newbcast source).  The
+// leading s_nop covers the VALU-write -> DPP-read hazard on `q`.
+template <int OFF>
+__device__ __forceinline__ void dot8_bcast(float &acc, uint32_t q, const half2_t (&k)[8]) {
+  asm("s_nop 1\n\t"
+      "v_dot2c_f32_f16_dpp %0, %1, %2 row_newbcast:%10 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %0, %1, %3 row_newbcast:%11 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %0, %1, %4 row_newbcast:%12 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %0, %1, %5 row_newbcast:%13 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %0, %1, %6 row_newbcast:%14 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %0, %1, %7 row_newbcast:%15 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %0, %1, %8 row_newbcast:%16 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %0, %1, %9 row_newbcast:%17 row_mask:0xf bank_mask:0xf"
+      : "+v"(acc)
+      : "v"(q), "v"(k[0]), "v"(k[1]), "v"(k[2]), "v"(k[3]), "v"(k[4]), "v"(k[5]), "v"(k[6]), "v"(k[7]),
+        "n"(OFF), "n"(OFF + 1), "n"(OFF + 2), "n"(OFF + 3), "n"(OFF + 4), "n"(OFF + 5), "n"(OFF + 6), "n"(OFF + 7));
+}
+
+// fp16 queries and their per-group sums; resets the split counters.
+template <int D, int NR, int G>
+__global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
+  const int hk = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const int64_t row0 = ((int64_t)b * a.Hkv + hk) * NR;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int hq = hk * a.R + r % a.R, j = r / a.R;
+    const uint16_t *qp = a.q + (((int64_t)b * a.Hq + hq) * a.Lq + j) * D;
+    float gs[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) gs[g] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < D / 64; ++k) {
+      const int d = lane + 64 * k;
+      const _Float16 h = (_Float16)load_q(qp + d, a.q_dtype);
+      a.q16[(row0 + r) * D + d] = __builtin_bit_cast(uint16_t, h);
+      gs[(64 * k) / (D / G)] += (float)h;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float t = wave_allsum(gs[g]);
+      if (lane == 0) a.qsum[(row0 + r) * G + g] = t;
+    }
+  }
+  if (lane == 0) a.count[(int64_t)b * a.Hkv + hk] = 0u;
+}
+
 template <int D, int NR, int MODE>
 __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
-  constexpr int NC = D / 32;   // lanes per token in the score loop
-  constexpr int TPI = 64 / NC; // tokens per score iteration
   constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
-  constexpr int ND = D / 32;   // d columns per lane in the P.V loop
-  constexpr int KPG = ND / G;  // of which per scale group
-  constexpr int LPG = NC / G;  // score lanes per scale group
+  constexpr int NP = D / 16;   // 16-byte K pieces per token row
+  constexpr int PPG = NP / G;  // pieces per scale group
+  constexpr int DPL = D / 64;  // V^T rows (d values) per lane
+  constexpr int MAXS = 256;    // splits merged per LDS pass
 
   __shared__ __attribute__((aligned(16))) uint16_t w_lds[NR * G * 64];
-  __shared__ __attribute__((aligned(16))) uint16_t s_lds[64];
-  __shared__ __attribute__((aligned(16))) uint16_t z_lds[64];
+  __shared__ __attribute__((aligned(16))) uint16_t sz_lds[2 * 64];
+  __shared__ float e_lds[MAXS];
+  __shared__ int last_lds;
 
   const int lane = threadIdx.x;
   const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
@@ -61,231 +117,347 @@ __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
   const int blk1 = min(nb, blk0 + a.split_blocks);
   const int n_splits = (nb + a.split_blocks - 1) / a.split_blocks;
 
-  const int dq = lane % NC, tl = lane / NC;
-  const int my_g = MODE == MODE_AFFINE ? dq / LPG : 0;
-  const bool writer = (dq % LPG) == 0;
-
-  // Query slice of this lane: d in [32*dq, 32*dq + 32) as 16 fp16 pairs.
-  half2_t qh[NR][16];
-  float qc[NR];
+  const int64_t qrow = ((int64_t)b * a.Hkv + hk) * NR;
+  // fp16 query pairs: qv[r][c] holds pair 16*c + (lane & 15) of row r, so
+  // every 16-lane row carries the whole query (one VGPR per 32 d)
+  uint32_t qv[NR][D / 32];
+  {
+    const uint32_t *q16 = reinterpret_cast<const uint32_t *>(a.q16 + qrow * D);
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) qv[r][c] = q16[r * (D / 2) + 16 * c + (lane & 15)];
+  }
+  scalar_f32 *qs = (scalar_f32 *)(a.qsum + qrow * G);
   int lim[NR];
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    const int hq = hk * a.R + r % a.R, j = r / a.R;
-    lim[r] = len - a.Lq + j + 1;
-    const uint16_t *qp = a.q + (((int64_t)b * a.Hq + hq) * a.Lq + j) * D + 32 * dq;
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const _Float16 h0 = (_Float16)load_q(qp + 2 * i, a.q_dtype);
-      const _Float16 h1 = (_Float16)load_q(qp + 2 * i + 1, a.q_dtype);
-      qh[r][i] = half2_t{h0, h1};
-      s += (float)h0 + (float)h1;
-    }
-    qc[r] = s;
-  }
+  for (int r = 0; r < NR; ++r) lim[r] = len - a.Lq + r / a.R + 1;
+  const int gl = MODE == MODE_AFFINE ? (DPL * lane) / 64 : 0;  // scale group of this lane's V rows
+  const int pos = ((lane >> 5) << 5) + vpos(lane & 31);        // this lane's token in V order
 
-  float m_run[NR], l_part[NR], c_part[NR], acc[NR][ND];
+  float m_run[NR], l_part[NR], c_part[NR][G], acc[NR][DPL];
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
     m_run[r] = -INFINITY;
     l_part[r] = 0.0f;
-    c_part[r] = 0.0f;
 #pragma unroll
-    for (int k = 0; k < ND; ++k) acc[r][k] = 0.0f;
+    for (int g = 0; g < G; ++g) c_part[r][g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[r][e] = 0.0f;
   }
   const half2_t m1024 = half2_t{(_Float16)-1024.0f, (_Float16)-1024.0f};
 
-  for (int blk = blk0; blk < blk1; ++blk) {
+  auto region_of = [&](int blk) -> const uint8_t * {
     int phys = a.tables[(int64_t)b * a.max_blocks + blk];
     phys = (unsigned)phys < (unsigned)a.lv.num_blocks ? phys : 0;
-    const uint8_t *reg = head_region(a.lv, phys, hk);
-    const int tbase = blk << 6;
+    return head_region(a.lv, phys, hk);
+  };
+  uint4 kr[NP];
+  uint4 vr[2][2 * DPL];
+  auto load_k = [&](const uint8_t *reg) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) kr[p] = *reinterpret_cast<const uint4 *>(reg + k_byte(lane, 16 * p));
+  };
+  auto load_v = [&](const uint8_t *reg) {
+#pragma unroll
+    for (int tg = 0; tg < 2; ++tg)
+#pragma unroll
+      for (int i = 0; i < 2 * DPL; ++i)
+        vr[tg][i] = *reinterpret_cast<const uint4 *>(reg + v_offset(D) + ((tg * D + DPL * lane) << 5) + 16 * i);
+  };
 
-    // ---- scores (log2 domain)
-    float sc[NC][NR];
+  const uint8_t *reg = region_of(blk0);
+  load_k(reg);
+  load_v(reg);
+
+  for (int blk = blk0; blk < blk1; ++blk) {
+    const int tbase = blk << 6;
+    const bool has_next = blk + 1 < blk1;
+    const uint8_t *nreg = has_next ? region_of(blk + 1) : reg;
+    uint32_t km[G], vm[G];
 #pragma unroll
-    for (int it = 0; it < NC; ++it) {
-      const int tok = it * TPI + tl;
-      const uint4 *kp = reinterpret_cast<const uint4 *>(reg + ((dq * 64 + tok) << 5));
-      const uint4 k0 = kp[0], k1 = kp[1];
-      const uint32_t km = *reinterpret_cast<const uint32_t *>(reg + km_offset(D) + ((tok * G + my_g) << 2));
-      const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-      half2_t kv[16];
+    for (int g = 0; g < G; ++g) {
+      km[g] = *reinterpret_cast<const uint32_t *>(reg + km_offset(D) + ((lane * G + g) << 2));
+      vm[g] = *reinterpret_cast<const uint32_t *>(reg + vm_offset(D, G) + ((lane * G + g) << 2));
+    }
+
+    // ---- scores: this lane's token against every query row; the query
+    // pair of each dot comes from lane (pair & 15) of the lane's 16-lane row
+    // through the DPP broadcast of v_dot2c.
+    float accg[NR][G];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        kv[2 * i] = bytes01_plus1024(kw[i]);
-        kv[2 * i + 1] = bytes23_plus1024(kw[i]);
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+      for (int g = 0; g < G; ++g) accg[r][g] = 0.0f;
+    half2_t ks2 = m1024, kz2 = m1024;
+    if constexpr (MODE == MODE_REF) {
+      const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)(km[0] & 0xffffu));
+      const _Float16 z = __builtin_bit_cast(_Float16, (uint16_t)(km[0] >> 16));
+      ks2 = half2_t{s, s};
+      kz2 = half2_t{z, z};
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      if (p > 0) order_after(kr[p], accg[NR - 1][MODE == MODE_AFFINE ? (p - 1) / PPG : 0]);
+      const uint32_t w4[4] = {kr[p].x, kr[p].y, kr[p].z, kr[p].w};
+      half2_t kp[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kp[2 * i] = bytes01_plus1024(w4[i]);
+        kp[2 * i + 1] = bytes23_plus1024(w4[i]);
       }
-      const _Float16 ksh = __builtin_bit_cast(_Float16, (uint16_t)(km & 0xffffu));
-      const _Float16 kzh = __builtin_bit_cast(_Float16, (uint16_t)(km >> 16));
       if constexpr (MODE == MODE_REF) {
-        const half2_t s2 = half2_t{ksh, ksh}, z2 = half2_t{kzh, kzh};
 #pragma unroll
-        for (int i = 0; i < 16; ++i) kv[i] = (kv[i] + m1024) * s2 + z2;
+        for (int i = 0; i < 8; ++i) kp[i] = (kp[i] + m1024) * ks2 + kz2;
       }
-      const float ksf = (float)ksh, zz = (float)kzh - 1024.0f * (float)ksh;
+      const int g = MODE == MODE_AFFINE ? p / PPG : 0;
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
-        float d = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) d = dot2(qh[r][i], kv[i], d);
-        float part = MODE == MODE_AFFINE ? fmaf(ksf, d, zz * qc[r]) : d;
-#pragma unroll
-        for (int m = 1; m < NC; m <<= 1) part += shfl_xor(part, m);
-        sc[it][r] = (tbase + tok < lim[r]) ? part * a.scale_log2 : -INFINITY;
+        if (p & 1)
+          dot8_bcast<8>(accg[r][g], qv[r][p >> 1], kp);
+        else
+          dot8_bcast<0>(accg[r][g], qv[r][p >> 1], kp);
       }
     }
+    // K registers are free: fetch the next block.  Unconditional on purpose
+    // (the last block re-reads itself from L2): a conditional load would keep
+    // the consumed registers alive through the loop header.
+    load_k(nreg);
 
-    // ---- online softmax
+    float s[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      float mb = sc[0][r];
+      float v;
+      if constexpr (MODE == MODE_AFFINE) {
+        v = 0.0f;
 #pragma unroll
-      for (int it = 1; it < NC; ++it) mb = fmaxf(mb, sc[it][r]);
-#pragma unroll
-      for (int m = NC; m < 64; m <<= 1) mb = fmaxf(mb, shfl_xor(mb, m));
-      const float mn = fmaxf(m_run[r], mb);
-      const float mu = mn == -INFINITY ? 0.0f : mn;
-      const float al = fast_exp2(m_run[r] - mu);
-      m_run[r] = mn;
-      float ps = 0.0f;
-#pragma unroll
-      for (int it = 0; it < NC; ++it) {
-        sc[it][r] = fast_exp2(sc[it][r] - mu);
-        ps += sc[it][r];
+        for (int g = 0; g < G; ++g) {
+          const float kss = f16_bits_to_f32((uint16_t)(km[g] & 0xffffu));
+          const float kzz = f16_bits_to_f32((uint16_t)(km[g] >> 16));
+          v += kss * accg[r][g] + (kzz - 1024.0f * kss) * qs[r * G + g];
+        }
+      } else {
+        v = accg[r][0];
       }
-      l_part[r] = l_part[r] * al + (dq == 0 ? ps : 0.0f);
-      c_part[r] *= al;
-#pragma unroll
-      for (int k = 0; k < ND; ++k) acc[r][k] *= al;
+      s[r] = (tbase + lane < lim[r]) ? v * a.scale_log2 : -INFINITY;
     }
 
-    // ---- weights to LDS, in V storage order
-    if (writer) {
+    // ---- online softmax with a lazily raised running max
+    bool raise = blk == blk0;
+    if (!raise) {
+      bool over = false;
 #pragma unroll
-      for (int it = 0; it < NC; ++it) {
-        const int tok = it * TPI + tl;
-        const int pos = ((tok >> 5) << 5) + vpos(tok & 31);
-        const bool valid = tbase + tok < len;
-        const uint32_t vm =
-            valid ? *reinterpret_cast<const uint32_t *>(reg + vm_offset(D, G) + ((tok * G + my_g) << 2)) : 0u;
-        if constexpr (MODE == MODE_AFFINE) {
-          const float vsf = f16_bits_to_f32((uint16_t)(vm & 0xffffu));
-          const float vzf = f16_bits_to_f32((uint16_t)(vm >> 16));
+      for (int r = 0; r < NR; ++r) over |= s[r] > m_run[r] + 8.0f;
+      raise = __any(over);
+    }
+    if (raise) {
 #pragma unroll
-          for (int r = 0; r < NR; ++r) {
-            const float p = sc[it][r];
-            const _Float16 wv = (_Float16)(p * vsf);
-            w_lds[(r * G + my_g) * 64 + pos] = __builtin_bit_cast(uint16_t, wv);
-            c_part[r] += p * vzf - 1024.0f * (float)wv;
-          }
-        } else {
+      for (int r = 0; r < NR; ++r) {
+        const float mb = wave_allmax(s[r]);
+        const float mn = fmaxf(m_run[r], mb);
+        const float al = m_run[r] == -INFINITY ? 0.0f : fast_exp2(m_run[r] - mn);
+        m_run[r] = mn;
+        l_part[r] *= al;
 #pragma unroll
-          for (int r = 0; r < NR; ++r) w_lds[r * 64 + pos] = __builtin_bit_cast(uint16_t, (_Float16)sc[it][r]);
-          s_lds[pos] = (uint16_t)(vm & 0xffffu);
-          z_lds[pos] = (uint16_t)(vm >> 16);
+        for (int g = 0; g < G; ++g) c_part[r][g] *= al;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[r][e] *= al;
+      }
+    }
+    float pr[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      pr[r] = fast_exp2(s[r] - (m_run[r] == -INFINITY ? 0.0f : m_run[r]));
+      l_part[r] += pr[r];
+    }
+
+    // ---- weights to LDS in V storage order
+    const bool valid = tbase + lane < len;
+    if constexpr (MODE == MODE_AFFINE) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float vsf = valid ? f16_bits_to_f32((uint16_t)(vm[g] & 0xffffu)) : 0.0f;
+        const float vzf = valid ? f16_bits_to_f32((uint16_t)(vm[g] >> 16)) : 0.0f;
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          const _Float16 wv = (_Float16)(pr[r] * vsf);
+          w_lds[(r * G + g) * 64 + pos] = __builtin_bit_cast(uint16_t, wv);
+          c_part[r][g] += pr[r] * vzf - 1024.0f * (float)wv;
         }
       }
+    } else {
+#pragma unroll
+      for (int r = 0; r < NR; ++r) w_lds[r * 64 + pos] = __builtin_bit_cast(uint16_t, (_Float16)pr[r]);
+      sz_lds[pos] = valid ? (uint16_t)(vm[0] & 0xffffu) : (uint16_t)0;
+      sz_lds[64 + pos] = valid ? (uint16_t)(vm[0] >> 16) : (uint16_t)0;
     }
     __syncthreads();
 
-    // ---- P.V
-    const int hh = lane & 1, dl = lane >> 1;
+    // ---- P.V: lane owns V^T rows d = DPL*lane .. +DPL, 32 tokens per group
     const uint32_t *w32 = reinterpret_cast<const uint32_t *>(w_lds);
 #pragma unroll
     for (int tg = 0; tg < 2; ++tg) {
-      const int p0 = tg * 32 + hh * 16;
+      if (tg > 0) {
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        half2_t wv[NR][8];
+        for (int i = 0; i < 2 * DPL; ++i) order_after(vr[1][i], acc[NR - 1][DPL - 1]);
+      }
+      half2_t vp[DPL][16];
 #pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          const uint4 *wp = reinterpret_cast<const uint4 *>(w32 + (r * G + g) * 32 + (p0 >> 1));
-          const uint4 a0 = wp[0], a1 = wp[1];
-          const uint32_t ww[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      for (int e = 0; e < DPL; ++e)
 #pragma unroll
-          for (int i = 0; i < 8; ++i) wv[r][i] = u32_as_h2(ww[i]);
+        for (int h = 0; h < 2; ++h) {
+          const uint4 w = vr[tg][2 * e + h];
+          vp[e][8 * h + 0] = bytes01_plus1024(w.x);
+          vp[e][8 * h + 1] = bytes23_plus1024(w.x);
+          vp[e][8 * h + 2] = bytes01_plus1024(w.y);
+          vp[e][8 * h + 3] = bytes23_plus1024(w.y);
+          vp[e][8 * h + 4] = bytes01_plus1024(w.z);
+          vp[e][8 * h + 5] = bytes23_plus1024(w.z);
+          vp[e][8 * h + 6] = bytes01_plus1024(w.w);
+          vp[e][8 * h + 7] = bytes23_plus1024(w.w);
         }
-        half2_t sp[8], zp[8];
-        if constexpr (MODE == MODE_REF) {
-          const uint4 *spp = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint32_t *>(s_lds) + (p0 >> 1));
-          const uint4 *zpp = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint32_t *>(z_lds) + (p0 >> 1));
-          const uint4 s0 = spp[0], s1 = spp[1], z0 = zpp[0], z1 = zpp[1];
-          const uint32_t ss[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-          const uint32_t zzz[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+      if constexpr (MODE == MODE_REF) {
+        const uint32_t *s32 = reinterpret_cast<const uint32_t *>(sz_lds);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            sp[i] = u32_as_h2(ss[i]);
-            zp[i] = u32_as_h2(zzz[i]);
-          }
-        }
+        for (int i = 0; i < 16; ++i) {
+          const half2_t sp = u32_as_h2(s32[tg * 16 + i]);
+          const half2_t zp = u32_as_h2(s32[32 + tg * 16 + i]);
 #pragma unroll
-        for (int kk = 0; kk < KPG; ++kk) {
-          const int k = g * KPG + kk;
-          const int d = 32 * k + dl;
-          const uint4 vw = *reinterpret_cast<const uint4 *>(reg + v_offset(D) + ((tg * D + d) << 5) + hh * 16);
-          half2_t vp[8] = {bytes01_plus1024(vw.x), bytes23_plus1024(vw.x), bytes01_plus1024(vw.y),
-                           bytes23_plus1024(vw.y), bytes01_plus1024(vw.z), bytes23_plus1024(vw.z),
-                           bytes01_plus1024(vw.w), bytes23_plus1024(vw.w)};
-          if constexpr (MODE == MODE_REF) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) vp[i] = (vp[i] + m1024) * sp[i] + zp[i];
-          }
-#pragma unroll
-          for (int r = 0; r < NR; ++r) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) acc[r][k] = dot2(wv[r][i], vp[i], acc[r][k]);
-          }
+          for (int e = 0; e < DPL; ++e) vp[e][i] = (vp[e][i] + m1024) * sp + zp;
         }
       }
+      // weights of row r + 1 are read while row r is reduced
+      uint4 wn[4];
+      {
+        const uint4 *wp = reinterpret_cast<const uint4 *>(w32 + gl * 32 + tg * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wn[i] = wp[i];
+      }
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const uint4 a0 = wn[0], a1 = wn[1], a2 = wn[2], a3 = wn[3];
+        asm volatile("" ::: "memory");
+        if (r + 1 < NR) {
+          const uint4 *wp = reinterpret_cast<const uint4 *>(w32 + ((r + 1) * G + gl) * 32 + tg * 16);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) wn[i] = wp[i];
+        }
+        const uint32_t ww[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
+                                 a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+#pragma unroll
+        for (int e = 0; e < DPL; ++e)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[r][e] = dot2(u32_as_h2(ww[i]), vp[e][i], acc[r][e]);
+      }
     }
+    load_v(nreg);  // V registers are free: fetch the next block
+    reg = nreg;
     __syncthreads();
   }
 
   // ---- epilogue
-  const int hh = lane & 1, dl = lane >> 1;
+  float o[NR][DPL], lsum[NR];
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
+    lsum[r] = wave_allsum(l_part[r]);
+    float cg = 0.0f;
+    if constexpr (MODE == MODE_AFFINE) {
 #pragma unroll
-    for (int k = 0; k < ND; ++k) acc[r][k] += shfl_xor(acc[r][k], 1);
-    const float l = wave_sum_range<1, 32>(l_part[r]);
-    float cg[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-      cg[g] = MODE == MODE_AFFINE ? wave_sum_range<1, 32>(my_g == g ? c_part[r] : 0.0f) : 0.0f;
-    if (n_splits == 1) {
-      if (hh == 0) {
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        const int64_t ob = out_row_base(a, b, hk, r, D);
-#pragma unroll
-        for (int k = 0; k < ND; ++k) store_out(a.out, ob + 32 * k + dl, (acc[r][k] + cg[k / KPG]) * inv, a.out_dtype);
-      }
-    } else {
-      const int64_t pi = part_index(a, b, hk, split, r);
-      if (hh == 0) {
-#pragma unroll
-        for (int k = 0; k < ND; ++k) a.ws_o[pi * D + 32 * k + dl] = acc[r][k] + cg[k / KPG];
-      }
-      if (lane == 0) {
-        a.ws_ml[pi * 2] = m_run[r];
-        a.ws_ml[pi * 2 + 1] = l;
+      for (int g = 0; g < G; ++g) {
+        const float c = wave_allsum(c_part[r][g]);
+        cg = g == gl ? c : cg;
       }
     }
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) o[r][e] = acc[r][e] + cg;
   }
+  if (n_splits == 1) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const float inv = lsum[r] > 0.0f ? 1.0f / lsum[r] : 0.0f;
+      const int64_t ob = out_row_base(a, b, hk, r, D);
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) store_out(a.out, ob + DPL * lane + e, o[r][e] * inv, a.out_dtype);
+    }
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int64_t pi = part_index(a, b, hk, split, r);
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) a.ws_o[pi * D + DPL * lane + e] = o[r][e];
+    if (lane == 0) {
+      a.ws_ml[pi * 2] = m_run[r];
+      a.ws_ml[pi * 2 + 1] = lsum[r];
+    }
+  }
+  // publish the partials; the last split of this (sequence, KV head) merges
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (lane == 0) {
+    const uint32_t done = __hip_atomic_fetch_add(a.count + (int64_t)b * a.Hkv + hk, 1u, __ATOMIC_ACQ_REL,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    last_lds = done == (uint32_t)(n_splits - 1);
+  }
+  __syncthreads();
+  if (!last_lds) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  const int64_t pbase = part_index(a, b, hk, 0, 0);
+#pragma unroll 1
+  for (int r = 0; r < NR; ++r) {
+    float M = -INFINITY;
+    for (int sp = lane; sp < n_splits; sp += 64) M = fmaxf(M, a.ws_ml[(pbase + (int64_t)sp * NR + r) * 2]);
+    M = wave_allmax(M);
+    float Lsum = 0.0f, oacc[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) oacc[e] = 0.0f;
+    for (int s0 = 0; s0 < n_splits; s0 += MAXS) {
+      const int cnt = min(MAXS, n_splits - s0);
+      float lpart = 0.0f;
+      for (int i = lane; i < cnt; i += 64) {
+        const int64_t pi = pbase + (int64_t)(s0 + i) * NR + r;
+        const float m = a.ws_ml[pi * 2];
+        const float w = m == -INFINITY ? 0.0f : fast_exp2(m - M);
+        e_lds[i] = w;
+        lpart += w * a.ws_ml[pi * 2 + 1];
+      }
+      Lsum += wave_allsum(lpart);
+      __syncthreads();
+#pragma unroll 4
+      for (int i = 0; i < cnt; ++i) {
+        const float w = e_lds[i];
+        const int64_t pi = pbase + (int64_t)(s0 + i) * NR + r;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) oacc[e] += w * a.ws_o[pi * D + DPL * lane + e];
+      }
+      __syncthreads();
+    }
+    const float inv = (M == -INFINITY || !(Lsum > 0.0f)) ? 0.0f : 1.0f / Lsum;
+    const int64_t ob = out_row_base(a, b, hk, r, D);
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) store_out(a.out, ob + DPL * lane + e, oacc[e] * inv, a.out_dtype);
+  }
+  if (lane == 0) a.count[(int64_t)b * a.Hkv + hk] = 0u;
+}
+
+template <int D, int MODE, int NR>
+static void launch_one(const AttnArgs &args, int B, dim3 grid, hipStream_t st) {
+  constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
+  k_attn_prep<D, NR, G><<<dim3((unsigned)args.Hkv, (unsigned)B), dim3(64), 0, st>>>(args);
+  k_attn_valu<D, NR, MODE><<<grid, dim3(64), 0, st>>>(args);
 }
 
 template <int D, int MODE>
-static hipError_t launch_valu_nr(const AttnArgs &args, int NR, dim3 grid, hipStream_t st) {
+static hipError_t launch_valu_nr(const AttnArgs &args, int NR, int B, dim3 grid, hipStream_t st) {
   switch (NR) {
-    case 1: k_attn_valu<D, 1, MODE><<<grid, dim3(64), 0, st>>>(args); break;
-    case 2: k_attn_valu<D, 2, MODE><<<grid, dim3(64), 0, st>>>(args); break;
-    case 3: k_attn_valu<D, 3, MODE><<<grid, dim3(64), 0, st>>>(args); break;
-    case 4: k_attn_valu<D, 4, MODE><<<grid, dim3(64), 0, st>>>(args); break;
-    case 5: k_attn_valu<D, 5, MODE><<<grid, dim3(64), 0, st>>>(args); break;
-    case 6: k_attn_valu<D, 6, MODE><<<grid, dim3(64), 0, st>>>(args); break;
-    case 7: k_attn_valu<D, 7, MODE><<<grid, dim3(64), 0, st>>>(args); break;
-    case 8: k_attn_valu<D, 8, MODE><<<grid, dim3(64), 0, st>>>(args); break;
+    case 1: launch_one<D, MODE, 1>(args, B, grid, st); break;
+    case 2: launch_one<D, MODE, 2>(args, B, grid, st); break;
+    case 3: launch_one<D, MODE, 3>(args, B, grid, st); break;
+    case 4: launch_one<D, MODE, 4>(args, B, grid, st); break;
+    case 5: launch_one<D, MODE, 5>(args, B, grid, st); break;
+    case 6: launch_one<D, MODE, 6>(args, B, grid, st); break;
+    case 7: launch_one<D, MODE, 7>(args, B, grid, st); break;
+    case 8: launch_one<D, MODE, 8>(args, B, grid, st); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -297,14 +469,14 @@ hipError_t launch_attn_valu(const PoolGeometry &g, int32_t layer, const AttnLaun
   const dim3 grid((unsigned)p.max_splits, (unsigned)g.Hkv, (unsigned)a.B);
   switch (g.D) {
     case 64:
-      return g.mode == MODE_REF ? launch_valu_nr<64, MODE_REF>(args, p.NR, grid, st)
-                                : launch_valu_nr<64, MODE_AFFINE>(args, p.NR, grid, st);
+      return g.mode == MODE_REF ? launch_valu_nr<64, MODE_REF>(args, p.NR, a.B, grid, st)
+                                : launch_valu_nr<64, MODE_AFFINE>(args, p.NR, a.B, grid, st);
     case 128:
-      return g.mode == MODE_REF ? launch_valu_nr<128, MODE_REF>(args, p.NR, grid, st)
-                                : launch_valu_nr<128, MODE_AFFINE>(args, p.NR, grid, st);
+      return g.mode == MODE_REF ? launch_valu_nr<128, MODE_REF>(args, p.NR, a.B, grid, st)
+                                : launch_valu_nr<128, MODE_AFFINE>(args, p.NR, a.B, grid, st);
     case 256:
-      return g.mode == MODE_REF ? launch_valu_nr<256, MODE_REF>(args, p.NR, grid, st)
-                                : launch_valu_nr<256, MODE_AFFINE>(args, p.NR, grid, st);
+      return g.mode == MODE_REF ? launch_valu_nr<256, MODE_REF>(args, p.NR, a.B, grid, st)
+                                : launch_valu_nr<256, MODE_AFFINE>(args, p.NR, a.B, grid, st);
     default:
       return hipErrorInvalidValue;
   }

@@ -139,4 +139,52 @@ __device__ __forceinline__ float wave_min_range(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Whole-wave all-reductions without LDS: DPP inside each 16-lane row
+// (quad xor 1, quad xor 2, row rotate 4, row rotate 8), then the gfx950
+// row-pair and half-wave swaps (v_permlane16_swap / v_permlane32_swap).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(unsigned, v), CTRL, 0xf, 0xf,
+                                                               false));
+}
+__device__ __forceinline__ float wave_allsum(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x124>(v);  // row_ror:4
+  v += dpp_f32<0x128>(v);  // row_ror:8
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  auto s16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = __builtin_bit_cast(float, s16[0]) + __builtin_bit_cast(float, s16[1]);
+  const unsigned w = __builtin_bit_cast(unsigned, v);
+  auto s32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return __builtin_bit_cast(float, s32[0]) + __builtin_bit_cast(float, s32[1]);
+}
+__device__ __forceinline__ float wave_allmax(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x124>(v));
+  v = fmaxf(v, dpp_f32<0x128>(v));
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  auto s16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = fmaxf(__builtin_bit_cast(float, s16[0]), __builtin_bit_cast(float, s16[1]));
+  const unsigned w = __builtin_bit_cast(unsigned, v);
+  auto s32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return fmaxf(__builtin_bit_cast(float, s32[0]), __builtin_bit_cast(float, s32[1]));
+}
+
+// A zero the compiler cannot see through: loads addressed with it stay below
+// the point where it is produced (used to keep scalar loads from being
+// hoisted all at once).
+__device__ __forceinline__ int opaque_zero() {
+  int z;
+  asm volatile("s_mov_b32 %0, 0" : "=s"(z));
+  return z;
+}
+// Register fence: `x` is treated as rewritten after `after` is available, so
+// work on `x` cannot be scheduled ahead of the work that produced `after`
+// (bounds register live ranges the scheduler would otherwise stretch).
+__device__ __forceinline__ void order_after(uint4 &x, float after) {
+  asm volatile("; order %0 %1 %2 %3 after %4" : "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w) : "v"(after));
+}
+
 }  // namespace krill

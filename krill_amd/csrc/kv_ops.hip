@@ -7,6 +7,7 @@
 #include <algorithm>
 #include <cmath>
 
+#include "attn_common.hpp"
 #include "block_manager.hpp"
 #include "kdev.hpp"
 #include "launch.hpp"
@@ -506,18 +507,19 @@ int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq,
   sb = std::min(sb, nb_max);
   p.split_blocks = sb;
   p.max_splits = (nb_max + sb - 1) / sb;
-  const size_t o_bytes = (size_t)B * g.Hkv * p.max_splits * p.NR * g.D * sizeof(float);
-  const size_t ml_bytes = (size_t)B * g.Hkv * p.max_splits * p.NR * 2 * sizeof(float);
-  p.ws_bytes = ((o_bytes + 255) & ~(size_t)255) + ml_bytes;
+  p.ws_bytes = ws_layout(B, g.Hkv, p.max_splits, p.NR, g.D, g.G).total;
   *plan = p;
   return 0;
 }
 
+// Separate split merge, used after the MFMA kernel (the VALU kernel merges
+// inside its last split).
 hipError_t launch_attn_merge(const PoolGeometry &g, const AttnLaunch &a, const AttnPlan &p, hipStream_t st) {
   if (p.max_splits <= 1 || a.B == 0) return hipSuccess;
-  const size_t o_bytes = (size_t)a.B * g.Hkv * p.max_splits * p.NR * g.D * sizeof(float);
-  const float *ws_o = static_cast<const float *>(a.ws);
-  const float *ws_ml = reinterpret_cast<const float *>(static_cast<const uint8_t *>(a.ws) + ((o_bytes + 255) & ~(size_t)255));
+  const WsLayout w = ws_layout(a.B, g.Hkv, p.max_splits, p.NR, g.D, g.G);
+  const uint8_t *base = static_cast<const uint8_t *>(a.ws);
+  const float *ws_o = reinterpret_cast<const float *>(base + w.o);
+  const float *ws_ml = reinterpret_cast<const float *>(base + w.ml);
   k_attn_merge<<<dim3((unsigned)p.NR, (unsigned)g.Hkv, (unsigned)a.B), dim3(64), 0, st>>>(
       ws_o, ws_ml, a.lens, a.max_blocks, g.Hkv, p.NR, a.Hq / g.Hkv, a.Lq, a.Hq, g.D, p.split_blocks, p.max_splits, a.out,
       a.out_dtype);
@@ -527,7 +529,8 @@ hipError_t launch_attn_merge(const PoolGeometry &g, const AttnLaunch &a, const A
 hipError_t launch_attention(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
                             hipStream_t st) {
   if (a.B == 0) return hipSuccess;
-  hipError_t e = p.use_mfma ? launch_attn_mfma(g, layer, a, p, st) : launch_attn_valu(g, layer, a, p, st);
+  if (!p.use_mfma) return launch_attn_valu(g, layer, a, p, st);
+  hipError_t e = launch_attn_mfma(g, layer, a, p, st);
   if (e != hipSuccess) return e;
   return launch_attn_merge(g, a, p, st);
 }

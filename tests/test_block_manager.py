@@ -1,0 +1,422 @@
+"""Block manager through the C ABI on a host-only pool (no GPU needed).
+
+Known-answer cases re-express the reference's cache tests at the level of
+token positions: the paged cache must hold, position by position, what the
+reference's contiguous cache holds after the same updates, truncates and
+restores (KVCacheTests.swift, SpeculativeDecodingTests.swift:99-158,
+QuantizedPrefixCacheTests.swift, PrefixCacheTests.swift).  A simulated
+device (slot -> token id, block copies applied for every copy-on-write)
+checks the paging itself."""
+import threading
+
+import numpy as np
+import pytest
+
+import krill_amd
+from krill_amd import KrillError
+from krill_amd import _lib as L
+
+
+def host_pool(blocks=64, **kw):
+    return krill_amd.KVPool(2, 2, 128, blocks, "affine_g64", "bf16", host_only=True, **kw)
+
+
+class Sim:
+    """Logical content per sequence and a simulated device memory.  Block
+    copies are applied whenever a reservation replaced a shared tail block."""
+
+    def __init__(self, pool):
+        self.pool = pool
+        self.mem = {}      # slot -> token id
+        self.content = {}  # seq -> list of token ids
+        self.next_tok = 1
+
+    def create(self):
+        s = self.pool.seq_create()
+        self.content[s] = []
+        return s
+
+    def append(self, s, n):
+        before = self.pool.block_table(s)
+        length = len(self.content[s])
+        slots = self.pool.reserve_append(s, n)
+        after = self.pool.block_table(s)
+        if length % 64 and before[length // 64] != after[length // 64]:
+            src, dst = before[length // 64], after[length // 64]   # copy-on-write
+            for t in range(64):
+                if src * 64 + t in self.mem:
+                    self.mem[dst * 64 + t] = self.mem[src * 64 + t]
+        rc = self.pool.refcounts()
+        for sl in slots:
+            assert rc[sl // 64] == 1, "a slot handed out for writing lives in a shared block"
+        toks = list(range(self.next_tok, self.next_tok + n))
+        self.next_tok += n
+        for sl, t in zip(slots, toks):
+            self.mem[int(sl)] = t
+        self.content[s] += toks
+        return slots
+
+    def fork(self, s, n):
+        f = self.pool.seq_fork(s, n)
+        self.content[f] = self.content[s][:n]
+        return f
+
+    def truncate(self, s, n):
+        self.pool.seq_truncate(s, n)
+        if 0 <= n < len(self.content[s]):
+            self.content[s] = self.content[s][:n]
+
+    def free(self, s):
+        self.pool.seq_free(s)
+        del self.content[s]
+
+    def read(self, s):
+        table = self.pool.block_table(s)
+        n = self.pool.seq_length(s)
+        return [self.mem.get(int(table[p // 64]) * 64 + p % 64) for p in range(n)]
+
+    def check(self, entries=()):
+        for s, c in self.content.items():
+            assert self.pool.seq_length(s) == len(c)
+            assert len(self.pool.block_table(s)) == (len(c) + 63) // 64
+            assert self.read(s) == c
+        # refcount = number of tables (live + prefix entries) holding the block
+        want = np.zeros(self.pool.num_blocks, np.int32)
+        for s in list(self.content) + list(entries):
+            for b in self.pool.block_table(s):
+                want[b] += 1
+        np.testing.assert_array_equal(self.pool.refcounts(), want)
+        st = self.pool.stats()
+        assert st["blocks_used"] == int((want > 0).sum())
+        assert st["blocks_free"] == self.pool.num_blocks - st["blocks_used"]
+
+
+# ------------------------------------------------------- known answers
+
+def test_update_concatenates_along_sequence_axis():
+    """KVCacheTests.swift:54-89: 1 row then 2 rows -> positions 0,1,2 in order."""
+    p = host_pool()
+    sim = Sim(p)
+    s = sim.create()
+    sim.append(s, 1)
+    sim.append(s, 2)
+    assert sim.read(s) == [1, 2, 3] and p.seq_length(s) == 3
+    sim.check()
+
+
+def test_truncate_slices_and_beyond_length_is_noop():
+    """KVCacheTests.swift:134-179 and QuantizedKVCache.truncate (:135-145)."""
+    p = host_pool()
+    sim = Sim(p)
+    s = sim.create()
+    sim.append(s, 4)
+    sim.truncate(s, 3)
+    assert sim.read(s) == [1, 2, 3]
+    sim.truncate(s, 6)   # beyond length: no-op
+    sim.truncate(s, -1)  # negative: no-op for the quantized cache
+    assert sim.read(s) == [1, 2, 3]
+    sim.check()
+
+
+def test_truncate_then_update_overwrites_stale_rows():
+    """KVCacheTests.swift:239-275: append 10, truncate 6, append 2 equals a
+    fresh cache fed the final sequence; the stale slots are reused."""
+    p = host_pool()
+    sim = Sim(p)
+    s = sim.create()
+    first = sim.append(s, 10)
+    sim.truncate(s, 6)
+    again = sim.append(s, 2)
+    np.testing.assert_array_equal(again, first[6:8])
+    assert sim.read(s) == [1, 2, 3, 4, 5, 6, 11, 12]
+    sim.check()
+
+
+def test_speculative_rollback_vectors():
+    """SpeculativeDecodingTests.swift:99-158: keep prev + accepted; full accept
+    keeps all k verify rows plus the bonus row."""
+    p = host_pool()
+    sim = Sim(p)
+    s = sim.create()
+    sim.append(s, 10)
+    prev = p.seq_length(s)
+    sim.append(s, 4)
+    assert p.seq_length(s) == 14
+    sim.truncate(s, prev + 2)
+    assert sim.read(s) == list(range(1, 11)) + [11, 12]
+    t = sim.create()
+    sim.append(t, 10)
+    sim.append(t, 4)
+    sim.append(t, 1)
+    assert p.seq_length(t) == 15 and sim.read(t)[-5:] == [25, 26, 27, 28, 29]
+    sim.check()
+
+
+def test_growth_across_many_blocks():
+    """KVCacheTests.swift:306-331: 300 appends of 2 rows survive intact."""
+    p = host_pool(blocks=16)
+    sim = Sim(p)
+    s = sim.create()
+    for _ in range(300):
+        sim.append(s, 2)
+    assert p.seq_length(s) == 600 and sim.read(s) == list(range(1, 601))
+    sim.check()
+
+
+def test_reset_and_memory_bytes():
+    p = host_pool()
+    s = p.seq_create()
+    p.reserve_append(s, 100)
+    # memorySizeBytes (QuantizedKVCache.swift:33-42) with G = 2 groups
+    assert p.seq_memory_bytes(s) == 2 * 100 * 2 * 128 + 4 * 100 * 2 * 2 * 2
+    p.seq_reset(s)
+    assert p.seq_length(s) == 0 and p.stats()["blocks_used"] == 0
+
+
+def test_fork_shares_blocks_and_cow_protects_the_sharer():
+    p = host_pool()
+    sim = Sim(p)
+    a = sim.create()
+    sim.append(a, 100)
+    f = sim.fork(a, 70)
+    assert p.block_table(f).tolist() == p.block_table(a).tolist()
+    assert p.refcounts()[p.block_table(a)].tolist() == [2, 2]
+    sim.append(f, 5)            # tail block 1 is shared -> copied
+    assert p.stats()["cow_copies"] == 1
+    assert p.block_table(f)[0] == p.block_table(a)[0] and p.block_table(f)[1] != p.block_table(a)[1]
+    sim.append(a, 3)            # a's tail is no longer shared: written in place
+    assert p.stats()["cow_copies"] == 1
+    sim.check()
+    g = sim.fork(a, 64)          # fork at a block boundary: the next token opens a new block
+    sim.append(g, 1)
+    assert p.stats()["cow_copies"] == 1
+    sim.check()
+
+
+def test_pool_exhaustion_is_an_error_that_changes_nothing():
+    p = host_pool(blocks=4)
+    s = p.seq_create()
+    p.reserve_append(s, 200)
+    with pytest.raises(KrillError) as e:
+        p.reserve_append(s, 100)
+    assert e.value.code == L.KRILL_E_NOMEM
+    assert p.seq_length(s) == 200 and p.stats()["blocks_used"] == 4
+    p.reserve_append(s, 56)  # exactly fills the pool
+    assert p.seq_length(s) == 256
+
+
+def test_frozen_entries_reject_mutation_and_bad_handles():
+    p = host_pool()
+    s = p.seq_create()
+    p.reserve_append(s, 20)
+    assert p.prefix_store(s, list(range(20)), "m")
+    _, e = p.prefix_lookup(list(range(20)), "m")
+    for fn in (lambda: p.reserve_append(e, 1), lambda: p.seq_truncate(e, 3), lambda: p.seq_free(e)):
+        with pytest.raises(KrillError) as err:
+            fn()
+        assert err.value.code == L.KRILL_E_STATE
+    for fn in (lambda: p.seq_length(999), lambda: p.seq_free(-1)):
+        with pytest.raises(KrillError) as err:
+            fn()
+        assert err.value.code == L.KRILL_E_INVAL
+    with pytest.raises(KrillError) as err:
+        p.seq_fork(s, 21)
+    assert err.value.code == L.KRILL_E_RANGE
+
+
+# ---------------------------------------------------------------- prefix
+
+def test_prefix_store_and_full_hit():
+    """QuantizedPrefixCacheTests.swift:25-53, :142-171: a full hit restores
+    the stored sequence; truncate(count - 1) and re-forward returns to count."""
+    p = host_pool(min_prefix_len=4, max_prefix_entries=4)
+    sim = Sim(p)
+    s = sim.create()
+    sim.append(s, 6)
+    assert p.prefix_store(s, list(range(6)), "m-int8")
+    plen, e = p.prefix_lookup(list(range(6)), "m-int8")
+    assert plen == 6 and e is not None
+    r = p.seq_fork(e, 5)           # restore + truncate(to: 5)
+    sim.content[r] = sim.content[s][:5]
+    sim.append(r, 1)               # re-feed the last token
+    assert p.seq_length(r) == 6
+    sim.check(entries=[e])
+    # the entry is unchanged by the restored sequence's write
+    assert sim.read(e) == [1, 2, 3, 4, 5, 6]
+
+
+def test_lookup_longest_prefix_vectors():
+    """QuantizedPrefixCacheTests.swift:92-121 (LCP 5, below-min miss)."""
+    p = host_pool(min_prefix_len=4)
+    s = p.seq_create()
+    p.reserve_append(s, 8)
+    stored = [10, 11, 12, 13, 14, 15, 16, 17]
+    assert p.prefix_store(s, stored, "m-int8")
+    assert p.prefix_lookup_longest([10, 11, 12, 13, 14, 99, 99], "m-int8")[0] == 5
+    assert p.prefix_lookup_longest([10, 11, 0, 0, 0, 0], "m-int8") == (0, None)
+    assert p.prefix_lookup_longest([10, 11, 12, 13, 14, 99, 99], "other") == (0, None)
+    assert p.prefix_lookup_longest([10, 11, 12, 13, 14, 99, 99], "m-int8", "img") == (0, None)
+
+
+def test_longest_match_wins():
+    """PrefixCacheTests.swift:321-343."""
+    p = host_pool(min_prefix_len=4)
+    short = list(range(6)) + [50]
+    long = list(range(9)) + [60]
+    a, b = p.seq_create(), p.seq_create()
+    p.reserve_append(a, len(short))
+    p.reserve_append(b, len(long))
+    p.prefix_store(a, short, "m")
+    p.prefix_store(b, long, "m")
+    plen, e = p.prefix_lookup_longest(list(range(9)) + [99, 99], "m")
+    assert plen == 9 and p.seq_length(e) == len(long)
+
+
+def test_exact_scan_steps_down_by_half_min_length():
+    """scan (PrefixCache.swift:273-308): checkLen = n, n - min/2, ..."""
+    p = host_pool(min_prefix_len=8)
+    s = p.seq_create()
+    p.reserve_append(s, 16)
+    p.prefix_store(s, list(range(12)), "m")
+    assert p.prefix_lookup(list(range(16)), "m")[0] == 12      # 16 -> 12 hits
+    assert p.prefix_lookup(list(range(15)), "m") == (0, None)   # 15, 11: no entry of that length
+    assert p.prefix_lookup(list(range(7)), "m") == (0, None)    # below minPrefixLength
+
+
+def test_store_guards_and_lru_capacity():
+    p = host_pool(min_prefix_len=4, max_prefix_entries=3, max_entry_bytes=2 * (2 * 10 * 2 * 128 + 4 * 10 * 2 * 2 * 2))
+    s = p.seq_create()
+    p.reserve_append(s, 40)
+    assert not p.prefix_store(s, [1, 2, 3], "m")            # below minPrefixLength
+    assert not p.prefix_store(s, list(range(11)), "m")      # over the per-entry byte cap
+    for i in range(5):
+        assert p.prefix_store(s, [100 + i] + list(range(5)), "m")
+    assert p.prefix_count() == 3                            # LRU capacity
+    assert p.prefix_lookup([100] + list(range(5)), "m") == (0, None)   # oldest evicted
+    assert p.prefix_lookup([104] + list(range(5)), "m")[0] == 6
+
+
+def test_watermark_eviction_frees_unreferenced_blocks():
+    """At 90% occupancy the oldest entries whose blocks no live sequence holds
+    are evicted; entries shared with live sequences survive."""
+    p = host_pool(blocks=20, max_prefix_entries=16, min_prefix_len=4)
+    live = p.seq_create()
+    p.reserve_append(live, 128)                       # 2 blocks, stays live
+    p.prefix_store(live, list(range(128)), "m")       # entry shares live's blocks
+    olds = []
+    for i in range(4):
+        s = p.seq_create()
+        p.reserve_append(s, 192)                      # 3 blocks each
+        p.prefix_store(s, [1000 * (i + 1)] + list(range(191)), "m")
+        p.seq_free(s)                                 # only the entry holds them now
+        olds.append([1000 * (i + 1)] + list(range(191)))
+    assert p.stats()["blocks_used"] == 14 and p.prefix_count() == 5
+    big = p.seq_create()
+    p.reserve_append(big, 5 * 64)                     # 14 + 5 > 18 (90% of 20)
+    st = p.stats()
+    assert st["blocks_used"] <= 18 and st["evicted_entries"] >= 1
+    assert p.prefix_lookup(olds[0], "m") == (0, None)  # least recently stored went first
+    assert p.prefix_lookup(list(range(128)), "m")[0] == 128  # shared with a live seq: kept
+    p.reserve_append(big, 64 * 5)                     # needs the rest: evicts what it must
+    assert p.prefix_lookup(list(range(128)), "m")[0] == 128
+    with pytest.raises(KrillError):
+        p.reserve_append(big, 64 * 10)
+
+
+def test_prefix_key_matches_oracle(oracle):
+    toks = [5, -3, 1 << 40]
+    assert krill_amd.prefix_key("model", "media", 2, toks) == oracle.prefix_key("model", "media", 2, toks)
+    assert krill_amd.prefix_key("model", None, 2, []) == oracle.prefix_key("model", None, 2, [])
+
+
+# ----------------------------------------------------------- randomized
+
+def test_model_based_random_operations():
+    hypothesis = pytest.importorskip("hypothesis")
+    st = hypothesis.strategies
+
+    @hypothesis.settings(max_examples=60, deadline=None)
+    @hypothesis.given(st.lists(st.tuples(st.integers(0, 6), st.integers(0, 10**6)), min_size=5, max_size=60))
+    def run(ops):
+        p = host_pool(blocks=48, min_prefix_len=4, max_prefix_entries=4, evict_watermark=0.9)
+        sim = Sim(p)
+        entries = {}
+        for op, arg in ops:
+            seqs = sorted(sim.content)
+            if op == 0 or not seqs:
+                sim.create()
+            elif op == 1:
+                s = seqs[arg % len(seqs)]
+                try:
+                    sim.append(s, 1 + arg % 90)
+                except KrillError as e:
+                    assert e.code == L.KRILL_E_NOMEM
+            elif op == 2:
+                s = seqs[arg % len(seqs)]
+                sim.truncate(s, arg % (len(sim.content[s]) + 2) - 1)
+            elif op == 3:
+                s = seqs[arg % len(seqs)]
+                sim.fork(s, arg % (len(sim.content[s]) + 1))
+            elif op == 4:
+                sim.free(seqs[arg % len(seqs)])
+            elif op == 5:
+                s = seqs[arg % len(seqs)]
+                if not sim.content[s]:
+                    continue
+                toks = [arg] + sim.content[s][1:]
+                if p.prefix_store(s, toks, "m"):
+                    entries[tuple(toks)] = list(sim.content[s])
+            else:
+                keys = list(entries)
+                if keys:
+                    toks = list(keys[arg % len(keys)])
+                    plen, e = p.prefix_lookup(toks, "m")
+                    if e is not None:
+                        # an entry that survives still holds exactly what was stored
+                        got = sim.read(e)
+                        assert got == entries[tuple(toks)][:plen]
+            # entries evicted or alive: recount
+            live_entries = []
+            for toks in list(entries):
+                plen, e = p.prefix_lookup(list(toks), "m")
+                if e is None:
+                    del entries[toks]
+                else:
+                    live_entries.append(e)
+            sim.check(entries=live_entries)
+        p.close()
+
+    run()
+
+
+def test_concurrent_hammer_keeps_capacity_invariant():
+    """PrefixCacheTests.swift:354-380: 8 threads x 200 iterations."""
+    p = host_pool(blocks=4096, min_prefix_len=4, max_prefix_entries=4)
+    errors = []
+
+    def worker(t):
+        try:
+            for i in range(200):
+                s = p.seq_create()
+                p.reserve_append(s, 6)
+                toks = list(range(t * 1000 + i, t * 1000 + i + 6))
+                p.prefix_store(s, toks, f"m{i % 3}")
+                p.prefix_lookup(toks, f"m{i % 3}")
+                p.prefix_lookup(list(range(6)), f"m{i % 3}")
+                p.seq_free(s)
+                if i % 50 == 0:
+                    p.prefix_clear()
+        except Exception as e:  # pragma: no cover - reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(8)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors
+    assert p.prefix_count() <= 4
+    st = p.stats()
+    assert st["live_seqs"] == 0
+    p.prefix_clear()
+    assert p.stats()["blocks_used"] == 0

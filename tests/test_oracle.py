@@ -1,0 +1,307 @@
+"""Pins of the CPU oracle: each oracle function is checked against something
+other than itself -- IEEE conversions in numpy/torch, independent dtype
+arithmetic, the reference's own unit-test tolerances and closed forms."""
+import os
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+# --------------------------------------------------------------- conversions
+
+def test_f16_exhaustive_round_trip(oracle):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = oracle.c_f16_to_f32_array(bits)
+    np.testing.assert_array_equal(f.view(np.uint32), bits.view(np.float16).astype(np.float32).view(np.uint32))
+    nan = np.isnan(f)
+    back = oracle.c_f32_to_f16_array(f)
+    np.testing.assert_array_equal(back[~nan], bits[~nan])
+    assert np.all(np.isnan(back[nan].view(np.float16)))
+
+
+def test_f32_to_f16_matches_numpy_ieee_cast(oracle):
+    rng = np.random.default_rng(0)
+    parts = [
+        rng.standard_normal(200_000).astype(np.float32),
+        (rng.standard_normal(100_000) * 1e-5).astype(np.float32),   # subnormal range
+        (rng.standard_normal(100_000) * 1e-7).astype(np.float32),   # below half the smallest subnormal
+        (rng.uniform(6.0e4, 7.0e4, 100_000) * rng.choice([-1, 1], 100_000)).astype(np.float32),  # overflow edge
+        rng.integers(0, 2**32, 200_000, dtype=np.uint64).astype(np.uint32).view(np.float32),  # any pattern
+    ]
+    # exact ties of binary16 (round to even) and boundaries
+    h = np.arange(0, 0x7BFF, dtype=np.uint16)
+    lo = h.view(np.float16).astype(np.float64)
+    hi = (h + 1).view(np.float16).astype(np.float64)
+    parts.append(((lo + hi) / 2).astype(np.float32))
+    parts.append(np.array([65504, 65519.99, 65520, 2.0**-24, 2.0**-25, 3 * 2.0**-26, 0.0, -0.0], np.float32))
+    x = np.concatenate(parts)
+    x = x[~np.isnan(x)]
+    np.testing.assert_array_equal(oracle.c_f32_to_f16_array(x), x.astype(np.float16).view(np.uint16))
+
+
+def test_f32_to_bf16_matches_torch_rne(oracle):
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        rng.standard_normal(200_000).astype(np.float32),
+        rng.integers(0, 2**32, 200_000, dtype=np.uint64).astype(np.uint32).view(np.float32),
+    ])
+    x = x[~np.isnan(x)]
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(oracle.c_f32_to_bf16_array(x), want)
+    np.testing.assert_array_equal(oracle.f32_to_bf16_bits(x), want)
+
+
+# --------------------------------------------------- reference row quantizer
+
+def _numpy_ref_quantize(x_bits, dt):
+    """Restatement of QuantizedKVCache.quantizePerHead with numpy/torch dtype
+    arithmetic (independent of the oracle's bit-level code): dtype subtraction,
+    float32 division by 255 and by the safe scale, clip, truncating cast."""
+    torch = pytest.importorskip("torch")
+    if dt == 0:
+        x = x_bits.view(np.float16)
+        mn = x.min(axis=-1, keepdims=True)
+        mx = x.max(axis=-1, keepdims=True)
+        d = (mx - mn).astype(np.float32)                  # float16 subtraction
+        xm = (x - mn).astype(np.float32)
+        zero = mn.view(np.uint16)
+    else:
+        t = torch.from_numpy(x_bits.view(np.int16)).view(torch.bfloat16)
+        mn = t.min(dim=-1, keepdim=True).values
+        mx = t.max(dim=-1, keepdim=True).values
+        d = (mx - mn).float().numpy()                     # bfloat16 subtraction
+        xm = (t - mn).float().numpy()
+        zero = mn.float().numpy().astype(np.float16).view(np.uint16)
+    scale = d / np.float32(255.0)
+    safe = np.maximum(scale, np.float32(1e-8))
+    n = np.clip(xm / safe, np.float32(0), np.float32(255))
+    q = n.astype(np.uint8)                                 # truncation
+    return q, safe.astype(np.float16).view(np.uint16), zero
+
+
+@pytest.mark.parametrize("dt", [0, 1])
+@pytest.mark.parametrize("D", [4, 7, 64, 128])
+def test_quantize_ref_matches_independent_restatement(oracle, dt, D):
+    rng = np.random.default_rng(10 + D + dt)
+    x = rng.standard_normal((500, D)).astype(np.float32) * rng.choice([0.01, 1, 30], (500, 1)).astype(np.float32)
+    bits = oracle.f32_to_bf16_bits(x) if dt == 1 else oracle.f32_to_f16_bits(x)
+    q, s, z = oracle.quantize_ref(bits, dt)
+    eq, es, ez = _numpy_ref_quantize(bits, dt)
+    np.testing.assert_array_equal(q, eq)
+    np.testing.assert_array_equal(s, es)
+    np.testing.assert_array_equal(z, ez)
+
+
+def test_quantize_ref_known_answers(oracle):
+    # [0, 1]: scale = f32(1)/255 rounds up, so 1/scale truncates to 254
+    q, s, z = oracle.quantize_ref(np.array([[0, 1]], np.float32).astype(np.float16).view(np.uint16), 0)
+    assert q.tolist() == [[0, 254]]
+    assert s[0, 0] == np.float16(np.float32(1) / np.float32(255)).view(np.uint16)
+    # constant row: scale clamps to 1e-8, which rounds to fp16 zero; q = 0; zero = the value
+    c = np.full((1, 16), 3.5, np.float32).astype(np.float16).view(np.uint16)
+    q, s, z = oracle.quantize_ref(c, 0)
+    assert not q.any() and s[0, 0] == 0 and z[0, 0] == np.float16(3.5).view(np.uint16)
+    deq = oracle.dequant_ref_f16(q, s, z).view(np.float16)
+    assert np.all(deq == np.float16(3.5))
+    # the row minimum always maps to byte 0
+    rng = np.random.default_rng(3)
+    x = oracle.f32_to_bf16_bits(rng.standard_normal((200, 64)).astype(np.float32))
+    q, _, _ = oracle.quantize_ref(x, 1)
+    xf = oracle.bf16_bits_to_f32(x)
+    assert np.all(q[np.arange(200), xf.argmin(axis=1)] == 0)
+
+
+def _weyl(shape, lo, hi):
+    """deterministicTensor of QuantizedKVCacheUnitTests.swift:17-27 in float32
+    (Swift Float arithmetic, no fused multiply-add), then fp16."""
+    total = int(np.prod(shape))
+    span = np.float32(max(np.float32(hi) - np.float32(lo), np.float32(1e-3)))
+    c = np.float32(0.6180339887)
+    i = np.arange(total).astype(np.float32)
+    prod = (i * c).astype(np.float32)
+    frac = (prod - np.trunc(prod).astype(np.float32)).astype(np.float32)
+    vals = (np.float32(lo) + (frac * span).astype(np.float32)).astype(np.float32)
+    return vals.reshape(shape).astype(np.float16).view(np.uint16)
+
+
+@pytest.mark.parametrize("lo,hi,extra", [(0.0, 10.0, 1e-3), (0.0, 5.0, 1e-3), (-64.0, 64.0, 1e-2),
+                                         (-32.0, 64.0, 1e-2)])
+def test_reference_unit_test_round_trip_tolerance(oracle, lo, hi, extra):
+    """QuantizedKVCacheUnitTests.swift:38-84: round trip within 1.5 steps + slack."""
+    x = _weyl([1, 4, 8, 16], lo, hi)
+    q, s, z = oracle.quantize_ref(x, 0)
+    deq = oracle.dequant_ref_f16(q, s, z).view(np.float16).astype(np.float32)
+    err = np.abs(deq - x.view(np.float16).astype(np.float32)).max()
+    assert err < (hi - lo) / 255.0 * 1.5 + extra
+
+
+def test_golden_quantize_vectors(oracle):
+    """Committed fixtures (tests/golden/make_golden.py) still reproduce."""
+    path = os.path.join(HERE, "golden", "quantize_golden.npz")
+    g = np.load(path, allow_pickle=False)
+    for name in sorted({k.rsplit("__", 1)[0] for k in g.files}):
+        x, dt, mode = g[name + "__x"], int(g[name + "__dt"]), int(g[name + "__mode"])
+        q, s, z = oracle.quantize(x, dt, mode)
+        np.testing.assert_array_equal(q, g[name + "__q"], err_msg=name)
+        np.testing.assert_array_equal(s, g[name + "__s"], err_msg=name)
+        np.testing.assert_array_equal(z, g[name + "__z"], err_msg=name)
+
+
+# ------------------------------------------------------ affine group-64 mode
+
+def _numpy_affine(w16):
+    """The affine rule restated with numpy float32 arithmetic."""
+    w = w16.view(np.float16).astype(np.float32)
+    wmin, wmax = w.min(), w.max()
+    side = abs(wmin) > abs(wmax)
+    s = np.float32((wmax - wmin) / np.float32(255))
+    s = s if s > np.float32(1e-7) else np.float32(1e-7)
+    s = s if side else -s
+    edge = wmin if side else wmax
+    q0 = np.rint(np.float32(edge / s))
+    bias = np.float32(0)
+    if q0 != 0:
+        s = np.float32(edge / q0)
+        bias = edge
+    q = np.minimum(np.rint((w - bias) / s), np.float32(255)).astype(np.uint8)
+    return q, np.float16(s).view(np.uint16), np.float16(bias).view(np.uint16)
+
+
+def test_affine_matches_restatement_and_invariants(oracle):
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((300, 128)).astype(np.float32) * rng.choice([0.001, 1, 50], (300, 1)).astype(np.float32)
+    x[:20, 5] = 0.0  # an exact zero in some groups
+    bits = oracle.f32_to_f16_bits(x)
+    q, s, b = oracle.quantize_mlx(bits, 0, 64)
+    for r in range(0, 300, 7):
+        for g in range(2):
+            eq, es, eb = _numpy_affine(bits[r, 64 * g: 64 * (g + 1)])
+            np.testing.assert_array_equal(q[r, 64 * g: 64 * (g + 1)], eq)
+            assert s[r, g] == es and b[r, g] == eb
+    sf = s.view(np.float16).astype(np.float64)
+    bf = b.view(np.float16).astype(np.float64)
+    w = bits.view(np.float16).astype(np.float64)
+    deq = oracle.dequant_f64(q, s, b, 1)
+    # half a step, plus the fp16 rounding of scale and bias (relative 2^-11,
+    # or half the subnormal spacing 2^-25 when the scale is subnormal)
+    ds = np.maximum(np.abs(sf) * 2.0**-11, 2.0**-25)
+    db = np.maximum(np.abs(bf) * 2.0**-11, 2.0**-25)
+    err = np.abs(deq - w)
+    rnd = np.repeat(255 * ds + db + 1e-12, 64, axis=1)
+    step = np.repeat(np.abs(sf), 64, axis=1)
+    # interior codes round to the nearest grid point: half a step
+    interior = (q > 0) & (q < 255)
+    assert np.all(err[interior] <= 0.5 * step[interior] + rnd[interior])
+    # the grid spans 255*|s| with |s| = |edge|/|q0|, which can fall short of
+    # the group range by under one step, so a clamped end code is within a step
+    assert np.all(err <= step + rnd)
+    # the zero point is a grid point before the fp16 rounding of scale/bias:
+    # 0 dequantizes to q0*ds + db at most
+    assert np.all(np.abs(deq[:20, 5]) <= q[:20, 5] * ds[:20, 0] + db[:20, 0] + 1e-12)
+
+
+def test_affine_bf16_input_is_cast_to_f16_first(oracle):
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((10, 64)).astype(np.float32)
+    b16 = oracle.f32_to_bf16_bits(x)
+    f16 = oracle.bf16_bits_to_f32(b16).astype(np.float16).view(np.uint16)
+    for a, c in zip(oracle.quantize_mlx(b16, 1), oracle.quantize_mlx(f16, 0)):
+        np.testing.assert_array_equal(a, c)
+
+
+# ------------------------------------------------------------- dequantizer
+
+def test_dequant_ref_two_roundings_exhaustive_bytes(oracle):
+    """f16(f16(f16(q)*s) + z) for every byte, against numpy float16 arithmetic."""
+    rng = np.random.default_rng(7)
+    q = np.tile(np.arange(256, dtype=np.uint8), (50, 1))
+    s = (rng.uniform(1e-4, 1.0, (50, 1)).astype(np.float32)).astype(np.float16)
+    z = (rng.standard_normal((50, 1)).astype(np.float32) * 10).astype(np.float16)
+    got = oracle.dequant_ref_f16(q, s.view(np.uint16), z.view(np.uint16)).view(np.float16)
+    want = (q.astype(np.float16) * s) + z   # two float16 roundings
+    np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+    # a fused multiply-add differs somewhere (the check has teeth)
+    fused = (q.astype(np.float64) * s.astype(np.float64) + z.astype(np.float64)).astype(np.float16)
+    assert np.any(fused.view(np.uint16) != want.view(np.uint16))
+
+
+# -------------------------------------------------------------- attention
+
+def _np_attention(q, k, v, limits, scale):
+    out = np.zeros_like(q)
+    for r in range(q.shape[0]):
+        s = (k[: limits[r]] @ q[r]) * scale
+        p = np.exp(s - s.max())
+        out[r] = p @ v[: limits[r]] / p.sum()
+    return out
+
+
+def test_attention_closed_forms(oracle):
+    rng = np.random.default_rng(8)
+    D = 16
+    v = rng.standard_normal((5, D))
+    k = rng.standard_normal((5, D))
+    q = rng.standard_normal((3, D))
+    # one visible key -> that value row
+    np.testing.assert_allclose(oracle.attention_f64(q, k, v, [1, 1, 1], 0.3), np.tile(v[0], (3, 1)), atol=1e-12)
+    # identical keys -> mean of the values
+    kk = np.tile(k[0], (5, 1))
+    np.testing.assert_allclose(oracle.attention_f64(q, kk, v, [5, 5, 5], 0.3), np.tile(v.mean(0), (3, 1)),
+                               atol=1e-12)
+    # rows see different prefixes (causal limits); keys past the limit never matter
+    lim = [2, 4, 5]
+    k2 = k.copy()
+    k2[4] = 1e6
+    got = oracle.attention_f64(q, k2, v, [2, 4, 4], 0.3)
+    np.testing.assert_allclose(got, _np_attention(q, k, v, [2, 4, 4], 0.3), atol=1e-12)
+    np.testing.assert_allclose(oracle.attention_f64(q, k, v, lim, 0.3), _np_attention(q, k, v, lim, 0.3),
+                               atol=1e-12)
+
+
+def test_masked_minus_10000_underflows_to_zero():
+    """BatchedDecode.swift:22-28: exp(score - 10000) is 0 in f16, bf16, f32,
+    so a length bound equals the reference's additive mask."""
+    for dt in (np.float16, np.float32):
+        assert np.exp(np.array(5.0 - 10000.0, dt)) == 0
+
+
+# ------------------------------------------------------- stack and prefix
+
+def test_stack_left_padded_closed_form(oracle):
+    rows_q = [np.arange(2 * 1 * 3, dtype=np.uint8).reshape(2, 1, 3), (10 + np.arange(2 * 3 * 3)).astype(np.uint8).reshape(2, 3, 3)]
+    rows_s = [np.full((2, 1, 1), 7, np.uint16), np.full((2, 3, 1), 9, np.uint16)]
+    rows_z = [np.full((2, 1, 1), 1, np.uint16), np.full((2, 3, 1), 2, np.uint16)]
+    q, s, z = oracle.stack_left_padded(rows_q, rows_s, rows_z, [1, 3])
+    assert q.shape == (2, 2, 3, 3)
+    assert q[0, 0].tolist() == [[0, 0, 0], [0, 0, 0], [0, 1, 2]]
+    assert q[0, 1].tolist() == [[0, 0, 0], [0, 0, 0], [3, 4, 5]]
+    assert q[1, 0].tolist() == [[10, 11, 12], [13, 14, 15], [16, 17, 18]]
+    assert s[0, 0, :, 0].tolist() == [0, 0, 7] and z[0, 1, :, 0].tolist() == [0, 0, 1]
+
+
+def test_fnv1a64_published_vectors(oracle):
+    assert oracle.fnv1a64(b"") == 0xCBF29CE484222325
+    assert oracle.fnv1a64(b"a") == 0xAF63DC4C8601EC8C
+    assert oracle.fnv1a64(b"foobar") == 0x85944171F73967E8
+
+
+def test_prefix_key_layout(oracle):
+    """cacheKey bytes: 3, tag, model, FF, media, FF, tokens as 8-byte LE."""
+    toks = [1, 258, -1]
+    data = bytes([3, 2]) + b"m" + b"\xff" + b"img" + b"\xff" + b"".join(int(t).to_bytes(8, "little", signed=True) for t in toks)
+    assert oracle.prefix_key("m", "img", 2, toks) == oracle.fnv1a64(data)
+    assert oracle.prefix_key("m", None, 2, toks) == oracle.prefix_key("m", "", 2, toks)
+    assert oracle.prefix_key("m", None, 1, toks) != oracle.prefix_key("m", None, 2, toks)
+
+
+def test_common_prefix_length_reference_vectors(oracle):
+    """PrefixCacheTests.swift:244-250."""
+    cpl = oracle.common_prefix_length
+    assert cpl([1, 2, 3, 4], [1, 2, 3, 4]) == 4
+    assert cpl([1, 2, 3, 9], [1, 2, 3, 4]) == 3
+    assert cpl([1, 2], [1, 2, 3, 4]) == 2
+    assert cpl([9, 1], [1, 2]) == 0
+    assert cpl([], [1]) == 0
