@@ -12,9 +12,8 @@ namespace krill {
 //   ml     float [B][Hkv][max_splits][NR][2]   (running max m in log2 units, sum l)
 //   q16    fp16  [B][Hkv][NR][D]               queries rounded to fp16 (VALU path)
 //   qsum   float [B][Hkv][NR][G]               per scale group sums of q16
-//   count  u32   [B][Hkv]                      splits finished (last one merges)
 struct WsLayout {
-  size_t o, ml, q16, qsum, count, total;
+  size_t o, ml, q16, qsum, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -25,8 +24,7 @@ inline WsLayout ws_layout(int64_t B, int64_t Hkv, int64_t max_splits, int64_t NR
   w.ml = align256(w.o + (size_t)(B * Hkv * max_splits * NR * D) * sizeof(float));
   w.q16 = align256(w.ml + (size_t)(B * Hkv * max_splits * NR * 2) * sizeof(float));
   w.qsum = align256(w.q16 + (size_t)(B * Hkv * NR * D) * sizeof(uint16_t));
-  w.count = align256(w.qsum + (size_t)(B * Hkv * NR * G) * sizeof(float));
-  w.total = align256(w.count + (size_t)(B * Hkv) * sizeof(uint32_t));
+  w.total = align256(w.qsum + (size_t)(B * Hkv * NR * G) * sizeof(float));
   return w;
 }
 
@@ -44,7 +42,6 @@ struct AttnArgs {
   float *ws_ml;
   uint16_t *q16;
   float *qsum;
-  uint32_t *count;
   void *out;  // [B][Hq][Lq][D]
   int32_t out_dtype;
 };
@@ -74,7 +71,6 @@ inline AttnArgs make_attn_args(const PoolGeometry &g, int32_t layer, const AttnL
   r.ws_ml = reinterpret_cast<float *>(base + w.ml);
   r.q16 = reinterpret_cast<uint16_t *>(base + w.q16);
   r.qsum = reinterpret_cast<float *>(base + w.qsum);
-  r.count = reinterpret_cast<uint32_t *>(base + w.count);
   r.out = a.out;
   r.out_dtype = a.out_dtype;
   return r;

@@ -30,8 +30,10 @@
 //  * the next block's K and V are loaded as soon as the current block's
 //    registers are consumed, so loads overlap the other phase's math.
 // A sequence with one split writes the output directly; otherwise every
-// split writes (m, l, o) to the workspace and the last split to finish
-// (device-scope counter) merges them.
+// split writes (m, l, o) to the workspace and k_attn_merge combines them in a
+// second launch.  (Merging inside the last split to finish would need an
+// agent-scope release/acquire per split, which on this multi-XCD part is a
+// whole-L2 writeback and invalidate per wave.)
 #include <hip/hip_runtime.h>
 
 #include "attn_common.hpp"
@@ -42,24 +44,37 @@ typedef __attribute__((address_space(4))) const float scalar_f32;
 
 // acc += sum_i k[i] . q_(OFF + i), i < 8, where q_n is lane n of this lane's
 // 16-lane row of `q` (v_dot2c_f32_f16 with a DPP row_newbcast source).  The
-// leading s_nop covers the VALU-write -> DPP-read hazard on `q`.
-template <int OFF>
+// leading s_nop covers the VALU-write -> DPP-read hazard of the operands.
+// The compiler cannot see the DOT instructions inside the asm, so it does not
+// guard their result: a VALU instruction other than another v_dot2c reading
+// `acc` as its accumulator needs 3 wait states after the last one (without
+// them it reads a value missing the last dots).  TAIL marks the block that
+// finishes `acc`; it ends with the wait.
+#define KRILL_DOT8_BODY                                                                    \
+  "s_nop 1\n\t"                                                                            \
+  "v_dot2c_f32_f16_dpp %0, %1, %2 row_newbcast:%10 row_mask:0xf bank_mask:0xf\n\t"         \
+  "v_dot2c_f32_f16_dpp %0, %1, %3 row_newbcast:%11 row_mask:0xf bank_mask:0xf\n\t"         \
+  "v_dot2c_f32_f16_dpp %0, %1, %4 row_newbcast:%12 row_mask:0xf bank_mask:0xf\n\t"         \
+  "v_dot2c_f32_f16_dpp %0, %1, %5 row_newbcast:%13 row_mask:0xf bank_mask:0xf\n\t"         \
+  "v_dot2c_f32_f16_dpp %0, %1, %6 row_newbcast:%14 row_mask:0xf bank_mask:0xf\n\t"         \
+  "v_dot2c_f32_f16_dpp %0, %1, %7 row_newbcast:%15 row_mask:0xf bank_mask:0xf\n\t"         \
+  "v_dot2c_f32_f16_dpp %0, %1, %8 row_newbcast:%16 row_mask:0xf bank_mask:0xf\n\t"         \
+  "v_dot2c_f32_f16_dpp %0, %1, %9 row_newbcast:%17 row_mask:0xf bank_mask:0xf"
+#define KRILL_DOT8_OPERANDS                                                                           \
+  : "+v"(acc)                                                                                         \
+  : "v"(q), "v"(k[0]), "v"(k[1]), "v"(k[2]), "v"(k[3]), "v"(k[4]), "v"(k[5]), "v"(k[6]), "v"(k[7]), \
+    "n"(OFF), "n"(OFF + 1), "n"(OFF + 2), "n"(OFF + 3), "n"(OFF + 4), "n"(OFF + 5), "n"(OFF + 6), "n"(OFF + 7)
+template <int OFF, bool TAIL>
 __device__ __forceinline__ void dot8_bcast(float &acc, uint32_t q, const half2_t (&k)[8]) {
-  asm("s_nop 1\n\t"
-      "v_dot2c_f32_f16_dpp %0, %1, %2 row_newbcast:%10 row_mask:0xf bank_mask:0xf\n\t"
-      "v_dot2c_f32_f16_dpp %0, %1, %3 row_newbcast:%11 row_mask:0xf bank_mask:0xf\n\t"
-      "v_dot2c_f32_f16_dpp %0, %1, %4 row_newbcast:%12 row_mask:0xf bank_mask:0xf\n\t"
-      "v_dot2c_f32_f16_dpp %0, %1, %5 row_newbcast:%13 row_mask:0xf bank_mask:0xf\n\t"
-      "v_dot2c_f32_f16_dpp %0, %1, %6 row_newbcast:%14 row_mask:0xf bank_mask:0xf\n\t"
-      "v_dot2c_f32_f16_dpp %0, %1, %7 row_newbcast:%15 row_mask:0xf bank_mask:0xf\n\t"
-      "v_dot2c_f32_f16_dpp %0, %1, %8 row_newbcast:%16 row_mask:0xf bank_mask:0xf\n\t"
-      "v_dot2c_f32_f16_dpp %0, %1, %9 row_newbcast:%17 row_mask:0xf bank_mask:0xf"
-      : "+v"(acc)
-      : "v"(q), "v"(k[0]), "v"(k[1]), "v"(k[2]), "v"(k[3]), "v"(k[4]), "v"(k[5]), "v"(k[6]), "v"(k[7]),
-        "n"(OFF), "n"(OFF + 1), "n"(OFF + 2), "n"(OFF + 3), "n"(OFF + 4), "n"(OFF + 5), "n"(OFF + 6), "n"(OFF + 7));
+  if constexpr (TAIL)
+    asm(KRILL_DOT8_BODY "\n\ts_nop 3" KRILL_DOT8_OPERANDS);
+  else
+    asm(KRILL_DOT8_BODY KRILL_DOT8_OPERANDS);
 }
+#undef KRILL_DOT8_BODY
+#undef KRILL_DOT8_OPERANDS
 
-// fp16 queries and their per-group sums; resets the split counters.
+// fp16 queries and their per-group sums.
 template <int D, int NR, int G>
 __global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
   const int hk = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
@@ -84,7 +99,6 @@ __global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
       if (lane == 0) a.qsum[(row0 + r) * G + g] = t;
     }
   }
-  if (lane == 0) a.count[(int64_t)b * a.Hkv + hk] = 0u;
 }
 
 template <int D, int NR, int MODE>
@@ -93,12 +107,9 @@ __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
   constexpr int NP = D / 16;   // 16-byte K pieces per token row
   constexpr int PPG = NP / G;  // pieces per scale group
   constexpr int DPL = D / 64;  // V^T rows (d values) per lane
-  constexpr int MAXS = 256;    // splits merged per LDS pass
 
   __shared__ __attribute__((aligned(16))) uint16_t w_lds[NR * G * 64];
   __shared__ __attribute__((aligned(16))) uint16_t sz_lds[2 * 64];
-  __shared__ float e_lds[MAXS];
-  __shared__ int last_lds;
 
   const int lane = threadIdx.x;
   const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
@@ -147,10 +158,18 @@ __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
   }
   const half2_t m1024 = half2_t{(_Float16)-1024.0f, (_Float16)-1024.0f};
 
+  // Physical block ids of this split (at most 64 blocks): lane i holds the
+  // entry of block blk0 + i, read back with v_readlane, so no table load sits
+  // between a prefetch and its use (a load there would have to drain the
+  // prefetch before its value could move to a scalar register).
+  int tab;
+  {
+    const int i = blk0 + lane;
+    const int phys = i < blk1 ? a.tables[(int64_t)b * a.max_blocks + i] : 0;
+    tab = (unsigned)phys < (unsigned)a.lv.num_blocks ? phys : 0;
+  }
   auto region_of = [&](int blk) -> const uint8_t * {
-    int phys = a.tables[(int64_t)b * a.max_blocks + blk];
-    phys = (unsigned)phys < (unsigned)a.lv.num_blocks ? phys : 0;
-    return head_region(a.lv, phys, hk);
+    return head_region(a.lv, __builtin_amdgcn_readlane(tab, blk - blk0), hk);
   };
   uint4 kr[NP];
   uint4 vr[2][2 * DPL];
@@ -166,20 +185,41 @@ __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
         vr[tg][i] = *reinterpret_cast<const uint4 *>(reg + v_offset(D) + ((tg * D + DPL * lane) << 5) + 16 * i);
   };
 
+  // this lane's token's (scale, zero) pairs, K and V
+  uint32_t km[G], vm[G];
+  auto load_meta = [&](const uint8_t *reg, uint32_t (&kmo)[G], uint32_t (&vmo)[G]) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      kmo[g] = *reinterpret_cast<const uint32_t *>(reg + km_offset(D) + ((lane * G + g) << 2));
+      vmo[g] = *reinterpret_cast<const uint32_t *>(reg + vm_offset(D, G) + ((lane * G + g) << 2));
+    }
+  };
+
+  // Loads of block n+1 are issued in a fixed order inside the loop: K bytes
+  // and metadata once block n's K registers are consumed, V bytes once its V
+  // registers are; waits on a load never cover a younger prefetch.  The
+  // first block's loads are settled before the loop so the loop-head waits
+  // follow the steady-state order only.
   const uint8_t *reg = region_of(blk0);
   load_k(reg);
+  load_meta(reg, km, vm);
   load_v(reg);
+#pragma unroll
+  for (int p = 0; p < NP; ++p) settle(kr[p]);
+#pragma unroll
+  for (int tg = 0; tg < 2; ++tg)
+#pragma unroll
+    for (int i = 0; i < 2 * DPL; ++i) settle(vr[tg][i]);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    settle(km[g]);
+    settle(vm[g]);
+  }
 
   for (int blk = blk0; blk < blk1; ++blk) {
     const int tbase = blk << 6;
     const bool has_next = blk + 1 < blk1;
     const uint8_t *nreg = has_next ? region_of(blk + 1) : reg;
-    uint32_t km[G], vm[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      km[g] = *reinterpret_cast<const uint32_t *>(reg + km_offset(D) + ((lane * G + g) << 2));
-      vm[g] = *reinterpret_cast<const uint32_t *>(reg + vm_offset(D, G) + ((lane * G + g) << 2));
-    }
 
     // ---- scores: this lane's token against every query row; the query
     // pair of each dot comes from lane (pair & 15) of the lane's 16-lane row
@@ -211,18 +251,30 @@ __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
         for (int i = 0; i < 8; ++i) kp[i] = (kp[i] + m1024) * ks2 + kz2;
       }
       const int g = MODE == MODE_AFFINE ? p / PPG : 0;
+      // the last piece of a scale group finishes accg[.][g]
+      const bool tail = MODE == MODE_AFFINE ? (p + 1) % PPG == 0 : p == NP - 1;
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
-        if (p & 1)
-          dot8_bcast<8>(accg[r][g], qv[r][p >> 1], kp);
-        else
-          dot8_bcast<0>(accg[r][g], qv[r][p >> 1], kp);
+        if (p & 1) {
+          if (tail)
+            dot8_bcast<8, true>(accg[r][g], qv[r][p >> 1], kp);
+          else
+            dot8_bcast<8, false>(accg[r][g], qv[r][p >> 1], kp);
+        } else {
+          if (tail)
+            dot8_bcast<0, true>(accg[r][g], qv[r][p >> 1], kp);
+          else
+            dot8_bcast<0, false>(accg[r][g], qv[r][p >> 1], kp);
+        }
       }
     }
-    // K registers are free: fetch the next block.  Unconditional on purpose
-    // (the last block re-reads itself from L2): a conditional load would keep
-    // the consumed registers alive through the loop header.
+    // K registers are free: fetch the next block's K bytes and metadata.
+    // Unconditional on purpose (the last block re-reads itself from L2): a
+    // conditional load would keep the consumed registers alive through the
+    // loop header.
     load_k(nreg);
+    uint32_t km_next[G], vm_next[G];
+    load_meta(nreg, km_next, vm_next);
 
     float s[NR];
 #pragma unroll
@@ -351,6 +403,11 @@ __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
       }
     }
     load_v(nreg);  // V registers are free: fetch the next block
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      km[g] = km_next[g];
+      vm[g] = vm_next[g];
+    }
     reg = nreg;
     __syncthreads();
   }
@@ -391,53 +448,6 @@ __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
       a.ws_ml[pi * 2 + 1] = lsum[r];
     }
   }
-  // publish the partials; the last split of this (sequence, KV head) merges
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __syncthreads();
-  if (lane == 0) {
-    const uint32_t done = __hip_atomic_fetch_add(a.count + (int64_t)b * a.Hkv + hk, 1u, __ATOMIC_ACQ_REL,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    last_lds = done == (uint32_t)(n_splits - 1);
-  }
-  __syncthreads();
-  if (!last_lds) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  const int64_t pbase = part_index(a, b, hk, 0, 0);
-#pragma unroll 1
-  for (int r = 0; r < NR; ++r) {
-    float M = -INFINITY;
-    for (int sp = lane; sp < n_splits; sp += 64) M = fmaxf(M, a.ws_ml[(pbase + (int64_t)sp * NR + r) * 2]);
-    M = wave_allmax(M);
-    float Lsum = 0.0f, oacc[DPL];
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) oacc[e] = 0.0f;
-    for (int s0 = 0; s0 < n_splits; s0 += MAXS) {
-      const int cnt = min(MAXS, n_splits - s0);
-      float lpart = 0.0f;
-      for (int i = lane; i < cnt; i += 64) {
-        const int64_t pi = pbase + (int64_t)(s0 + i) * NR + r;
-        const float m = a.ws_ml[pi * 2];
-        const float w = m == -INFINITY ? 0.0f : fast_exp2(m - M);
-        e_lds[i] = w;
-        lpart += w * a.ws_ml[pi * 2 + 1];
-      }
-      Lsum += wave_allsum(lpart);
-      __syncthreads();
-#pragma unroll 4
-      for (int i = 0; i < cnt; ++i) {
-        const float w = e_lds[i];
-        const int64_t pi = pbase + (int64_t)(s0 + i) * NR + r;
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) oacc[e] += w * a.ws_o[pi * D + DPL * lane + e];
-      }
-      __syncthreads();
-    }
-    const float inv = (M == -INFINITY || !(Lsum > 0.0f)) ? 0.0f : 1.0f / Lsum;
-    const int64_t ob = out_row_base(a, b, hk, r, D);
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) store_out(a.out, ob + DPL * lane + e, oacc[e] * inv, a.out_dtype);
-  }
-  if (lane == 0) a.count[(int64_t)b * a.Hkv + hk] = 0u;
 }
 
 template <int D, int MODE, int NR>
@@ -465,6 +475,8 @@ static hipError_t launch_valu_nr(const AttnArgs &args, int NR, int B, dim3 grid,
 
 hipError_t launch_attn_valu(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
                             hipStream_t st) {
+  // one VGPR of block-table entries per split
+  if (p.split_blocks < 1 || p.split_blocks > 64) return hipErrorInvalidValue;
   const AttnArgs args = make_attn_args(g, layer, a, p);
   const dim3 grid((unsigned)p.max_splits, (unsigned)g.Hkv, (unsigned)a.B);
   switch (g.D) {

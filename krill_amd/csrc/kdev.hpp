@@ -147,29 +147,52 @@ __device__ __forceinline__ float dpp_f32(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(unsigned, v), CTRL, 0xf, 0xf,
                                                                false));
 }
+// The row swaps are issued as inline asm with both registers as in/out
+// operands: through __builtin_amdgcn_permlane{16,32}_swap this compiler
+// reads only the first register after the swap and uses it for both
+// results.  With a == b on entry, v_permlane16_swap leaves rows {0,0,2,2} of
+// the value in `a` and rows {1,1,3,3} in `b`; v_permlane32_swap leaves rows
+// {0,1,0,1} and {2,3,2,3}.  The s_nop covers the VALU-write -> permlane-read
+// hazard of the copy the compiler makes to split a from b.
+__device__ __forceinline__ void row_swap16(float &a, float &b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void row_swap32(float &a, float &b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float swap16_sum(float v) {
+  float a = v, b = v;
+  row_swap16(a, b);
+  return a + b;
+}
+__device__ __forceinline__ float swap32_sum(float v) {
+  float a = v, b = v;
+  row_swap32(a, b);
+  return a + b;
+}
+__device__ __forceinline__ float swap16_max(float v) {
+  float a = v, b = v;
+  row_swap16(a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float swap32_max(float v) {
+  float a = v, b = v;
+  row_swap32(a, b);
+  return fmaxf(a, b);
+}
 __device__ __forceinline__ float wave_allsum(float v) {
   v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
   v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
   v += dpp_f32<0x124>(v);  // row_ror:4
   v += dpp_f32<0x128>(v);  // row_ror:8
-  const unsigned u = __builtin_bit_cast(unsigned, v);
-  auto s16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  v = __builtin_bit_cast(float, s16[0]) + __builtin_bit_cast(float, s16[1]);
-  const unsigned w = __builtin_bit_cast(unsigned, v);
-  auto s32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
-  return __builtin_bit_cast(float, s32[0]) + __builtin_bit_cast(float, s32[1]);
+  return swap32_sum(swap16_sum(v));
 }
 __device__ __forceinline__ float wave_allmax(float v) {
   v = fmaxf(v, dpp_f32<0xB1>(v));
   v = fmaxf(v, dpp_f32<0x4E>(v));
   v = fmaxf(v, dpp_f32<0x124>(v));
   v = fmaxf(v, dpp_f32<0x128>(v));
-  const unsigned u = __builtin_bit_cast(unsigned, v);
-  auto s16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  v = fmaxf(__builtin_bit_cast(float, s16[0]), __builtin_bit_cast(float, s16[1]));
-  const unsigned w = __builtin_bit_cast(unsigned, v);
-  auto s32 = __builtin_amdgcn_permlane32_swap(w, w, false, false);
-  return fmaxf(__builtin_bit_cast(float, s32[0]), __builtin_bit_cast(float, s32[1]));
+  return swap32_max(swap16_max(v));
 }
 
 // A zero the compiler cannot see through: loads addressed with it stay below
@@ -183,8 +206,23 @@ __device__ __forceinline__ int opaque_zero() {
 // Register fence: `x` is treated as rewritten after `after` is available, so
 // work on `x` cannot be scheduled ahead of the work that produced `after`
 // (bounds register live ranges the scheduler would otherwise stretch).
+// The 16 bytes go in as one 128-bit register tuple: split into four 32-bit
+// operands, the register allocator may give the components of a loop-carried
+// load different registers on the two sides of the back edge, and the copies
+// it then adds on the latch must wait for the load.
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void order_after(uint4 &x, float after) {
-  asm volatile("; order %0 %1 %2 %3 after %4" : "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w) : "v"(after));
+  u32x4_t v = __builtin_bit_cast(u32x4_t, x);
+  asm volatile("; order %0 after %1" : "+v"(v) : "v"(after));
+  x = __builtin_bit_cast(uint4, v);
 }
+// Register settle: `x` counts as read and rewritten here, so a load into it
+// completes before this point and later waits no longer track it.
+__device__ __forceinline__ void settle(uint4 &x) {
+  u32x4_t v = __builtin_bit_cast(u32x4_t, x);
+  asm volatile("; settle %0" : "+v"(v));
+  x = __builtin_bit_cast(uint4, v);
+}
+__device__ __forceinline__ void settle(uint32_t &x) { asm volatile("; settle %0" : "+v"(x)); }
 
 }  // namespace krill

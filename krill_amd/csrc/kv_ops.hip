@@ -330,31 +330,49 @@ __global__ __launch_bounds__(64) void k_attn_merge(const float *__restrict__ ws_
                                                    int32_t Hkv, int32_t NR, int32_t R, int32_t Lq, int32_t Hq,
                                                    int32_t D, int32_t split_blocks, int32_t max_splits, void *out,
                                                    int32_t out_dtype) {
+  __shared__ float w_lds[64];
   const int r = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x;
   const int len = lens[b];
   const int nb = min(min((len + 63) >> 6, max_blocks), max_splits * split_blocks);
   const int n_splits = (nb + split_blocks - 1) / split_blocks;
-  if (n_splits == 1) return;
+  if (n_splits <= 1) return;
   const int hq = hk * R + r % R, j = r / R;
   const int64_t obase = (((int64_t)b * Hq + hq) * Lq + j) * D;
   const int64_t pbase = ((int64_t)b * Hkv + hk) * max_splits;
+  const float2 *ml2 = reinterpret_cast<const float2 *>(ws_ml);
+  // lane s reads split s0 + s: all (m, l) loads of a 64-split chunk are in
+  // flight together
   float M = -INFINITY;
-  for (int s = 0; s < n_splits; ++s) M = fmaxf(M, ws_ml[((pbase + s) * NR + r) * 2]);
-  float Lsum = 0.0f;
-  for (int s = 0; s < n_splits; ++s) {
-    const float m = ws_ml[((pbase + s) * NR + r) * 2];
-    Lsum += m == -INFINITY ? 0.0f : ws_ml[((pbase + s) * NR + r) * 2 + 1] * fast_exp2(m - M);
-  }
-  const float inv = (M == -INFINITY || !(Lsum > 0.0f)) ? 0.0f : 1.0f / Lsum;
-  for (int d = lane; d < D; d += 64) {
-    float acc = 0.0f;
-    for (int s = 0; s < n_splits; ++s) {
-      const float m = ws_ml[((pbase + s) * NR + r) * 2];
-      if (m != -INFINITY) acc += ws_o[((pbase + s) * NR + r) * (int64_t)D + d] * fast_exp2(m - M);
+  for (int s0 = 0; s0 < n_splits; s0 += 64)
+    if (s0 + lane < n_splits) M = fmaxf(M, ml2[(pbase + s0 + lane) * NR + r].x);
+  M = wave_allmax(M);
+  float lpart = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // d = lane + 64 e, D <= 256
+  for (int s0 = 0; s0 < n_splits; s0 += 64) {
+    const int cnt = min(64, n_splits - s0);
+    float w = 0.0f;
+    if (lane < cnt) {
+      const float2 ml = ml2[(pbase + s0 + lane) * NR + r];
+      w = ml.x == -INFINITY ? 0.0f : fast_exp2(ml.x - M);
+      lpart += w * ml.y;
     }
-    store_out(out, obase + d, acc * inv, out_dtype);
+    w_lds[lane] = w;
+    __syncthreads();
+#pragma unroll 8
+    for (int i = 0; i < cnt; ++i) {
+      const float wi = w_lds[i];
+      const float *op = ws_o + ((pbase + s0 + i) * NR + r) * (int64_t)D;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (64 * e < D) acc[e] += wi * op[lane + 64 * e];
+    }
+    __syncthreads();
   }
+  const float Lsum = wave_allsum(lpart);
+  const float inv = (M == -INFINITY || !(Lsum > 0.0f)) ? 0.0f : 1.0f / Lsum;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (64 * e < D) store_out(out, obase + lane + 64 * e, acc[e] * inv, out_dtype);
 }
 
 // ---------------------------------------------------------------------------
@@ -504,6 +522,9 @@ int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq,
     const int64_t units = (int64_t)B * g.Hkv * p.row_groups;
     sb = (int32_t)std::max<int64_t>(2, ((int64_t)nb_max * units + 4095) / 4096);
   }
+  // The VALU kernel holds a split's block-table entries in one VGPR (one
+  // entry per lane), so a split covers at most 64 blocks.
+  if (!p.use_mfma) sb = std::min(sb, 64);
   sb = std::min(sb, nb_max);
   p.split_blocks = sb;
   p.max_splits = (nb_max + sb - 1) / sb;
@@ -512,8 +533,8 @@ int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq,
   return 0;
 }
 
-// Separate split merge, used after the MFMA kernel (the VALU kernel merges
-// inside its last split).
+// Split merge, launched after either attention kernel when some sequence
+// spans more than one split.
 hipError_t launch_attn_merge(const PoolGeometry &g, const AttnLaunch &a, const AttnPlan &p, hipStream_t st) {
   if (p.max_splits <= 1 || a.B == 0) return hipSuccess;
   const WsLayout w = ws_layout(a.B, g.Hkv, p.max_splits, p.NR, g.D, g.G);
@@ -529,8 +550,7 @@ hipError_t launch_attn_merge(const PoolGeometry &g, const AttnLaunch &a, const A
 hipError_t launch_attention(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
                             hipStream_t st) {
   if (a.B == 0) return hipSuccess;
-  if (!p.use_mfma) return launch_attn_valu(g, layer, a, p, st);
-  hipError_t e = launch_attn_mfma(g, layer, a, p, st);
+  hipError_t e = p.use_mfma ? launch_attn_mfma(g, layer, a, p, st) : launch_attn_valu(g, layer, a, p, st);
   if (e != hipSuccess) return e;
   return launch_attn_merge(g, a, p, st);
 }
