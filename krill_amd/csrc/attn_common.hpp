@@ -7,24 +7,23 @@
 
 namespace krill {
 
-// Workspace carve-up, 256-byte aligned pieces:
-//   o      float [B][Hkv][max_splits][NR][D]   unnormalised split outputs
-//   ml     float [B][Hkv][max_splits][NR][2]   (running max m in log2 units, sum l)
-//   q16    fp16  [B][Hkv][NR][D]               queries rounded to fp16 (VALU path)
-//   qsum   float [B][Hkv][NR][G]               per scale group sums of q16
+// Workspace: `slots` partial results of NR query rows each, 256-byte aligned
+// pieces:
+//   o      float [slots][NR][D]   unnormalised partial outputs
+//   ml     float [slots][NR][2]   (running max m in log2 units, sum l)
+// MFMA path: slot = (b * Hkv + hk) * max_splits + split.
+// VALU path: slot = hk * (waves + B) + wave + b (see k_attn_valu).
 struct WsLayout {
-  size_t o, ml, q16, qsum, total;
+  size_t o, ml, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-inline WsLayout ws_layout(int64_t B, int64_t Hkv, int64_t max_splits, int64_t NR, int64_t D, int64_t G) {
+inline WsLayout ws_layout(int64_t slots, int64_t NR, int64_t D) {
   WsLayout w;
   w.o = 0;
-  w.ml = align256(w.o + (size_t)(B * Hkv * max_splits * NR * D) * sizeof(float));
-  w.q16 = align256(w.ml + (size_t)(B * Hkv * max_splits * NR * 2) * sizeof(float));
-  w.qsum = align256(w.q16 + (size_t)(B * Hkv * NR * D) * sizeof(uint16_t));
-  w.total = align256(w.qsum + (size_t)(B * Hkv * NR * G) * sizeof(float));
+  w.ml = align256(w.o + (size_t)(slots * NR * D) * sizeof(float));
+  w.total = align256(w.ml + (size_t)(slots * NR * 2) * sizeof(float));
   return w;
 }
 
@@ -34,14 +33,14 @@ struct AttnArgs {
   int32_t q_dtype;
   const int32_t *tables;
   const int32_t *lens;
-  int32_t max_blocks;
+  int32_t B, max_blocks;
+  int32_t nb_cap;  // blocks per sequence the plan covers (from max_seq_len)
   int32_t Hkv, R, Lq, Hq, NR;
   float scale_log2;  // softmax scale * log2(e)
   int32_t split_blocks, max_splits;
+  int32_t waves;  // VALU path: waves per KV head
   float *ws_o;
   float *ws_ml;
-  uint16_t *q16;
-  float *qsum;
   void *out;  // [B][Hq][Lq][D]
   int32_t out_dtype;
 };
@@ -56,7 +55,9 @@ inline AttnArgs make_attn_args(const PoolGeometry &g, int32_t layer, const AttnL
   r.q_dtype = g.in_dtype;
   r.tables = a.tables;
   r.lens = a.lens;
+  r.B = a.B;
   r.max_blocks = a.max_blocks;
+  r.nb_cap = p.nb_cap;
   r.Hkv = g.Hkv;
   r.R = a.Hq / g.Hkv;
   r.Lq = a.Lq;
@@ -65,25 +66,24 @@ inline AttnArgs make_attn_args(const PoolGeometry &g, int32_t layer, const AttnL
   r.scale_log2 = a.scale * 1.4426950408889634f;
   r.split_blocks = p.split_blocks;
   r.max_splits = p.max_splits;
-  const WsLayout w = ws_layout(a.B, g.Hkv, p.max_splits, p.NR, g.D, g.G);
+  r.waves = p.waves;
+  const WsLayout w = ws_layout(p.slots, p.NR, g.D);
   uint8_t *base = static_cast<uint8_t *>(a.ws);
   r.ws_o = reinterpret_cast<float *>(base + w.o);
   r.ws_ml = reinterpret_cast<float *>(base + w.ml);
-  r.q16 = reinterpret_cast<uint16_t *>(base + w.q16);
-  r.qsum = reinterpret_cast<float *>(base + w.qsum);
   r.out = a.out;
   r.out_dtype = a.out_dtype;
   return r;
 }
 
-// Blocks of sequence b that the kernels may touch: bounded by the table width
-// and by the split grid sized from the host's max_seq_len, so a length beyond
-// either bound can never index past the table or the workspace.
+// Blocks of a sequence of length `len` that the kernels may touch: bounded by
+// the table width and by the plan's per-sequence cap (from the host's
+// max_seq_len), so a length beyond either bound can never index past the
+// table or the workspace.
 __device__ __forceinline__ int seq_blocks(const AttnArgs &a, int len) {
-  int nb = (len + 63) >> 6;
+  int nb = len > 0 ? (len + 63) >> 6 : 0;
   nb = nb < a.max_blocks ? nb : a.max_blocks;
-  const int cap = a.max_splits * a.split_blocks;
-  return nb < cap ? nb : cap;
+  return nb < a.nb_cap ? nb : a.nb_cap;
 }
 
 __device__ __forceinline__ float load_q(const uint16_t *p, int dt) {
@@ -98,6 +98,40 @@ __device__ __forceinline__ int64_t out_row_base(const AttnArgs &a, int b, int hk
 }
 __device__ __forceinline__ int64_t part_index(const AttnArgs &a, int b, int hk, int split, int r) {
   return (((int64_t)b * a.Hkv + hk) * a.max_splits + split) * a.NR + r;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(v, d, 64);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+
+// Flat block order of the VALU path: the blocks of sequences 0, 1, .., B-1
+// one after another.  Finds the sequence holding flat block `i` (the first
+// one whose blocks reach past i) and the flat index of its first block;
+// returns false when i lies beyond the last block.  Uniform across the wave.
+__device__ __forceinline__ bool flat_locate(const AttnArgs &a, int i, int &b_out, int &start_out) {
+  const int lane = threadIdx.x & 63;
+  int carry = 0;
+  for (int c0 = 0; c0 < a.B; c0 += 64) {
+    const int bb = c0 + lane;
+    const int nbv = bb < a.B ? seq_blocks(a, a.lens[bb]) : 0;
+    const int incl = wave_incl_scan(nbv) + carry;
+    const unsigned long long m = __ballot(bb < a.B && incl > i);
+    if (m) {
+      const int l = __builtin_ctzll(m);
+      b_out = c0 + l;
+      start_out = __builtin_amdgcn_readlane(incl - nbv, l);
+      return true;
+    }
+    carry = __builtin_amdgcn_readlane(incl, 63);
+  }
+  return false;
 }
 
 }  // namespace krill

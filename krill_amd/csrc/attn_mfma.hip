@@ -263,7 +263,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a, int32_t row_groups
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
         const int d = 16 * dt + n;
-        const uint2 vb = *reinterpret_cast<const uint2 *>(reg + v_offset(D) + ((tg * D + d) << 5) + 8 * q4);
+        const uint2 vb = *reinterpret_cast<const uint2 *>(reg + v_pos_byte(D, tg, d, 8 * q4));
         half8_t A;
         if constexpr (MODE == MODE_REF) {
           half2_t p0 = (bytes01_plus1024(vb.x) + m1024) * sp[0] + zp[0];

@@ -8,15 +8,19 @@
 // Sources/KrillEngine/BatchedDecode.swift:277-287 replaced by per-row lengths
 // (the -10000 mask underflows those weights to exactly zero, :22-28).
 //
-// Two launches: a prep kernel rounds the queries to fp16 once per
-// (sequence, KV head) and sums them per scale group; the main kernel runs one
-// wave64 per (split of 64-token blocks, KV head, sequence).  Per block:
+// Work split: per KV head, the 64-token blocks of all sequences are laid end
+// to end (flat order) and each wave64 takes the same number of consecutive
+// blocks, crossing sequence boundaries, so every wave streams the same bytes
+// whatever the length mix.  A wave processes its range one sequence segment
+// at a time; for each it rounds the query rows to fp16 pairs held in VGPRs
+// (each 16-lane DPP row holds the whole query) and, in affine mode, sums
+// them per 64-d group.  Per block:
 //  * scores, one token per lane: the lane reads its token's K row (D bytes,
 //    16-byte loads that are contiguous across lanes in the d-chunk-major
 //    layout), turns byte pairs into fp16 (1024 + u) with one v_perm_b32, and
-//    accumulates v_dot2c_f32_f16 against fp16 query pairs that are
-//    wave-uniform and therefore come from scalar registers (scalar loads of
-//    the prep output).  Affine mode uses linearity per 64-group:
+//    accumulates v_dot2c_f32_f16 whose query operand is broadcast from the
+//    right lane of the row by DPP row_newbcast.  Affine mode uses linearity
+//    per 64-group:
 //      q.k = s * (q.(1024 + u) - 1024 * sum q) + z * sum q,
 //    so no element is dequantised.  Reference row mode dequantises exactly
 //    (f16(f16(u*s) + z), QuantizedKVCache.swift:200-204) before the dot.
@@ -25,22 +29,21 @@
 //    running max by more than 8 (a wave vote), so weights stay below 2^8;
 //  * weights w = p * s_v (fp16) go to LDS in V storage order; each lane
 //    then owns D/64 V^T rows (d values), loaded as contiguous 16-byte pieces,
-//    and reduces token pairs with v_dot2c_f32_f16.  The V zero points and the
-//    1024 offset collapse into one per-(row, group) term.
+//    and reduces token pairs with v_dot2c_f32_f16, 8 tokens at a time.  The
+//    V zero points and the 1024 offset collapse into one per-(row, group)
+//    term.
 //  * the next block's K and V are loaded as soon as the current block's
 //    registers are consumed, so loads overlap the other phase's math.
-// A sequence with one split writes the output directly; otherwise every
-// split writes (m, l, o) to the workspace and k_attn_merge combines them in a
-// second launch.  (Merging inside the last split to finish would need an
-// agent-scope release/acquire per split, which on this multi-XCD part is a
-// whole-L2 writeback and invalidate per wave.)
+// A sequence that lies inside one wave's range is written directly;
+// otherwise each wave writes its segment's (m, l, o) to the workspace and
+// k_attn_merge_flat combines them in a second launch.  (Merging inside the
+// last wave to finish would need an agent-scope release/acquire per wave,
+// which on this multi-XCD part is a whole-L2 writeback and invalidate.)
 #include <hip/hip_runtime.h>
 
 #include "attn_common.hpp"
 
 namespace krill {
-
-typedef __attribute__((address_space(4))) const float scalar_f32;
 
 // acc += sum_i k[i] . q_(OFF + i), i < 8, where q_n is lane n of this lane's
 // 16-lane row of `q` (v_dot2c_f32_f16 with a DPP row_newbcast source).  The
@@ -74,35 +77,44 @@ __device__ __forceinline__ void dot8_bcast(float &acc, uint32_t q, const half2_t
 #undef KRILL_DOT8_BODY
 #undef KRILL_DOT8_OPERANDS
 
-// fp16 queries and their per-group sums.
-template <int D, int NR, int G>
-__global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
-  const int hk = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  const int64_t row0 = ((int64_t)b * a.Hkv + hk) * NR;
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    const int hq = hk * a.R + r % a.R, j = r / a.R;
-    const uint16_t *qp = a.q + (((int64_t)b * a.Hq + hq) * a.Lq + j) * D;
-    float gs[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) gs[g] = 0.0f;
-#pragma unroll
-    for (int k = 0; k < D / 64; ++k) {
-      const int d = lane + 64 * k;
-      const _Float16 h = (_Float16)load_q(qp + d, a.q_dtype);
-      a.q16[(row0 + r) * D + d] = __builtin_bit_cast(uint16_t, h);
-      gs[(64 * k) / (D / G)] += (float)h;
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float t = wave_allsum(gs[g]);
-      if (lane == 0) a.qsum[(row0 + r) * G + g] = t;
-    }
+// Block region of the pool as a buffer resource: loads past `bytes` return
+// zero without touching memory, so the prefetch after a wave's last block is
+// free (bytes = 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const uint8_t *p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p), (short)0, bytes, 0x00020000);
+}
+// Streaming (non-temporal) loads: each block byte is read once per launch.
+__device__ __forceinline__ uint4 ld_stream16(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+}
+// N consecutive 32-bit words (N = 1, 2 or 4) in one load.
+template <int N>
+__device__ __forceinline__ void ld_stream_words(__amdgpu_buffer_rsrc_t r, int off, uint32_t (&w)[N]) {
+  if constexpr (N == 1) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 2);
+  } else if constexpr (N == 2) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 2);
+    w[0] = v[0];
+    w[1] = v[1];
+  } else {
+    static_assert(N == 4, "1, 2 or 4 words");
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
+    w[0] = v[0];
+    w[1] = v[1];
+    w[2] = v[2];
+    w[3] = v[3];
   }
 }
 
+// Waves per SIMD the register budget aims for: 3 (168 VGPRs) where the
+// kernel fits without spilling, else 2.
+template <int D, int NR>
+constexpr int valu_waves_per_simd() {
+  return D <= 64 || (D == 128 && NR <= 5) ? 3 : 2;
+}
+
 template <int D, int NR, int MODE>
-__global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
+__global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_valu(AttnArgs a) {
   constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
   constexpr int NP = D / 16;   // 16-byte K pieces per token row
   constexpr int PPG = NP / G;  // pieces per scale group
@@ -112,87 +124,61 @@ __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t sz_lds[2 * 64];
 
   const int lane = threadIdx.x;
-  const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
-  const int len = a.lens[b];
-  const int nb = seq_blocks(a, len);
-  if (nb == 0) {
-    if (split == 0) {
-#pragma unroll
-      for (int r = 0; r < NR; ++r)
-        for (int d = lane; d < D; d += 64) store_out(a.out, out_row_base(a, b, hk, r, D) + d, 0.0f, a.out_dtype);
-    }
-    return;
-  }
-  const int blk0 = split * a.split_blocks;
-  if (blk0 >= nb) return;
-  const int blk1 = min(nb, blk0 + a.split_blocks);
-  const int n_splits = (nb + a.split_blocks - 1) / a.split_blocks;
+  const int wv = blockIdx.x, hk = blockIdx.y;
+  // This wave's blocks: flat indices [i0, iend) of the concatenated block
+  // lists of all sequences (so every wave streams the same number of bytes).
+  const int PW = a.split_blocks;
+  const int i0 = wv * PW, iend = i0 + PW;
+  int b, s;  // sequence holding block i0 and the flat index of its first block
+  if (!flat_locate(a, i0, b, s)) return;
 
-  const int64_t qrow = ((int64_t)b * a.Hkv + hk) * NR;
-  // fp16 query pairs: qv[r][c] holds pair 16*c + (lane & 15) of row r, so
-  // every 16-lane row carries the whole query (one VGPR per 32 d)
-  uint32_t qv[NR][D / 32];
+  // Physical block ids of flat blocks i0 .. iend-1 (at most 64): lane j holds
+  // the entry of block i0 + j, read back with v_readlane, so no table load
+  // sits between a prefetch and its use (a load there would have to drain the
+  // prefetch before its value could move to a scalar register).
+  int tab = 0, iend_eff = iend;
   {
-    const uint32_t *q16 = reinterpret_cast<const uint32_t *>(a.q16 + qrow * D);
-#pragma unroll
-    for (int r = 0; r < NR; ++r)
-#pragma unroll
-      for (int c = 0; c < D / 32; ++c) qv[r][c] = q16[r * (D / 2) + 16 * c + (lane & 15)];
+    const int f = i0 + lane;
+    int bs = b, ss = s;
+    while (bs < a.B && ss < iend) {
+      const int nbs = seq_blocks(a, a.lens[bs]);
+      if (lane < PW && f >= ss && f < ss + nbs) {
+        const int phys = a.tables[(int64_t)bs * a.max_blocks + (f - ss)];
+        tab = (unsigned)phys < (unsigned)a.lv.num_blocks ? phys : 0;
+      }
+      ss += nbs;
+      ++bs;
+    }
+    if (ss < iend) iend_eff = ss;  // the last sequence ends inside this range
   }
-  scalar_f32 *qs = (scalar_f32 *)(a.qsum + qrow * G);
-  int lim[NR];
-#pragma unroll
-  for (int r = 0; r < NR; ++r) lim[r] = len - a.Lq + r / a.R + 1;
+  auto rsrc_of = [&](int i) -> __amdgpu_buffer_rsrc_t {
+    const bool ok = i < iend_eff;
+    const int phys = __builtin_amdgcn_readlane(tab, ok ? i - i0 : 0);
+    return block_rsrc(head_region(a.lv, phys, hk), ok ? a.lv.head_bytes : 0);
+  };
+
   const int gl = MODE == MODE_AFFINE ? (DPL * lane) / 64 : 0;  // scale group of this lane's V rows
   const int pos = ((lane >> 5) << 5) + vpos(lane & 31);        // this lane's token in V order
-
-  float m_run[NR], l_part[NR], c_part[NR][G], acc[NR][DPL];
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    m_run[r] = -INFINITY;
-    l_part[r] = 0.0f;
-#pragma unroll
-    for (int g = 0; g < G; ++g) c_part[r][g] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) acc[r][e] = 0.0f;
-  }
   const half2_t m1024 = half2_t{(_Float16)-1024.0f, (_Float16)-1024.0f};
 
-  // Physical block ids of this split (at most 64 blocks): lane i holds the
-  // entry of block blk0 + i, read back with v_readlane, so no table load sits
-  // between a prefetch and its use (a load there would have to drain the
-  // prefetch before its value could move to a scalar register).
-  int tab;
-  {
-    const int i = blk0 + lane;
-    const int phys = i < blk1 ? a.tables[(int64_t)b * a.max_blocks + i] : 0;
-    tab = (unsigned)phys < (unsigned)a.lv.num_blocks ? phys : 0;
-  }
-  auto region_of = [&](int blk) -> const uint8_t * {
-    return head_region(a.lv, __builtin_amdgcn_readlane(tab, blk - blk0), hk);
-  };
   uint4 kr[NP];
   uint4 vr[2][2 * DPL];
-  auto load_k = [&](const uint8_t *reg) {
+  auto load_k = [&](__amdgpu_buffer_rsrc_t r) {
 #pragma unroll
-    for (int p = 0; p < NP; ++p) kr[p] = *reinterpret_cast<const uint4 *>(reg + k_byte(lane, 16 * p));
+    for (int p = 0; p < NP; ++p) kr[p] = ld_stream16(r, k_byte(lane, 16 * p));
   };
-  auto load_v = [&](const uint8_t *reg) {
+  auto load_v = [&](__amdgpu_buffer_rsrc_t r) {
 #pragma unroll
     for (int tg = 0; tg < 2; ++tg)
 #pragma unroll
       for (int i = 0; i < 2 * DPL; ++i)
-        vr[tg][i] = *reinterpret_cast<const uint4 *>(reg + v_offset(D) + ((tg * D + DPL * lane) << 5) + 16 * i);
+        vr[tg][i] = ld_stream16(r, v_offset(D) + tg * 32 * D + ((i * 64 + lane) << 4));  // d = DPL*lane + i/2, half i%2
   };
-
   // this lane's token's (scale, zero) pairs, K and V
   uint32_t km[G], vm[G];
-  auto load_meta = [&](const uint8_t *reg, uint32_t (&kmo)[G], uint32_t (&vmo)[G]) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      kmo[g] = *reinterpret_cast<const uint32_t *>(reg + km_offset(D) + ((lane * G + g) << 2));
-      vmo[g] = *reinterpret_cast<const uint32_t *>(reg + vm_offset(D, G) + ((lane * G + g) << 2));
-    }
+  auto load_meta = [&](__amdgpu_buffer_rsrc_t r, uint32_t (&kmo)[G], uint32_t (&vmo)[G]) {
+    ld_stream_words<G>(r, km_offset(D) + lane * 4 * G, kmo);
+    ld_stream_words<G>(r, vm_offset(D, G) + lane * 4 * G, vmo);
   };
 
   // Loads of block n+1 are issued in a fixed order inside the loop: K bytes
@@ -200,10 +186,12 @@ __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
   // registers are; waits on a load never cover a younger prefetch.  The
   // first block's loads are settled before the loop so the loop-head waits
   // follow the steady-state order only.
-  const uint8_t *reg = region_of(blk0);
-  load_k(reg);
-  load_meta(reg, km, vm);
-  load_v(reg);
+  {
+    const __amdgpu_buffer_rsrc_t r0 = rsrc_of(i0);
+    load_k(r0);
+    load_meta(r0, km, vm);
+    load_v(r0);
+  }
 #pragma unroll
   for (int p = 0; p < NP; ++p) settle(kr[p]);
 #pragma unroll
@@ -216,10 +204,61 @@ __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
     settle(vm[g]);
   }
 
-  for (int blk = blk0; blk < blk1; ++blk) {
-    const int tbase = blk << 6;
-    const bool has_next = blk + 1 < blk1;
-    const uint8_t *nreg = has_next ? region_of(blk + 1) : reg;
+  int i = i0;
+  // one pass per sequence segment [max(s, i0), min(s + nb, iend))
+  while (true) {
+    const int len = a.lens[b];
+    const int e = s + seq_blocks(a, len);
+    const int seg_start = i, seg_end = min(e, iend_eff);
+
+    // fp16 query pairs: qv[r][c] holds pair 16*c + (lane & 15) of row r, so
+    // every 16-lane row carries the whole query (one VGPR per 32 d).  Affine
+    // mode also needs the sum of each 64-d group of the fp16 query (pairs
+    // 32g .. 32g+31 = columns 2g and 2g+1), reduced inside each 16-lane row.
+    uint32_t qv[NR][D / 32];
+    float qs[NR][G];
+    const bool q_bf16 = a.q_dtype == DT_BF16;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int hq = hk * a.R + r % a.R, j = r / a.R;
+      const uint32_t *qp = reinterpret_cast<const uint32_t *>(a.q + (((int64_t)b * a.Hq + hq) * a.Lq + j) * D);
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) {
+        const uint32_t w = qp[16 * c + (lane & 15)];
+        // bf16 pairs are widened to fp32 and rounded to fp16; fp16 pairs pass through
+        const half2_t hb = half2_t{(_Float16)__builtin_bit_cast(float, w << 16),
+                                   (_Float16)__builtin_bit_cast(float, w & 0xffff0000u)};
+        qv[r][c] = q_bf16 ? h2_as_u32(hb) : w;
+      }
+      if constexpr (MODE == MODE_AFFINE) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const half2_t p0 = u32_as_h2(qv[r][2 * g]), p1 = u32_as_h2(qv[r][2 * g + 1]);
+          qs[r][g] = uniform_f32(row_allsum(((float)p0.x + (float)p0.y) + ((float)p1.x + (float)p1.y)));
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g) qs[r][g] = 0.0f;
+      }
+    }
+    int lim[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) lim[r] = len - a.Lq + r / a.R + 1;
+
+    float m_run[NR], l_part[NR], c_part[NR][G], acc[NR][DPL];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      m_run[r] = -INFINITY;
+      l_part[r] = 0.0f;
+#pragma unroll
+      for (int g = 0; g < G; ++g) c_part[r][g] = 0.0f;
+#pragma unroll
+      for (int e2 = 0; e2 < DPL; ++e2) acc[r][e2] = 0.0f;
+    }
+
+  for (; i < seg_end; ++i) {
+    const int tbase = (i - s) << 6;
+    const __amdgpu_buffer_rsrc_t nrs = rsrc_of(i + 1);
 
     // ---- scores: this lane's token against every query row; the query
     // pair of each dot comes from lane (pair & 15) of the lane's 16-lane row
@@ -269,12 +308,13 @@ __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
       }
     }
     // K registers are free: fetch the next block's K bytes and metadata.
-    // Unconditional on purpose (the last block re-reads itself from L2): a
+    // Unconditional on purpose (after the wave's last block the resource is
+    // empty and the loads return zeros without a memory access): a
     // conditional load would keep the consumed registers alive through the
     // loop header.
-    load_k(nreg);
+    load_k(nrs);
     uint32_t km_next[G], vm_next[G];
-    load_meta(nreg, km_next, vm_next);
+    load_meta(nrs, km_next, vm_next);
 
     float s[NR];
 #pragma unroll
@@ -286,7 +326,7 @@ __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
         for (int g = 0; g < G; ++g) {
           const float kss = f16_bits_to_f32((uint16_t)(km[g] & 0xffffu));
           const float kzz = f16_bits_to_f32((uint16_t)(km[g] >> 16));
-          v += kss * accg[r][g] + (kzz - 1024.0f * kss) * qs[r * G + g];
+          v += kss * accg[r][g] + (kzz - 1024.0f * kss) * qs[r][g];
         }
       } else {
         v = accg[r][0];
@@ -295,7 +335,7 @@ __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
     }
 
     // ---- online softmax with a lazily raised running max
-    bool raise = blk == blk0;
+    bool raise = i == seg_start;
     if (!raise) {
       bool over = false;
 #pragma unroll
@@ -308,7 +348,7 @@ __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
         const float mb = wave_allmax(s[r]);
         const float mn = fmaxf(m_run[r], mb);
         const float al = m_run[r] == -INFINITY ? 0.0f : fast_exp2(m_run[r] - mn);
-        m_run[r] = mn;
+        m_run[r] = uniform_f32(mn);
         l_part[r] *= al;
 #pragma unroll
         for (int g = 0; g < G; ++g) c_part[r][g] *= al;
@@ -345,115 +385,110 @@ __global__ __launch_bounds__(64) void k_attn_valu(AttnArgs a) {
     }
     __syncthreads();
 
-    // ---- P.V: lane owns V^T rows d = DPL*lane .. +DPL, 32 tokens per group
+    // ---- P.V: lane owns V^T rows d = DPL*lane .. +DPL.  Chunks of 8 tokens
+    // (4 pairs): the chunk's V bytes become fp16 pairs once and serve every
+    // row; the weights of one (chunk, row) are one 16-byte LDS read, issued
+    // two steps ahead of their use.
     const uint32_t *w32 = reinterpret_cast<const uint32_t *>(w_lds);
+    constexpr int NSTEP = 8 * NR;  // (tg, chunk, row) steps
+    auto wread = [&](int k) -> uint4 {
+      const int r = k % NR, c = k / NR;  // c = tg * 4 + chunk
+      return *reinterpret_cast<const uint4 *>(w32 + (r * G + gl) * 32 + 4 * c);
+    };
+    uint4 wq0 = wread(0), wq1 = wread(1 < NSTEP ? 1 : 0);
 #pragma unroll
-    for (int tg = 0; tg < 2; ++tg) {
-      if (tg > 0) {
+    for (int c = 0; c < 8; ++c) {
+      const int tg = c >> 2, ch = c & 3;
+      half2_t vp[DPL][4];
 #pragma unroll
-        for (int i = 0; i < 2 * DPL; ++i) order_after(vr[1][i], acc[NR - 1][DPL - 1]);
+      for (int e = 0; e < DPL; ++e) {
+        // conversion of this chunk waits for the previous chunk's dots
+        if (c > 0) order_after(vr[tg][2 * e + (ch >> 1)], acc[NR - 1][DPL - 1]);
+        const uint4 w = vr[tg][2 * e + (ch >> 1)];
+        const uint32_t w0 = (ch & 1) ? w.z : w.x, w1 = (ch & 1) ? w.w : w.y;
+        vp[e][0] = bytes01_plus1024(w0);
+        vp[e][1] = bytes23_plus1024(w0);
+        vp[e][2] = bytes01_plus1024(w1);
+        vp[e][3] = bytes23_plus1024(w1);
       }
-      half2_t vp[DPL][16];
-#pragma unroll
-      for (int e = 0; e < DPL; ++e)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint4 w = vr[tg][2 * e + h];
-          vp[e][8 * h + 0] = bytes01_plus1024(w.x);
-          vp[e][8 * h + 1] = bytes23_plus1024(w.x);
-          vp[e][8 * h + 2] = bytes01_plus1024(w.y);
-          vp[e][8 * h + 3] = bytes23_plus1024(w.y);
-          vp[e][8 * h + 4] = bytes01_plus1024(w.z);
-          vp[e][8 * h + 5] = bytes23_plus1024(w.z);
-          vp[e][8 * h + 6] = bytes01_plus1024(w.w);
-          vp[e][8 * h + 7] = bytes23_plus1024(w.w);
-        }
       if constexpr (MODE == MODE_REF) {
-        const uint32_t *s32 = reinterpret_cast<const uint32_t *>(sz_lds);
+        const uint4 sp4 = *reinterpret_cast<const uint4 *>(sz_lds + 8 * c);
+        const uint4 zp4 = *reinterpret_cast<const uint4 *>(sz_lds + 64 + 8 * c);
+        const uint32_t sp[4] = {sp4.x, sp4.y, sp4.z, sp4.w}, zp[4] = {zp4.x, zp4.y, zp4.z, zp4.w};
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const half2_t sp = u32_as_h2(s32[tg * 16 + i]);
-          const half2_t zp = u32_as_h2(s32[32 + tg * 16 + i]);
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) vp[e][i] = (vp[e][i] + m1024) * sp + zp;
-        }
-      }
-      // weights of row r + 1 are read while row r is reduced
-      uint4 wn[4];
-      {
-        const uint4 *wp = reinterpret_cast<const uint4 *>(w32 + gl * 32 + tg * 16);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) wn[i] = wp[i];
+          for (int e = 0; e < DPL; ++e) vp[e][i] = (vp[e][i] + m1024) * u32_as_h2(sp[i]) + u32_as_h2(zp[i]);
       }
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
-        const uint4 a0 = wn[0], a1 = wn[1], a2 = wn[2], a3 = wn[3];
+        const int k = c * NR + r;
+        const uint4 wc = wq0;
         asm volatile("" ::: "memory");
-        if (r + 1 < NR) {
-          const uint4 *wp = reinterpret_cast<const uint4 *>(w32 + ((r + 1) * G + gl) * 32 + tg * 16);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) wn[i] = wp[i];
-        }
-        const uint32_t ww[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
-                                 a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+        wq0 = wq1;
+        if (k + 2 < NSTEP) wq1 = wread(k + 2);
+        const uint32_t ww[4] = {wc.x, wc.y, wc.z, wc.w};
 #pragma unroll
         for (int e = 0; e < DPL; ++e)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) acc[r][e] = dot2(u32_as_h2(ww[i]), vp[e][i], acc[r][e]);
+          for (int i = 0; i < 4; ++i) acc[r][e] = dot2(u32_as_h2(ww[i]), vp[e][i], acc[r][e]);
       }
     }
-    load_v(nreg);  // V registers are free: fetch the next block
+    load_v(nrs);  // V registers are free: fetch the next block
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       km[g] = km_next[g];
       vm[g] = vm_next[g];
     }
-    reg = nreg;
     __syncthreads();
   }
 
-  // ---- epilogue
-  float o[NR][DPL], lsum[NR];
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    lsum[r] = wave_allsum(l_part[r]);
-    float cg = 0.0f;
-    if constexpr (MODE == MODE_AFFINE) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float c = wave_allsum(c_part[r][g]);
-        cg = g == gl ? c : cg;
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) o[r][e] = acc[r][e] + cg;
-  }
-  if (n_splits == 1) {
+    // ---- end of the segment: the whole sequence in this wave -> output;
+    // otherwise a partial in slot hk * (waves + B) + wave + b
+    float lsum[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      const float inv = lsum[r] > 0.0f ? 1.0f / lsum[r] : 0.0f;
-      const int64_t ob = out_row_base(a, b, hk, r, D);
+      lsum[r] = uniform_f32(wave_allsum(l_part[r]));
+      float cg = 0.0f;
+      if constexpr (MODE == MODE_AFFINE) {
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) store_out(a.out, ob + DPL * lane + e, o[r][e] * inv, a.out_dtype);
+        for (int g = 0; g < G; ++g) {
+          const float c = wave_allsum(c_part[r][g]);
+          cg = g == gl ? c : cg;
+        }
+      }
+#pragma unroll
+      for (int e2 = 0; e2 < DPL; ++e2) acc[r][e2] += cg;
     }
-    return;
-  }
+    if (s >= i0 && e <= iend) {
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    const int64_t pi = part_index(a, b, hk, split, r);
+      for (int r = 0; r < NR; ++r) {
+        const float inv = lsum[r] > 0.0f ? 1.0f / lsum[r] : 0.0f;
+        const int64_t ob = out_row_base(a, b, hk, r, D);
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) a.ws_o[pi * D + DPL * lane + e] = o[r][e];
-    if (lane == 0) {
-      a.ws_ml[pi * 2] = m_run[r];
-      a.ws_ml[pi * 2 + 1] = lsum[r];
+        for (int e2 = 0; e2 < DPL; ++e2) store_out(a.out, ob + DPL * lane + e2, acc[r][e2] * inv, a.out_dtype);
+      }
+    } else {
+      const int64_t slot = (int64_t)hk * (a.waves + a.B) + wv + b;
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const int64_t pi = slot * NR + r;
+#pragma unroll
+        for (int e2 = 0; e2 < DPL; ++e2) a.ws_o[pi * D + DPL * lane + e2] = acc[r][e2];
+        if (lane == 0) reinterpret_cast<float2 *>(a.ws_ml)[pi] = float2{m_run[r], lsum[r]};
+      }
     }
+    if (i >= iend_eff) break;
+    // next sequence with blocks (empty ones get zeros from the merge)
+    ++b;
+    s = e;
+    while (b < a.B && seq_blocks(a, a.lens[b]) == 0) ++b;
+    if (b >= a.B) break;
   }
 }
 
 template <int D, int MODE, int NR>
 static void launch_one(const AttnArgs &args, int B, dim3 grid, hipStream_t st) {
-  constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
-  k_attn_prep<D, NR, G><<<dim3((unsigned)args.Hkv, (unsigned)B), dim3(64), 0, st>>>(args);
   k_attn_valu<D, NR, MODE><<<grid, dim3(64), 0, st>>>(args);
 }
 
@@ -475,10 +510,10 @@ static hipError_t launch_valu_nr(const AttnArgs &args, int NR, int B, dim3 grid,
 
 hipError_t launch_attn_valu(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
                             hipStream_t st) {
-  // one VGPR of block-table entries per split
-  if (p.split_blocks < 1 || p.split_blocks > 64) return hipErrorInvalidValue;
+  // one VGPR of block-table entries per wave
+  if (p.split_blocks < 1 || p.split_blocks > 64 || p.waves < 1) return hipErrorInvalidValue;
   const AttnArgs args = make_attn_args(g, layer, a, p);
-  const dim3 grid((unsigned)p.max_splits, (unsigned)g.Hkv, (unsigned)a.B);
+  const dim3 grid((unsigned)p.waves, (unsigned)g.Hkv);
   switch (g.D) {
     case 64:
       return g.mode == MODE_REF ? launch_valu_nr<64, MODE_REF>(args, p.NR, a.B, grid, st)

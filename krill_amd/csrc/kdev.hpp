@@ -18,31 +18,39 @@ constexpr int kBlockTokens = 64;
 
 // Layout of one (layer, block, kv-head) region of the pool, D = head_dim,
 // G = scale/zero groups per token (1 in the reference's row mode, D/64 in the
-// affine group-64 mode):
-//   [0, 64*D)          K bytes, d-chunk major:  ((d/32)*64 + t)*32 + d%32
-//   [64*D, 128*D)      V bytes, token-group major, permuted inside each
-//                      32-token group:  ((t/32)*D + d)*32 + vpos(t%32)
+// affine group-64 mode).  Every piece is laid out so that a wave64 load of
+// 16 bytes per lane (4*G bytes for metadata) reads one contiguous run:
+//   [0, 64*D)          K bytes in 16-byte d-chunks, chunk major:
+//                        ((d/16)*64 + t)*16 + d%16
+//                      (lane = token reads chunk c of all 64 tokens at once)
+//   [64*D, 128*D)      V bytes, per 32-token group tg (32*D bytes each) in
+//                      16-byte pieces of 16 token positions of one d:
+//                        tg*32*D + ((2*(d%DPL) + p/16)*64 + d/DPL)*16 + p%16
+//                      with DPL = D/64 and p = vpos(t%32) the token's
+//                      position (lane l, owning d = DPL*l .. DPL*l+DPL-1,
+//                      reads piece i of all lanes at once)
 //   [128*D, +256*G)    K (scale, zero) fp16 pairs:  (t*G + g)*4
 //   [128*D+256*G, ..)  V (scale, zero) fp16 pairs
-// K rows of 32 consecutive d are 32-byte aligned so a 16x16x32 MFMA A
-// operand (8 d per lane) and the VALU score loop (32 d per lane) both load
-// contiguously; V stores 32 tokens of one d contiguously in the order the
-// MFMA P.V B operand produces them (lane quarter q holds tokens 4q..4q+3 and
-// 16+4q..16+4q+3), so P never has to be transposed.
+// The 16-byte K chunks also hold the 8 consecutive d of a 16x16x32 MFMA A
+// operand contiguously.  Token positions inside a V group follow the MFMA P.V
+// B operand (lane quarter q holds tokens 4q..4q+3 and 16+4q..16+4q+3 as
+// positions 8q..8q+7, contiguous), so P never has to be transposed.
 __host__ __device__ constexpr int head_region_bytes(int D, int G) { return 128 * D + 512 * G; }
 __host__ __device__ constexpr int v_offset(int D) { return 64 * D; }
 __host__ __device__ constexpr int km_offset(int D) { return 128 * D; }
 __host__ __device__ constexpr int vm_offset(int D, int G) { return 128 * D + 256 * G; }
-__host__ __device__ constexpr int k_byte(int t, int d) { return (((d >> 5) * 64 + t) << 5) + (d & 31); }
+__host__ __device__ constexpr int k_byte(int t, int d) { return (((d >> 4) * 64 + t) << 4) + (d & 15); }
 // position of token tt (0..31) inside its 32-token group of a V row
 __host__ __device__ constexpr int vpos(int tt) {
   return (((tt & 15) >> 2) << 3) + (tt & 3) + ((tt >> 4) << 2);
 }
 // inverse of vpos
 __host__ __device__ constexpr int vtok(int p) { return ((p >> 3) << 2) + (p & 3) + (((p >> 2) & 1) << 4); }
-__host__ __device__ constexpr int v_byte(int D, int t, int d) {
-  return 64 * D + (((t >> 5) * D + d) << 5) + vpos(t & 31);
+// byte of V row d, token group tg, position p (0..31)
+__host__ __device__ constexpr int v_pos_byte(int D, int tg, int d, int p) {
+  return 64 * D + tg * 32 * D + (((2 * (d % (D / 64)) + (p >> 4)) * 64 + d / (D / 64)) << 4) + (p & 15);
 }
+__host__ __device__ constexpr int v_byte(int D, int t, int d) { return v_pos_byte(D, t >> 5, d, vpos(t & 31)); }
 
 // Device view of one layer of the pool.
 struct LayerView {
@@ -180,13 +188,19 @@ __device__ __forceinline__ float swap32_max(float v) {
   row_swap32(a, b);
   return fmaxf(a, b);
 }
-__device__ __forceinline__ float wave_allsum(float v) {
+// Sum over the 16 lanes of each DPP row, left in every lane of the row.
+__device__ __forceinline__ float row_allsum(float v) {
   v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
   v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
   v += dpp_f32<0x124>(v);  // row_ror:4
   v += dpp_f32<0x128>(v);  // row_ror:8
-  return swap32_sum(swap16_sum(v));
+  return v;
 }
+// A value known to be the same in every lane, moved to a scalar register.
+__device__ __forceinline__ float uniform_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+__device__ __forceinline__ float wave_allsum(float v) { return swap32_sum(swap16_sum(row_allsum(v))); }
 __device__ __forceinline__ float wave_allmax(float v) {
   v = fmaxf(v, dpp_f32<0xB1>(v));
   v = fmaxf(v, dpp_f32<0x4E>(v));

@@ -319,40 +319,30 @@ __global__ __launch_bounds__(256) void k_copy_pairs(uint8_t *base, int64_t layer
 }
 
 // ---------------------------------------------------------------------------
-// Split-K merge of attention partials (log2-domain running max m, sum l,
-// unnormalised o) into the output.  One wave per (row, kv-head, sequence).
-// Splits of one (sequence, kv-head) that saw no visible key carry m = -inf
-// and contribute nothing.  A sequence with one split was written directly by
-// the attention kernel; an empty sequence gets zeros.
+// Merge of attention partials (log2-domain running max m, sum l, unnormalised
+// o) into the output.  One wave per (row, kv-head, sequence).  Partials that
+// saw no visible key carry m = -inf and contribute nothing.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void k_attn_merge(const float *__restrict__ ws_o, const float *__restrict__ ws_ml,
-                                                   const int32_t *__restrict__ lens, int32_t max_blocks,
-                                                   int32_t Hkv, int32_t NR, int32_t R, int32_t Lq, int32_t Hq,
-                                                   int32_t D, int32_t split_blocks, int32_t max_splits, void *out,
-                                                   int32_t out_dtype) {
+// Combines the n consecutive partial slots starting at `slot0` for row r.
+template <int D>
+__device__ __forceinline__ void merge_slots(const AttnArgs &a, int64_t slot0, int n, int r, int64_t obase) {
   __shared__ float w_lds[64];
-  const int r = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x;
-  const int len = lens[b];
-  const int nb = min(min((len + 63) >> 6, max_blocks), max_splits * split_blocks);
-  const int n_splits = (nb + split_blocks - 1) / split_blocks;
-  if (n_splits <= 1) return;
-  const int hq = hk * R + r % R, j = r / R;
-  const int64_t obase = (((int64_t)b * Hq + hq) * Lq + j) * D;
-  const int64_t pbase = ((int64_t)b * Hkv + hk) * max_splits;
-  const float2 *ml2 = reinterpret_cast<const float2 *>(ws_ml);
-  // lane s reads split s0 + s: all (m, l) loads of a 64-split chunk are in
+  const float2 *ml2 = reinterpret_cast<const float2 *>(a.ws_ml);
+  // lane s reads slot s0 + s: all (m, l) loads of a 64-slot chunk are in
   // flight together
   float M = -INFINITY;
-  for (int s0 = 0; s0 < n_splits; s0 += 64)
-    if (s0 + lane < n_splits) M = fmaxf(M, ml2[(pbase + s0 + lane) * NR + r].x);
+  for (int s0 = 0; s0 < n; s0 += 64)
+    if (s0 + lane < n) M = fmaxf(M, ml2[(slot0 + s0 + lane) * a.NR + r].x);
   M = wave_allmax(M);
-  float lpart = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // d = lane + 64 e, D <= 256
-  for (int s0 = 0; s0 < n_splits; s0 += 64) {
-    const int cnt = min(64, n_splits - s0);
+  float lpart = 0.0f, acc[D / 64];  // d = lane + 64 e
+#pragma unroll
+  for (int e = 0; e < D / 64; ++e) acc[e] = 0.0f;
+  for (int s0 = 0; s0 < n; s0 += 64) {
+    const int cnt = min(64, n - s0);
     float w = 0.0f;
     if (lane < cnt) {
-      const float2 ml = ml2[(pbase + s0 + lane) * NR + r];
+      const float2 ml = ml2[(slot0 + s0 + lane) * a.NR + r];
       w = ml.x == -INFINITY ? 0.0f : fast_exp2(ml.x - M);
       lpart += w * ml.y;
     }
@@ -361,18 +351,61 @@ __global__ __launch_bounds__(64) void k_attn_merge(const float *__restrict__ ws_
 #pragma unroll 8
     for (int i = 0; i < cnt; ++i) {
       const float wi = w_lds[i];
-      const float *op = ws_o + ((pbase + s0 + i) * NR + r) * (int64_t)D;
+      const float *op = a.ws_o + ((slot0 + s0 + i) * a.NR + r) * (int64_t)D;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (64 * e < D) acc[e] += wi * op[lane + 64 * e];
+      for (int e = 0; e < D / 64; ++e) acc[e] += wi * op[lane + 64 * e];
     }
     __syncthreads();
   }
   const float Lsum = wave_allsum(lpart);
   const float inv = (M == -INFINITY || !(Lsum > 0.0f)) ? 0.0f : 1.0f / Lsum;
 #pragma unroll
-  for (int e = 0; e < 4; ++e)
-    if (64 * e < D) store_out(out, obase + lane + 64 * e, acc[e] * inv, out_dtype);
+  for (int e = 0; e < D / 64; ++e) store_out(a.out, obase + lane + 64 * e, acc[e] * inv, a.out_dtype);
+}
+
+// After the MFMA kernel: splits of split_blocks blocks per sequence.  A
+// sequence with one split (or none) was written by the attention kernel.
+template <int D>
+__global__ __launch_bounds__(64) void k_attn_merge_split(AttnArgs a) {
+  const int r = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int nb = seq_blocks(a, a.lens[b]);
+  const int n_splits = (nb + a.split_blocks - 1) / a.split_blocks;
+  if (n_splits <= 1) return;
+  merge_slots<D>(a, part_index(a, b, hk, 0, 0) / a.NR, n_splits, r, out_row_base(a, b, hk, r, D));
+}
+
+// After the VALU kernel (flat block order, split_blocks blocks per wave):
+// sequence b's blocks are flat [s, s + nb), covered by waves s / PW ..
+// (s + nb - 1) / PW, whose partials sit in consecutive slots wave + b.  A
+// sequence inside one wave was written by the attention kernel; an empty one
+// gets zeros here.
+template <int D>
+__global__ __launch_bounds__(64) void k_attn_merge_flat(AttnArgs a) {
+  const int r = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x;
+  const int64_t obase = out_row_base(a, b, hk, r, D);
+  const int nb = seq_blocks(a, a.lens[b]);
+  if (nb == 0) {
+#pragma unroll
+    for (int e = 0; e < D / 64; ++e) store_out(a.out, obase + lane + 64 * e, 0.0f, a.out_dtype);
+    return;
+  }
+  // flat start of sequence b
+  int carry = 0, s = 0;
+  for (int c0 = 0; c0 <= b; c0 += 64) {
+    const int bb = c0 + lane;
+    const int nbv = bb < a.B ? seq_blocks(a, a.lens[bb]) : 0;
+    const int incl = wave_incl_scan(nbv) + carry;
+    if (b < c0 + 64) {
+      s = __builtin_amdgcn_readlane(incl - nbv, b - c0);
+      break;
+    }
+    carry = __builtin_amdgcn_readlane(incl, 63);
+  }
+  const int PW = a.split_blocks;
+  const int first = s / PW, last = (s + nb - 1) / PW;
+  if (first == last) return;
+  merge_slots<D>(a, (int64_t)hk * (a.waves + a.B) + first + b, last - first + 1, r, obase);
 }
 
 // ---------------------------------------------------------------------------
@@ -509,41 +542,54 @@ int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq,
   p.NR = R * Lq;
   p.use_mfma = path == 2 || (path == 0 && p.NR > 8);
   if (!p.use_mfma && p.NR > 8) return -2;
-  // MFMA: at most 32 query rows per wave (16 for D = 256) keeps the score,
-  // output and operand tiles in registers without spilling.
-  const int32_t max_tiles = g.D >= 256 ? 1 : 2;
-  p.nrt = p.use_mfma ? std::min(max_tiles, (p.NR + 15) / 16) : 0;
-  p.row_groups = p.use_mfma ? (p.NR + 16 * p.nrt - 1) / (16 * p.nrt) : 1;
   const int32_t nb_max = std::max(1, (max_seq_len + 63) / 64);
-  int32_t sb = split_blocks;
-  if (sb <= 0) {
-    // Aim for about 4096 workgroups over the longest sequence so the
-    // 256 CUs stay busy across ragged lengths; at least 2 blocks per split.
-    const int64_t units = (int64_t)B * g.Hkv * p.row_groups;
-    sb = (int32_t)std::max<int64_t>(2, ((int64_t)nb_max * units + 4095) / 4096);
+  if (p.use_mfma) {
+    // MFMA: at most 32 query rows per wave (16 for D = 256) keeps the score,
+    // output and operand tiles in registers without spilling.
+    const int32_t max_tiles = g.D >= 256 ? 1 : 2;
+    p.nrt = std::min(max_tiles, (p.NR + 15) / 16);
+    p.row_groups = (p.NR + 16 * p.nrt - 1) / (16 * p.nrt);
+    int32_t sb = split_blocks;
+    if (sb <= 0) {
+      // about 4096 workgroups over the longest sequence; at least 2 blocks
+      const int64_t units = (int64_t)B * g.Hkv * p.row_groups;
+      sb = (int32_t)std::max<int64_t>(2, ((int64_t)nb_max * units + 4095) / 4096);
+    }
+    sb = std::min(sb, nb_max);
+    p.split_blocks = sb;
+    p.max_splits = (nb_max + sb - 1) / sb;
+    p.nb_cap = p.max_splits * sb;
+    p.slots = (int64_t)B * g.Hkv * p.max_splits;
+  } else {
+    // VALU: the blocks of all sequences in flat order, split_blocks per wave
+    // (at most 64: one VGPR of block-table entries).  The automatic size
+    // aims at about 4096 waves when every sequence is max_seq_len long.
+    int32_t pw = split_blocks;
+    if (pw <= 0) pw = (int32_t)std::max<int64_t>(2, ((int64_t)B * nb_max * g.Hkv + 4095) / 4096);
+    pw = std::min(pw, 64);
+    p.split_blocks = pw;
+    p.max_splits = 0;
+    p.nb_cap = nb_max;
+    p.waves = (int32_t)std::max<int64_t>(1, ((int64_t)B * nb_max + pw - 1) / pw);
+    p.slots = (int64_t)g.Hkv * (p.waves + B);
   }
-  // The VALU kernel holds a split's block-table entries in one VGPR (one
-  // entry per lane), so a split covers at most 64 blocks.
-  if (!p.use_mfma) sb = std::min(sb, 64);
-  sb = std::min(sb, nb_max);
-  p.split_blocks = sb;
-  p.max_splits = (nb_max + sb - 1) / sb;
-  p.ws_bytes = ws_layout(B, g.Hkv, p.max_splits, p.NR, g.D, g.G).total;
+  p.ws_bytes = ws_layout(p.slots, p.NR, g.D).total;
   *plan = p;
   return 0;
 }
 
-// Split merge, launched after either attention kernel when some sequence
-// spans more than one split.
-hipError_t launch_attn_merge(const PoolGeometry &g, const AttnLaunch &a, const AttnPlan &p, hipStream_t st) {
-  if (p.max_splits <= 1 || a.B == 0) return hipSuccess;
-  const WsLayout w = ws_layout(a.B, g.Hkv, p.max_splits, p.NR, g.D, g.G);
-  const uint8_t *base = static_cast<const uint8_t *>(a.ws);
-  const float *ws_o = reinterpret_cast<const float *>(base + w.o);
-  const float *ws_ml = reinterpret_cast<const float *>(base + w.ml);
-  k_attn_merge<<<dim3((unsigned)p.NR, (unsigned)g.Hkv, (unsigned)a.B), dim3(64), 0, st>>>(
-      ws_o, ws_ml, a.lens, a.max_blocks, g.Hkv, p.NR, a.Hq / g.Hkv, a.Lq, a.Hq, g.D, p.split_blocks, p.max_splits, a.out,
-      a.out_dtype);
+hipError_t launch_attn_merge(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
+                             hipStream_t st) {
+  if (a.B == 0) return hipSuccess;
+  if (p.use_mfma && p.max_splits <= 1) return hipSuccess;
+  const AttnArgs args = make_attn_args(g, layer, a, p);
+  const dim3 grid((unsigned)p.NR, (unsigned)g.Hkv, (unsigned)a.B);
+  KRILL_DISPATCH_D(g.D, {
+    if (p.use_mfma)
+      k_attn_merge_split<D><<<grid, dim3(64), 0, st>>>(args);
+    else
+      k_attn_merge_flat<D><<<grid, dim3(64), 0, st>>>(args);
+  });
   return hipGetLastError();
 }
 
@@ -552,7 +598,7 @@ hipError_t launch_attention(const PoolGeometry &g, int32_t layer, const AttnLaun
   if (a.B == 0) return hipSuccess;
   hipError_t e = p.use_mfma ? launch_attn_mfma(g, layer, a, p, st) : launch_attn_valu(g, layer, a, p, st);
   if (e != hipSuccess) return e;
-  return launch_attn_merge(g, a, p, st);
+  return launch_attn_merge(g, layer, a, p, st);
 }
 
 }  // namespace krill

@@ -34,8 +34,11 @@ struct AttnLaunch {
 struct AttnPlan {
   int32_t NR;           // query rows per KV head = (Hq/Hkv) * Lq
   int32_t use_mfma;     // 1 when the MFMA kernel runs
-  int32_t split_blocks; // blocks per split
-  int32_t max_splits;
+  int32_t split_blocks; // blocks per split (MFMA) / per wave (VALU)
+  int32_t max_splits;   // MFMA: splits per sequence
+  int32_t waves;        // VALU: waves per KV head
+  int32_t nb_cap;       // blocks per sequence covered (from max_seq_len)
+  int64_t slots;        // partial results the workspace holds
   int32_t row_groups;   // MFMA: row groups of nrt 16-row tiles
   int32_t nrt;          // MFMA: 16-row tiles per wave (register budget bound)
   size_t ws_bytes;
@@ -66,6 +69,7 @@ hipError_t launch_attn_valu(const PoolGeometry &g, int32_t layer, const AttnLaun
                             hipStream_t st);
 hipError_t launch_attn_mfma(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
                             hipStream_t st);
-hipError_t launch_attn_merge(const PoolGeometry &g, const AttnLaunch &a, const AttnPlan &p, hipStream_t st);
+hipError_t launch_attn_merge(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
+                             hipStream_t st);
 
 }  // namespace krill
