@@ -129,8 +129,30 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   // lists of all sequences (so every wave streams the same number of bytes).
   const int PW = a.split_blocks;
   const int i0 = wv * PW, iend = i0 + PW;
-  int b, s;  // sequence holding block i0 and the flat index of its first block
-  if (!flat_locate(a, i0, b, s)) return;
+  // Sequence holding block i0 (b) and the flat index of its first block (s),
+  // from a wave prefix scan of per-sequence block counts.  The lengths of
+  // the 64-sequence chunk holding b stay in `lenv` (lane j: sequence c0 + j)
+  // for the table walk and the segment loop.
+  int b = -1, s = 0, c0 = 0, lenv = 0;
+  {
+    int carry = 0;
+    for (c0 = 0; c0 < a.B; c0 += 64) {
+      const int bb = c0 + lane;
+      lenv = bb < a.B ? a.lens[bb] : 0;
+      const int nbv = seq_blocks(a, lenv);
+      const int incl = wave_incl_scan(nbv) + carry;
+      const unsigned long long m = __ballot(bb < a.B && incl > i0);
+      if (m) {
+        const int l = __builtin_ctzll(m);
+        b = c0 + l;
+        s = __builtin_amdgcn_readlane(incl - nbv, l);
+        break;
+      }
+      carry = __builtin_amdgcn_readlane(incl, 63);
+    }
+  }
+  if (b < 0) return;  // beyond the last block
+  auto seq_len = [&](int bs) -> int { return bs - c0 < 64 ? __builtin_amdgcn_readlane(lenv, bs - c0) : a.lens[bs]; };
 
   // Physical block ids of flat blocks i0 .. iend-1 (at most 64): lane j holds
   // the entry of block i0 + j, read back with v_readlane, so no table load
@@ -141,7 +163,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     const int f = i0 + lane;
     int bs = b, ss = s;
     while (bs < a.B && ss < iend) {
-      const int nbs = seq_blocks(a, a.lens[bs]);
+      const int nbs = seq_blocks(a, seq_len(bs));
       if (lane < PW && f >= ss && f < ss + nbs) {
         const int phys = a.tables[(int64_t)bs * a.max_blocks + (f - ss)];
         tab = (unsigned)phys < (unsigned)a.lv.num_blocks ? phys : 0;
@@ -181,11 +203,53 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     ld_stream_words<G>(r, vm_offset(D, G) + lane * 4 * G, vmo);
   };
 
+  // fp16 query pairs: qv[r][c] holds pair 16*c + (lane & 15) of row r, so
+  // every 16-lane row carries the whole query (one VGPR per 32 d).  Affine
+  // mode also needs the sum of each 64-d group of the fp16 query (pairs
+  // 32g .. 32g+31 = columns 2g and 2g+1), reduced inside each 16-lane row.
+  uint32_t qv[NR][D / 32];
+  float qs[NR][G];
+  const bool q_bf16 = a.q_dtype == DT_BF16;
+  auto load_q = [&](int bq) {  // raw pairs of sequence bq
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int hq = hk * a.R + r % a.R, j = r / a.R;
+      const uint32_t *qp = reinterpret_cast<const uint32_t *>(a.q + (((int64_t)bq * a.Hq + hq) * a.Lq + j) * D);
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) qv[r][c] = qp[16 * c + (lane & 15)];
+    }
+  };
+  auto finish_q = [&]() {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) {
+        // bf16 pairs are widened to fp32 and rounded to fp16; fp16 pairs pass through
+        const uint32_t w = qv[r][c];
+        const half2_t hb = half2_t{(_Float16)__builtin_bit_cast(float, w << 16),
+                                   (_Float16)__builtin_bit_cast(float, w & 0xffff0000u)};
+        qv[r][c] = q_bf16 ? h2_as_u32(hb) : w;
+      }
+      if constexpr (MODE == MODE_AFFINE) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const half2_t p0 = u32_as_h2(qv[r][2 * g]), p1 = u32_as_h2(qv[r][2 * g + 1]);
+          qs[r][g] = uniform_f32(row_allsum(((float)p0.x + (float)p0.y) + ((float)p1.x + (float)p1.y)));
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g) qs[r][g] = 0.0f;
+      }
+    }
+  };
+
   // Loads of block n+1 are issued in a fixed order inside the loop: K bytes
   // and metadata once block n's K registers are consumed, V bytes once its V
   // registers are; waits on a load never cover a younger prefetch.  The
-  // first block's loads are settled before the loop so the loop-head waits
-  // follow the steady-state order only.
+  // first block's loads (and the first segment's queries, issued ahead of
+  // them) are settled before the loop so the loop-head waits follow the
+  // steady-state order only.
+  load_q(b);
   {
     const __amdgpu_buffer_rsrc_t r0 = rsrc_of(i0);
     load_k(r0);
@@ -203,44 +267,16 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     settle(km[g]);
     settle(vm[g]);
   }
+  finish_q();
 
   int i = i0;
-  // one pass per sequence segment [max(s, i0), min(s + nb, iend))
+  // one pass per sequence segment [max(s, i0), min(s + nb, iend)); the
+  // queries of sequence b are ready on entry
   while (true) {
-    const int len = a.lens[b];
+    const int len = seq_len(b);
     const int e = s + seq_blocks(a, len);
     const int seg_start = i, seg_end = min(e, iend_eff);
 
-    // fp16 query pairs: qv[r][c] holds pair 16*c + (lane & 15) of row r, so
-    // every 16-lane row carries the whole query (one VGPR per 32 d).  Affine
-    // mode also needs the sum of each 64-d group of the fp16 query (pairs
-    // 32g .. 32g+31 = columns 2g and 2g+1), reduced inside each 16-lane row.
-    uint32_t qv[NR][D / 32];
-    float qs[NR][G];
-    const bool q_bf16 = a.q_dtype == DT_BF16;
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      const int hq = hk * a.R + r % a.R, j = r / a.R;
-      const uint32_t *qp = reinterpret_cast<const uint32_t *>(a.q + (((int64_t)b * a.Hq + hq) * a.Lq + j) * D);
-#pragma unroll
-      for (int c = 0; c < D / 32; ++c) {
-        const uint32_t w = qp[16 * c + (lane & 15)];
-        // bf16 pairs are widened to fp32 and rounded to fp16; fp16 pairs pass through
-        const half2_t hb = half2_t{(_Float16)__builtin_bit_cast(float, w << 16),
-                                   (_Float16)__builtin_bit_cast(float, w & 0xffff0000u)};
-        qv[r][c] = q_bf16 ? h2_as_u32(hb) : w;
-      }
-      if constexpr (MODE == MODE_AFFINE) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const half2_t p0 = u32_as_h2(qv[r][2 * g]), p1 = u32_as_h2(qv[r][2 * g + 1]);
-          qs[r][g] = uniform_f32(row_allsum(((float)p0.x + (float)p0.y) + ((float)p1.x + (float)p1.y)));
-        }
-      } else {
-#pragma unroll
-        for (int g = 0; g < G; ++g) qs[r][g] = 0.0f;
-      }
-    }
     int lim[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) lim[r] = len - a.Lq + r / a.R + 1;
@@ -482,8 +518,10 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     // next sequence with blocks (empty ones get zeros from the merge)
     ++b;
     s = e;
-    while (b < a.B && seq_blocks(a, a.lens[b]) == 0) ++b;
+    while (b < a.B && seq_blocks(a, seq_len(b)) == 0) ++b;
     if (b >= a.B) break;
+    load_q(b);
+    finish_q();
   }
 }
 

@@ -324,43 +324,59 @@ __global__ __launch_bounds__(256) void k_copy_pairs(uint8_t *base, int64_t layer
 // saw no visible key carry m = -inf and contribute nothing.
 // ---------------------------------------------------------------------------
 // Combines the n consecutive partial slots starting at `slot0` for row r.
+// The (m, l) pairs of the first 64 slots (lane s: slot s) and the o vectors
+// of the first 8 slots are loaded in one round; later slots (rare) loop.
 template <int D>
 __device__ __forceinline__ void merge_slots(const AttnArgs &a, int64_t slot0, int n, int r, int64_t obase) {
+  constexpr int E = D / 64;  // d = lane + 64 e
+  constexpr int K0 = 8;
   __shared__ float w_lds[64];
   const int lane = threadIdx.x;
   const float2 *ml2 = reinterpret_cast<const float2 *>(a.ws_ml);
-  // lane s reads slot s0 + s: all (m, l) loads of a 64-slot chunk are in
-  // flight together
-  float M = -INFINITY;
-  for (int s0 = 0; s0 < n; s0 += 64)
+  auto orow = [&](int k) { return a.ws_o + ((slot0 + k) * a.NR + r) * (int64_t)D + lane; };
+  float2 ml = lane < n ? ml2[(slot0 + lane) * a.NR + r] : float2{-INFINITY, 0.0f};
+  float ov[K0][E];
+#pragma unroll
+  for (int k = 0; k < K0; ++k)
+#pragma unroll
+    for (int e = 0; e < E; ++e) ov[k][e] = k < n ? orow(k)[64 * e] : 0.0f;
+  float M = ml.x;
+  for (int s0 = 64; s0 < n; s0 += 64)
     if (s0 + lane < n) M = fmaxf(M, ml2[(slot0 + s0 + lane) * a.NR + r].x);
   M = wave_allmax(M);
-  float lpart = 0.0f, acc[D / 64];  // d = lane + 64 e
+  float acc[E], lpart = 0.0f;
 #pragma unroll
-  for (int e = 0; e < D / 64; ++e) acc[e] = 0.0f;
+  for (int e = 0; e < E; ++e) acc[e] = 0.0f;
   for (int s0 = 0; s0 < n; s0 += 64) {
     const int cnt = min(64, n - s0);
-    float w = 0.0f;
-    if (lane < cnt) {
-      const float2 ml = ml2[(slot0 + s0 + lane) * a.NR + r];
-      w = ml.x == -INFINITY ? 0.0f : fast_exp2(ml.x - M);
-      lpart += w * ml.y;
-    }
+    if (s0 > 0) ml = lane < cnt ? ml2[(slot0 + s0 + lane) * a.NR + r] : float2{-INFINITY, 0.0f};
+    const float w = lane < cnt && ml.x != -INFINITY ? fast_exp2(ml.x - M) : 0.0f;
+    lpart += w * ml.y;
     w_lds[lane] = w;
     __syncthreads();
-#pragma unroll 8
-    for (int i = 0; i < cnt; ++i) {
-      const float wi = w_lds[i];
-      const float *op = a.ws_o + ((slot0 + s0 + i) * a.NR + r) * (int64_t)D;
+    int k = 0;
+    if (s0 == 0) {
 #pragma unroll
-      for (int e = 0; e < D / 64; ++e) acc[e] += wi * op[lane + 64 * e];
+      for (int kk = 0; kk < K0; ++kk) {
+        const float wk = kk < cnt ? w_lds[kk] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[e] += wk * ov[kk][e];
+      }
+      k = K0;
+    }
+#pragma unroll 4
+    for (; k < cnt; ++k) {
+      const float wk = w_lds[k];
+      const float *op = orow(s0 + k);
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] += wk * op[64 * e];
     }
     __syncthreads();
   }
   const float Lsum = wave_allsum(lpart);
   const float inv = (M == -INFINITY || !(Lsum > 0.0f)) ? 0.0f : 1.0f / Lsum;
 #pragma unroll
-  for (int e = 0; e < D / 64; ++e) store_out(a.out, obase + lane + 64 * e, acc[e] * inv, a.out_dtype);
+  for (int e = 0; e < E; ++e) store_out(a.out, obase + lane + 64 * e, acc[e] * inv, a.out_dtype);
 }
 
 // After the MFMA kernel: splits of split_blocks blocks per sequence.  A

@@ -162,6 +162,17 @@ def test_decode_attention_split_merge(split_blocks):
     assert err <= ATOL, f"max abs error {err:.3e}"
 
 
+@pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
+def test_decode_attention_many_partials(mode):
+    # one block per wave: the 5000-token sequence spreads over 79 waves, so
+    # the merge walks more than 64 partial slots; the empty sequence and the
+    # sequences around it cross wave boundaries at different offsets
+    print(f"\ncase decode_many_partials mode={mode}", flush=True)
+    got, ref = _attn_case(mode, 128, 2, 5, [70, 0, 5000, 130, 64], split_blocks=1, seed=5)
+    err = np.abs(got - ref).max()
+    assert err <= ATOL, f"max abs error {err:.3e}"
+
+
 @pytest.mark.parametrize("out_dtype", ["bf16", "f16"])
 def test_decode_attention_low_precision_output(out_dtype):
     print(f"\ncase decode_out {out_dtype}", flush=True)
