@@ -50,6 +50,9 @@ def parse():
     ap.add_argument("--kernel-reps", type=int, default=5, help="repetitions of the attention-only timing loop")
     ap.add_argument("--cpu-baseline", type=int, default=1, help="1: time the CPU baseline sample on rank 0")
     ap.add_argument("--seed", type=int, default=20261203)
+    ap.add_argument("--copy-calibration", type=int, default=0,
+                    help="MiB for a plain device copy (torch.neg of float32) run before the bench, so one "
+                         "rocprofv3 --pmc run reads FETCH_SIZE/WRITE_SIZE of a kernel of known traffic too")
     return ap.parse_args()
 
 
@@ -92,6 +95,15 @@ def main():
     sp = ctypes.c_void_p(stream.cuda_stream)
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
+
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        x = torch.ones(n, dtype=torch.float32, device=dev)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            torch.neg(x, out=y)
+        torch.cuda.synchronize()
+        del x, y
 
     # ---- fill every layer with the initial contexts (product path: reserve + quantize-append)
     seqs = [pool.seq_create() for _ in range(B)]
@@ -238,12 +250,12 @@ def main():
         "wall_s_timed": round(wall, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged decode attention (k_attn_valu + k_attn_merge), one layer",
+            "kernel": "paged decode attention call (k_attn_valu + k_attn_merge_flat), one layer",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args),
             "bytes_per_launch": int(launch_bytes),
             "avg_launch_ms": round(attn_ms, 5),
         },
@@ -251,6 +263,19 @@ def main():
         "pool": {"cow_copies": stats["cow_copies"], "blocks_used": stats["blocks_used"]},
     }
     print(json.dumps(rec))
+
+
+def measured_traffic(args):
+    """HBM bytes per decode-attention call from the committed rocprofv3 PMC
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated against a plain copy), when
+    it was taken on this workload; None otherwise."""
+    path = os.path.join(ROOT, "profiles", f"decode_attn_{args.workload}_{args.quant}_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return rec.get("traffic_bytes_per_call")
 
 
 def cpu_baseline(args, Hq, Hkv, D, lens0, per_tok):
@@ -276,7 +301,7 @@ def cpu_baseline(args, Hq, Hkv, D, lens0, per_tok):
         base.step(q, k, v, O.DT_BF16, 1.0 / math.sqrt(D), out)
         reps += 1
         el = time.perf_counter() - t0
-        if el > 10.0 or reps >= 8:
+        if el > 12.0 or reps >= 500:
             break
     per_layer_s = el / (reps * sample_layers)
     base.close()

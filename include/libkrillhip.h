@@ -57,7 +57,9 @@ extern "C" {
 #define KRILL_POOL_HOST_ONLY 1u /* block manager only: no device memory, kernels refused */
 
 /* pool options (krill_pool_set_option) */
-#define KRILL_OPT_SPLIT_BLOCKS 1 /* blocks per attention split; 0 = automatic */
+#define KRILL_OPT_SPLIT_BLOCKS 1 /* attention work unit in 64-token blocks: per wave on the VALU path
+                                    (1..64, consecutive blocks of the batch's concatenated block lists),
+                                    per split of one sequence on the MFMA path; 0 = automatic */
 #define KRILL_OPT_ATTN_PATH 2    /* 0 auto (VALU <= 8 query rows per KV head, else MFMA), 1 VALU, 2 MFMA */
 
 typedef struct krill_pool *krill_pool_t;
@@ -227,7 +229,9 @@ int32_t krill_attention_workspace_size(krill_pool_t pool, int32_t B, int32_t Hq,
  * Gemma4Model.swift:516-517 / Attention.swift:95-98 with the left-pad mask of
  * BatchedDecode.swift:277-287).  dev_q: [B][Hq][1][D] in_dtype;
  * dev_seq_lens include the token appended this step; out: [B][Hq][1][D]
- * in out_dtype (F32, F16 or BF16).  max_seq_len: host bound on seq_lens. */
+ * in out_dtype (F32, F16 or BF16).  max_seq_len: host bound on seq_lens
+ * (blocks of a longer sequence beyond it are not read).  Two launches on
+ * `stream`: the attention kernel and the merge of partial results. */
 int32_t krill_decode_attention(krill_pool_t pool, int32_t layer, const void *dev_q,
                                const int32_t *dev_block_tables, const int32_t *dev_seq_lens, int32_t B,
                                int32_t max_blocks, int32_t max_seq_len, int32_t Hq, float scale,
