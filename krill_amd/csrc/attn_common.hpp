@@ -111,27 +111,30 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
+__device__ __forceinline__ int wave_allsum_int(int v) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+
 // Flat block order of the VALU path: the blocks of sequences 0, 1, .., B-1
-// one after another.  Finds the sequence holding flat block `i` (the first
-// one whose blocks reach past i) and the flat index of its first block;
-// returns false when i lies beyond the last block.  Uniform across the wave.
-__device__ __forceinline__ bool flat_locate(const AttnArgs &a, int i, int &b_out, int &start_out) {
+// one after another, split evenly over W = min(grid waves, T) waves (wave w
+// holds flat blocks [ceil(w T / W), ceil((w+1) T / W)), at least one).  Returns the total T and sets
+// start_out to the flat index of sequence b's first block.  Uniform across
+// the wave.
+__device__ __forceinline__ int flat_total_and_start(const AttnArgs &a, int b, int &start_out) {
   const int lane = threadIdx.x & 63;
   int carry = 0;
   for (int c0 = 0; c0 < a.B; c0 += 64) {
     const int bb = c0 + lane;
     const int nbv = bb < a.B ? seq_blocks(a, a.lens[bb]) : 0;
     const int incl = wave_incl_scan(nbv) + carry;
-    const unsigned long long m = __ballot(bb < a.B && incl > i);
-    if (m) {
-      const int l = __builtin_ctzll(m);
-      b_out = c0 + l;
-      start_out = __builtin_amdgcn_readlane(incl - nbv, l);
-      return true;
-    }
+    if (b >= c0 && b < c0 + 64) start_out = __builtin_amdgcn_readlane(incl - nbv, b - c0);
     carry = __builtin_amdgcn_readlane(incl, 63);
   }
-  return false;
+  return carry;
 }
+// The wave holding flat block i (T > 0 blocks over W waves).
+__device__ __forceinline__ int flat_wave_of(int64_t i, int T, int W) { return (int)(i * W / T); }
 
 }  // namespace krill

@@ -126,22 +126,40 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   const int lane = threadIdx.x;
   const int wv = blockIdx.x, hk = blockIdx.y;
   // This wave's blocks: flat indices [i0, iend) of the concatenated block
-  // lists of all sequences (so every wave streams the same number of bytes).
-  const int PW = a.split_blocks;
-  const int i0 = wv * PW, iend = i0 + PW;
-  // Sequence holding block i0 (b) and the flat index of its first block (s),
-  // from a wave prefix scan of per-sequence block counts.  The lengths of
-  // the 64-sequence chunk holding b stay in `lenv` (lane j: sequence c0 + j)
-  // for the table walk and the segment loop.
-  int b = -1, s = 0, c0 = 0, lenv = 0;
+  // lists of all sequences.  The T blocks are split evenly over the grid's
+  // waves (sized to the resident wave capacity of the GPU; min(W, T) of them
+  // take part), wave w taking [ceil(w T / W), ceil((w+1) T / W)), so every
+  // wave streams the same bytes whatever the length mix and every SIMD
+  // carries the same load.
+  // Sequence lengths of the first 64 sequences stay in `lenv` (lane j:
+  // sequence c0 + j, c0 = the chunk holding the wave's first sequence).
+  const int W = a.waves;
+  int c0 = 0, lenv = lane < a.B ? a.lens[lane] : 0;
+  int nbv = seq_blocks(a, lenv);
+  int incl = wave_incl_scan(nbv);
+  int T = __builtin_amdgcn_readlane(incl, 63);
+  for (int cc = 64; cc < a.B; cc += 64) {
+    const int bb = cc + lane;
+    T += __builtin_amdgcn_readfirstlane(wave_allsum_int(bb < a.B ? seq_blocks(a, a.lens[bb]) : 0));
+  }
+  // At most T waves take part, so every participating wave holds at least
+  // one block (the merge relies on it: each wave between a sequence's first
+  // and last writes that sequence's partial).
+  const int Wt = min(W, T);
+  if (wv >= Wt) return;
+  const int i0 = (int)(((int64_t)wv * T + Wt - 1) / Wt);
+  const int iend = (int)(((int64_t)(wv + 1) * T + Wt - 1) / Wt);
+  int b = -1, s = 0;  // sequence holding block i0 and the flat index of its first block
   {
     int carry = 0;
     for (c0 = 0; c0 < a.B; c0 += 64) {
-      const int bb = c0 + lane;
-      lenv = bb < a.B ? a.lens[bb] : 0;
-      const int nbv = seq_blocks(a, lenv);
-      const int incl = wave_incl_scan(nbv) + carry;
-      const unsigned long long m = __ballot(bb < a.B && incl > i0);
+      if (c0 > 0) {
+        const int bb = c0 + lane;
+        lenv = bb < a.B ? a.lens[bb] : 0;
+        nbv = seq_blocks(a, lenv);
+        incl = wave_incl_scan(nbv) + carry;
+      }
+      const unsigned long long m = __ballot(c0 + lane < a.B && incl > i0);
       if (m) {
         const int l = __builtin_ctzll(m);
         b = c0 + l;
@@ -151,7 +169,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       carry = __builtin_amdgcn_readlane(incl, 63);
     }
   }
-  if (b < 0) return;  // beyond the last block
+  if (b < 0) return;
   auto seq_len = [&](int bs) -> int { return bs - c0 < 64 ? __builtin_amdgcn_readlane(lenv, bs - c0) : a.lens[bs]; };
 
   // Physical block ids of flat blocks i0 .. iend-1 (at most 64): lane j holds
@@ -164,7 +182,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     int bs = b, ss = s;
     while (bs < a.B && ss < iend) {
       const int nbs = seq_blocks(a, seq_len(bs));
-      if (lane < PW && f >= ss && f < ss + nbs) {
+      if (f < iend && f >= ss && f < ss + nbs) {
         const int phys = a.tables[(int64_t)bs * a.max_blocks + (f - ss)];
         tab = (unsigned)phys < (unsigned)a.lv.num_blocks ? phys : 0;
       }
@@ -546,10 +564,50 @@ static hipError_t launch_valu_nr(const AttnArgs &args, int NR, int B, dim3 grid,
   return hipGetLastError();
 }
 
+template <int D, int MODE>
+static int32_t occupancy_nr(int NR) {
+  int n = 0;
+  hipError_t e = hipErrorInvalidValue;
+  switch (NR) {
+#define KRILL_OCC(N)                                                                                        \
+  case N:                                                                                                   \
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(&k_attn_valu<D, N, MODE>), \
+                                                     64, 0);                                                \
+    if (e != hipSuccess || n <= 0) n = 4 * valu_waves_per_simd<D, N>();                                    \
+    break;
+    KRILL_OCC(1) KRILL_OCC(2) KRILL_OCC(3) KRILL_OCC(4) KRILL_OCC(5) KRILL_OCC(6) KRILL_OCC(7) KRILL_OCC(8)
+#undef KRILL_OCC
+    default: n = 8;
+  }
+  if (e != hipSuccess) (void)hipGetLastError();
+  return n;
+}
+
+int32_t valu_waves_per_cu(const PoolGeometry &g, int32_t NR) {
+  const int dsel = g.D == 64 ? 0 : g.D == 128 ? 1 : 2;
+  if (NR < 1 || NR > 8) return 8;
+  if (g.num_cus <= 0) {  // host-only pool: the design point
+    static const int est[3][9] = {{0, 12, 12, 12, 12, 12, 12, 12, 12},
+                                  {0, 12, 12, 12, 12, 12, 8, 8, 8},
+                                  {0, 8, 8, 8, 8, 8, 8, 8, 8}};
+    return est[dsel][NR];
+  }
+  static int cache[2][3][9] = {};  // [mode][D][NR], filled on first use per process
+  int &c = cache[g.mode == MODE_AFFINE][dsel][NR];
+  if (c == 0) {
+    int n = 8;
+    if (g.D == 64) n = g.mode == MODE_REF ? occupancy_nr<64, MODE_REF>(NR) : occupancy_nr<64, MODE_AFFINE>(NR);
+    else if (g.D == 128) n = g.mode == MODE_REF ? occupancy_nr<128, MODE_REF>(NR) : occupancy_nr<128, MODE_AFFINE>(NR);
+    else n = g.mode == MODE_REF ? occupancy_nr<256, MODE_REF>(NR) : occupancy_nr<256, MODE_AFFINE>(NR);
+    c = n;
+  }
+  return c;
+}
+
 hipError_t launch_attn_valu(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
                             hipStream_t st) {
   // one VGPR of block-table entries per wave
-  if (p.split_blocks < 1 || p.split_blocks > 64 || p.waves < 1) return hipErrorInvalidValue;
+  if (p.waves < 1 || (int64_t)p.waves * 64 < (int64_t)a.B * p.nb_cap) return hipErrorInvalidValue;
   const AttnArgs args = make_attn_args(g, layer, a, p);
   const dim3 grid((unsigned)p.waves, (unsigned)g.Hkv);
   switch (g.D) {

@@ -137,6 +137,8 @@ int32_t krill_pool_create(const krill_pool_desc *desc, krill_stream_t stream, kr
   if (!p->host_only) {
     hipError_t e = hipGetDevice(&p->device);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    e = hipDeviceGetAttribute(&g.num_cus, hipDeviceAttributeMultiprocessorCount, p->device);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(multiprocessor count)");
     void *mem = nullptr;
     e = hipMalloc(&mem, static_cast<size_t>(total));
     if (e != hipSuccess) {

@@ -390,11 +390,11 @@ __global__ __launch_bounds__(64) void k_attn_merge_split(AttnArgs a) {
   merge_slots<D>(a, part_index(a, b, hk, 0, 0) / a.NR, n_splits, r, out_row_base(a, b, hk, r, D));
 }
 
-// After the VALU kernel (flat block order, split_blocks blocks per wave):
-// sequence b's blocks are flat [s, s + nb), covered by waves s / PW ..
-// (s + nb - 1) / PW, whose partials sit in consecutive slots wave + b.  A
-// sequence inside one wave was written by the attention kernel; an empty one
-// gets zeros here.
+// After the VALU kernel (flat block order, T blocks split evenly over the
+// waves): sequence b's blocks are flat [s, s + nb), covered by waves
+// flat_wave_of(s) .. flat_wave_of(s + nb - 1), whose partials sit in
+// consecutive slots wave + b.  A sequence inside one wave was written by the
+// attention kernel; an empty one gets zeros here.
 template <int D>
 __global__ __launch_bounds__(64) void k_attn_merge_flat(AttnArgs a) {
   const int r = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
@@ -406,20 +406,10 @@ __global__ __launch_bounds__(64) void k_attn_merge_flat(AttnArgs a) {
     for (int e = 0; e < D / 64; ++e) store_out(a.out, obase + lane + 64 * e, 0.0f, a.out_dtype);
     return;
   }
-  // flat start of sequence b
-  int carry = 0, s = 0;
-  for (int c0 = 0; c0 <= b; c0 += 64) {
-    const int bb = c0 + lane;
-    const int nbv = bb < a.B ? seq_blocks(a, a.lens[bb]) : 0;
-    const int incl = wave_incl_scan(nbv) + carry;
-    if (b < c0 + 64) {
-      s = __builtin_amdgcn_readlane(incl - nbv, b - c0);
-      break;
-    }
-    carry = __builtin_amdgcn_readlane(incl, 63);
-  }
-  const int PW = a.split_blocks;
-  const int first = s / PW, last = (s + nb - 1) / PW;
+  int s = 0;
+  const int T = flat_total_and_start(a, b, s);
+  const int Wt = min(a.waves, T);  // waves that took part (each holds >= 1 block)
+  const int first = flat_wave_of(s, T, Wt), last = flat_wave_of(s + nb - 1, T, Wt);
   if (first == last) return;
   merge_slots<D>(a, (int64_t)hk * (a.waves + a.B) + first + b, last - first + 1, r, obase);
 }
@@ -577,16 +567,26 @@ int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq,
     p.nb_cap = p.max_splits * sb;
     p.slots = (int64_t)B * g.Hkv * p.max_splits;
   } else {
-    // VALU: the blocks of all sequences in flat order, split_blocks per wave
-    // (at most 64: one VGPR of block-table entries).  The automatic size
-    // aims at about 4096 waves when every sequence is max_seq_len long.
-    int32_t pw = split_blocks;
-    if (pw <= 0) pw = (int32_t)std::max<int64_t>(2, ((int64_t)B * nb_max * g.Hkv + 4095) / 4096);
-    pw = std::min(pw, 64);
-    p.split_blocks = pw;
+    // VALU: the blocks of all sequences in flat order, split evenly over a
+    // grid of waves per KV head.  Automatic: the GPU's resident wave
+    // capacity (every SIMD gets the same load, one round); with
+    // split_blocks set: enough waves for that many blocks each when every
+    // sequence is max_seq_len long.  Never more than 64 blocks per wave (one
+    // VGPR of block-table entries).
+    const int64_t tmax = (int64_t)B * nb_max;
+    int64_t waves;
+    if (split_blocks > 0) {
+      const int64_t pw = std::min(split_blocks, 64);
+      waves = (tmax + pw - 1) / pw;
+    } else {
+      const int64_t cus = g.num_cus > 0 ? g.num_cus : 256;
+      waves = std::max<int64_t>(1, cus * valu_waves_per_cu(g, p.NR) / g.Hkv);
+    }
+    waves = std::max<int64_t>(waves, (tmax + 63) / 64);
+    p.split_blocks = (int32_t)std::min<int64_t>(64, (tmax + waves - 1) / waves);
     p.max_splits = 0;
     p.nb_cap = nb_max;
-    p.waves = (int32_t)std::max<int64_t>(1, ((int64_t)B * nb_max + pw - 1) / pw);
+    p.waves = (int32_t)waves;
     p.slots = (int64_t)g.Hkv * (p.waves + B);
   }
   p.ws_bytes = ws_layout(p.slots, p.NR, g.D).total;

@@ -14,6 +14,7 @@ struct PoolGeometry {
   int32_t num_layers = 0, num_blocks = 0, Hkv = 0, D = 0, G = 1;
   int32_t mode = 0;           // MODE_REF / MODE_AFFINE
   int32_t in_dtype = 1;       // DT_F16 / DT_BF16
+  int32_t num_cus = 0;        // compute units of the pool's device (0: host-only pool)
 };
 
 struct AttnLaunch {
@@ -63,6 +64,11 @@ hipError_t launch_scatter(const PoolGeometry &g, int32_t layer, const void *keys
 hipError_t launch_copy_blocks(const PoolGeometry &g, const int32_t *src_dst, int32_t n, hipStream_t st);
 hipError_t launch_attention(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
                             hipStream_t st);
+
+// Resident waves per compute unit of the VALU decode kernel for (D, NR,
+// mode), from the runtime's occupancy query on a device pool, else the
+// register-budget design point.
+int32_t valu_waves_per_cu(const PoolGeometry &g, int32_t NR);
 
 // Per-configuration kernels, defined in the attention translation units.
 hipError_t launch_attn_valu(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
