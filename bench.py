@@ -47,6 +47,9 @@ def parse():
     ap.add_argument("--workload", default="qwen3-14b-b32", choices=sorted(WORKLOADS))
     ap.add_argument("--quant", default="affine_g64", choices=["affine_g64", "ref_row"])
     ap.add_argument("--split-blocks", type=int, default=0)
+    ap.add_argument("--unfused", action="store_true",
+                    help="step as two calls per layer (quantize-append, then decode attention) instead of the "
+                         "fused krill_decode_append_attention")
     ap.add_argument("--kernel-reps", type=int, default=5, help="repetitions of the attention-only timing loop")
     ap.add_argument("--cpu-baseline", type=int, default=1, help="1: time the CPU baseline sample on rank 0")
     ap.add_argument("--seed", type=int, default=20261203)
@@ -149,6 +152,20 @@ def main():
     outp, wsp = out.data_ptr(), ws.data_ptr()
     cur_len = [int(x) for x in lens0]
 
+    def fused_call(layer, mx):
+        # the token at position len - 1 (its slot reserved above) is written, then attended over
+        KL.check(lib.krill_decode_append_attention(h, layer, qp[layer], kp[layer], vp[layer], Hkv * D, D,
+                                                   d_tables.data_ptr(), d_lens.data_ptr(), B, max_blocks, mx, Hq,
+                                                   ctypes.c_float(scale), outp, KL.DTYPE_BF16, wsp, ws_bytes, sp))
+
+    def attn_call(layer, mx):
+        if args.unfused:
+            KL.check(lib.krill_decode_attention(h, layer, qp[layer], d_tables.data_ptr(), d_lens.data_ptr(), B,
+                                                max_blocks, mx, Hq, ctypes.c_float(scale), outp, KL.DTYPE_BF16,
+                                                wsp, ws_bytes, sp))
+        else:
+            fused_call(layer, mx)  # rewrites the same token: the pool does not change
+
     def step(i):
         j = i % NBUF
         if buf_events[j] is not None:
@@ -159,7 +176,8 @@ def main():
             ps[b, 0] = one_slot[0]
             cur_len[b] += 1
         KL.check(lib.krill_batch_tables(h, i32p(seqs_np), B, max_blocks, i32p(pt), i32p(pl)))
-        d_slots.copy_(pin_slots[j], non_blocking=True)
+        if args.unfused:
+            d_slots.copy_(pin_slots[j], non_blocking=True)
         d_tables.copy_(pin_tables[j], non_blocking=True)
         d_lens.copy_(pin_lens[j], non_blocking=True)
         ev = torch.cuda.Event()
@@ -167,10 +185,13 @@ def main():
         buf_events[j] = ev
         mx = max(cur_len)
         for layer in range(layers):
-            KL.check(lib.krill_quantize_append(h, layer, kp[layer], vp[layer], d_slots.data_ptr(), B, 1, sp))
-            KL.check(lib.krill_decode_attention(h, layer, qp[layer], d_tables.data_ptr(), d_lens.data_ptr(), B,
-                                                max_blocks, mx, Hq, ctypes.c_float(scale), outp, KL.DTYPE_BF16,
-                                                wsp, ws_bytes, sp))
+            if args.unfused:
+                KL.check(lib.krill_quantize_append(h, layer, kp[layer], vp[layer], d_slots.data_ptr(), B, 1, sp))
+                KL.check(lib.krill_decode_attention(h, layer, qp[layer], d_tables.data_ptr(), d_lens.data_ptr(),
+                                                    B, max_blocks, mx, Hq, ctypes.c_float(scale), outp,
+                                                    KL.DTYPE_BF16, wsp, ws_bytes, sp))
+            else:
+                fused_call(layer, mx)
 
     for i in range(args.warmup):
         step(i)
@@ -196,25 +217,24 @@ def main():
     gbs_step = step_bytes / (ms_step * 1e-3) / 1e9
     tok_s = B / (ms_step * 1e-3)
 
-    # ---- dominant kernel alone: paged decode attention (+ its split merge), all layers
+    # ---- dominant kernel alone: paged decode attention (+ its split merge; with the append fused unless
+    # --unfused), all layers
     mx = max(cur_len)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     for layer in range(layers):  # warm
-        KL.check(lib.krill_decode_attention(h, layer, qp[layer], d_tables.data_ptr(), d_lens.data_ptr(), B,
-                                            max_blocks, mx, Hq, ctypes.c_float(scale), outp, KL.DTYPE_BF16, wsp,
-                                            ws_bytes, sp))
+        attn_call(layer, mx)
     torch.cuda.synchronize()
     e0.record(stream)
     for _ in range(args.kernel_reps):
         for layer in range(layers):
-            KL.check(lib.krill_decode_attention(h, layer, qp[layer], d_tables.data_ptr(), d_lens.data_ptr(), B,
-                                                max_blocks, mx, Hq, ctypes.c_float(scale), outp, KL.DTYPE_BF16,
-                                                wsp, ws_bytes, sp))
+            attn_call(layer, mx)
     e1.record(stream)
     torch.cuda.synchronize()
     attn_ms = e0.elapsed_time(e1) / (args.kernel_reps * layers)
     launch_bytes = sum(cur_len) * per_tok + qo_bytes_layer
+    if not args.unfused:  # the new token: bf16 K/V rows in, quantized bytes out
+        launch_bytes += B * (2 * Hkv * D * 2 + per_tok)
     achieved = launch_bytes / (attn_ms * 1e-3) / 1e9
 
     # ---- CPU baseline: the reference's per-step algorithm on the host cores
@@ -240,7 +260,8 @@ def main():
         "config": {
             "workload": f"{args.workload}: {layers} layers, Hq {Hq}, Hkv {Hkv}, D {D}, B {B}, "
                         f"context U[{lo},{hi}], 64-token blocks (permuted pool), {args.quant} int8, "
-                        "bf16 N(0,1) inputs; step = per layer quantize-append 1 token/seq + paged decode attention",
+                        "bf16 N(0,1) inputs; step = per layer quantize-append 1 token/seq + paged decode attention"
+                        + (" (two calls)" if args.unfused else " (one fused call)"),
             "layers": layers, "Hq": Hq, "Hkv": Hkv, "head_dim": D, "batch": B, "quant": args.quant,
             "context_mean": float(np.mean(lens0)), "num_blocks": num_blocks,
         },
@@ -250,7 +271,9 @@ def main():
         "wall_s_timed": round(wall, 4),
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged decode attention call (k_attn_valu + k_attn_merge_flat), one layer",
+            "kernel": ("paged decode attention call (k_attn_valu + k_attn_merge_flat), one layer" if args.unfused
+                       else "fused append + paged decode attention call (k_attn_valu + k_attn_merge_flat), "
+                            "one layer"),
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -266,10 +289,11 @@ def main():
 
 
 def measured_traffic(args):
-    """HBM bytes per decode-attention call from the committed rocprofv3 PMC
-    summary (FETCH_SIZE + WRITE_SIZE, calibrated against a plain copy), when
-    it was taken on this workload; None otherwise."""
-    path = os.path.join(ROOT, "profiles", f"decode_attn_{args.workload}_{args.quant}_traffic.json")
+    """HBM bytes per call of the timed entry point from the committed
+    rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, calibrated against a plain
+    copy), when it was taken on this workload; None otherwise."""
+    call = "decode_attn" if args.unfused else "decode_append_attn"
+    path = os.path.join(ROOT, "profiles", f"{call}_{args.workload}_{args.quant}_traffic.json")
     try:
         with open(path) as f:
             rec = json.load(f)

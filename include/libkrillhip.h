@@ -237,6 +237,24 @@ int32_t krill_decode_attention(krill_pool_t pool, int32_t layer, const void *dev
                                int32_t max_blocks, int32_t max_seq_len, int32_t Hq, float scale,
                                void *dev_out, int32_t out_dtype, void *dev_ws, size_t ws_bytes,
                                krill_stream_t stream);
+/* Decode step with the append fused: krill_quantize_append_strided of each
+ * sequence's newest token followed by krill_decode_attention, in one
+ * attention launch (plus the merge).  dev_k_new / dev_v_new: rows [b][h][D]
+ * in in_dtype at element strides (stride_b, stride_h), d contiguous (e.g.
+ * (Hkv*D, D) for [B][Hkv][1][D]).  The token is written at position
+ * seq_lens[b] - 1 of the sequence's table, i.e. the slot
+ * krill_seq_reserve_append handed out this step; the pool bytes and the
+ * output equal those of the two separate calls.  A sequence of length 0, or
+ * whose last position lies beyond max_seq_len or the table width, gets no
+ * token written.  Replaces the update + SDPA pair of a decode step
+ * (QuantizedKVCache.swift:49-74 followed by Attention.swift:95-98). */
+int32_t krill_decode_append_attention(krill_pool_t pool, int32_t layer, const void *dev_q,
+                                      const void *dev_k_new, const void *dev_v_new, int64_t stride_b,
+                                      int64_t stride_h, const int32_t *dev_block_tables,
+                                      const int32_t *dev_seq_lens, int32_t B, int32_t max_blocks,
+                                      int32_t max_seq_len, int32_t Hq, float scale, void *dev_out,
+                                      int32_t out_dtype, void *dev_ws, size_t ws_bytes,
+                                      krill_stream_t stream);
 /* Speculative-verify / chunked-prefill attention: Lq new query rows per
  * sequence, already appended, causal inside the window (row j sees tokens
  * [0, len - Lq + j]; BatchedDecode.swift:299-312, LlamaModel.swift:186-202).

@@ -151,6 +151,8 @@ SIGNATURES = {
     "krill_decode_attention": [P, I32, P, P, P, I32, I32, I32, I32, ctypes.c_float, P, I32, P, ctypes.c_size_t, P],
     "krill_verify_attention": [P, I32, P, I32, P, P, I32, I32, I32, I32, ctypes.c_float, P, I32, P,
                                ctypes.c_size_t, P],
+    "krill_decode_append_attention": [P, I32, P, P, P, I64, I64, P, P, I32, I32, I32, I32, ctypes.c_float, P,
+                                      I32, P, ctypes.c_size_t, P],
 }
 _RESTYPE = {"krill_last_error": ctypes.c_char_p}
 

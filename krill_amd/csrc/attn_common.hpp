@@ -43,6 +43,8 @@ struct AttnArgs {
   float *ws_ml;
   void *out;  // [B][Hq][Lq][D]
   int32_t out_dtype;
+  const uint16_t *k_new, *v_new;  // fused append of the newest token (null: none)
+  int64_t kn_sb, kn_sh;           // their element strides (batch, head)
 };
 
 inline AttnArgs make_attn_args(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p) {
@@ -73,6 +75,10 @@ inline AttnArgs make_attn_args(const PoolGeometry &g, int32_t layer, const AttnL
   r.ws_ml = reinterpret_cast<float *>(base + w.ml);
   r.out = a.out;
   r.out_dtype = a.out_dtype;
+  r.k_new = static_cast<const uint16_t *>(a.k_new);
+  r.v_new = static_cast<const uint16_t *>(a.v_new);
+  r.kn_sb = a.kn_sb;
+  r.kn_sh = a.kn_sh;
   return r;
 }
 

@@ -113,6 +113,51 @@ constexpr int valu_waves_per_simd() {
   return D <= 64 || (D == 128 && NR <= 5) ? 3 : 2;
 }
 
+// The step's new K/V rows of sequence b, head hk: lane l loads the raw
+// elements d = l*E .. l*E+E-1 (E = D/64), the quantizer's lane ownership.
+template <int D>
+__device__ __forceinline__ void load_new_rows(const AttnArgs &a, int b, int hk, uint16_t (&rk)[D / 64],
+                                              uint16_t (&rv)[D / 64]) {
+  constexpr int E = D / 64;
+  const int64_t off = (int64_t)b * a.kn_sb + (int64_t)hk * a.kn_sh + (threadIdx.x & 63) * E;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    rk[e] = a.k_new[off + e];
+    rv[e] = a.v_new[off + e];
+  }
+}
+
+// Quantizes rows loaded by load_new_rows and writes them as token t of
+// physical block `phys`: the same quantize_row / store_row as the append
+// kernels, so the bytes are the same.
+template <int D, int MODE, int DT>
+__device__ __forceinline__ void write_new_rows(const AttnArgs &a, int hk, int phys, int t,
+                                               const uint16_t (&rk)[D / 64], const uint16_t (&rv)[D / 64]) {
+  constexpr int E = D / 64;
+  const int lane = threadIdx.x & 63;
+  float xk[E], xv[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    xk[e] = elem_to_f32<DT>(rk[e]);
+    xv[e] = elem_to_f32<DT>(rv[e]);
+  }
+  uint8_t qk[E], qv[E];
+  float ks, kz, vs, vz;
+  quantize_row<D, MODE, DT>(xk, qk, ks, kz);
+  quantize_row<D, MODE, DT>(xv, qv, vs, vz);
+  uint8_t *reg = head_region(a.lv, phys, hk);
+  store_row<D, MODE>(reg, 0, t, lane, qk, ks, kz);
+  store_row<D, MODE>(reg, 1, t, lane, qv, vs, vz);
+}
+
+// Whether the wave reading flat blocks up to iend (exclusive) writes the
+// newest token of a sequence of length len whose nbs read blocks start at
+// flat index ss: it reads the last of them, and that block holds position
+// len - 1 (not so for len = 0, or when the blocks read stop short of it).
+__device__ __forceinline__ bool owns_newest(int len, int nbs, int ss, int iend) {
+  return nbs > 0 && ss + nbs - 1 < iend && ((len - 1) >> 6) == nbs - 1;
+}
+
 template <int D, int NR, int MODE>
 __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_valu(AttnArgs a) {
   constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
@@ -172,11 +217,36 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   if (b < 0) return;
   auto seq_len = [&](int bs) -> int { return bs - c0 < 64 ? __builtin_amdgcn_readlane(lenv, bs - c0) : a.lens[bs]; };
 
+  // Decode step with the append fused: the wave that reads a sequence's last
+  // block writes the sequence's newest token there (position len - 1) and
+  // waits for the stores before its first pool load, so it reads the token
+  // back like any cached one; no other wave reads that block for this head.
+  // The rows of the first such sequence are loaded here, alongside the block
+  // table; further ones (short sequences) one after another below.
+  constexpr int E = D / 64;
+  int own_b = -1, own_ss = 0;
+  uint16_t rk[E], rv[E];
+  if (a.k_new) {
+    int bs = b, ss = s;
+    while (bs < a.B && ss < iend) {
+      const int len = seq_len(bs), nbs = seq_blocks(a, len);
+      if (owns_newest(len, nbs, ss, iend)) {
+        own_b = bs;
+        own_ss = ss;
+        break;
+      }
+      ss += nbs;
+      ++bs;
+    }
+    if (own_b >= 0) load_new_rows<D>(a, own_b, hk, rk, rv);
+  }
+
   // Physical block ids of flat blocks i0 .. iend-1 (at most 64): lane j holds
   // the entry of block i0 + j, read back with v_readlane, so no table load
   // sits between a prefetch and its use (a load there would have to drain the
   // prefetch before its value could move to a scalar register).
   int tab = 0, iend_eff = iend;
+  bool tab_ok = false;  // the table entry names a block of the pool
   {
     const int f = i0 + lane;
     int bs = b, ss = s;
@@ -184,12 +254,37 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       const int nbs = seq_blocks(a, seq_len(bs));
       if (f < iend && f >= ss && f < ss + nbs) {
         const int phys = a.tables[(int64_t)bs * a.max_blocks + (f - ss)];
-        tab = (unsigned)phys < (unsigned)a.lv.num_blocks ? phys : 0;
+        tab_ok = (unsigned)phys < (unsigned)a.lv.num_blocks;
+        tab = tab_ok ? phys : 0;
       }
       ss += nbs;
       ++bs;
     }
     if (ss < iend) iend_eff = ss;  // the last sequence ends inside this range
+  }
+
+  if (own_b >= 0) {
+    const uint64_t ok = __ballot(tab_ok);
+    bool wrote = false;
+    int bs = own_b, ss = own_ss;
+    while (bs < a.B && ss < iend) {
+      const int len = seq_len(bs), nbs = seq_blocks(a, len);
+      if (owns_newest(len, nbs, ss, iend)) {
+        if (bs != own_b) load_new_rows<D>(a, bs, hk, rk, rv);
+        const int f = ss + nbs - 1;  // flat index of the sequence's last block
+        if ((ok >> (f - i0)) & 1) {
+          const int phys = __builtin_amdgcn_readlane(tab, f - i0);
+          if (a.q_dtype == DT_BF16)
+            write_new_rows<D, MODE, DT_BF16>(a, hk, phys, (len - 1) & 63, rk, rv);
+          else
+            write_new_rows<D, MODE, DT_F16>(a, hk, phys, (len - 1) & 63, rk, rv);
+          wrote = true;
+        }
+      }
+      ss += nbs;
+      ++bs;
+    }
+    if (wrote) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
   auto rsrc_of = [&](int i) -> __amdgpu_buffer_rsrc_t {
     const bool ok = i < iend_eff;

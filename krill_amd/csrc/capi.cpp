@@ -459,10 +459,16 @@ int32_t krill_attention_workspace_size(krill_pool_t pool, int32_t B, int32_t Hq,
   return KRILL_OK;
 }
 
+struct NewTokens {  // decode step with the append fused (all null/zero: none)
+  const void *k = nullptr, *v = nullptr;
+  int64_t sb = 0, sh = 0;
+};
+
 static int32_t run_attention(krill_pool_t pool, int32_t layer, const void *dev_q, int32_t Lq,
                              const int32_t *dev_block_tables, const int32_t *dev_seq_lens, int32_t B,
                              int32_t max_blocks, int32_t max_seq_len, int32_t Hq, float scale, void *dev_out,
-                             int32_t out_dtype, void *dev_ws, size_t ws_bytes, krill_stream_t stream) {
+                             int32_t out_dtype, void *dev_ws, size_t ws_bytes, krill_stream_t stream,
+                             const NewTokens &nt = NewTokens()) {
   if (int32_t rc = check_device_pool(pool, layer)) return rc;
   if (B < 0 || max_blocks < 0 || max_seq_len < 0) return fail(KRILL_E_INVAL, "negative B, max_blocks or length");
   if (B == 0) return KRILL_OK;
@@ -496,6 +502,10 @@ static int32_t run_attention(krill_pool_t pool, int32_t layer, const void *dev_q
   a.ws_bytes = ws_bytes;
   a.split_blocks = plan.split_blocks;
   a.path = pool->opt_path;
+  a.k_new = nt.k;
+  a.v_new = nt.v;
+  a.kn_sb = nt.sb;
+  a.kn_sh = nt.sh;
   DeviceGuard dg(pool->device);
   hipStream_t st = pick_stream(pool, stream);
   if (int32_t rc = flush_pending(pool, st)) return rc;
@@ -511,6 +521,24 @@ int32_t krill_decode_attention(krill_pool_t pool, int32_t layer, const void *dev
   krill::clear_error();
   return run_attention(pool, layer, dev_q, 1, dev_block_tables, dev_seq_lens, B, max_blocks, max_seq_len, Hq, scale,
                        dev_out, out_dtype, dev_ws, ws_bytes, stream);
+}
+
+int32_t krill_decode_append_attention(krill_pool_t pool, int32_t layer, const void *dev_q, const void *dev_k_new,
+                                      const void *dev_v_new, int64_t stride_b, int64_t stride_h,
+                                      const int32_t *dev_block_tables, const int32_t *dev_seq_lens, int32_t B,
+                                      int32_t max_blocks, int32_t max_seq_len, int32_t Hq, float scale,
+                                      void *dev_out, int32_t out_dtype, void *dev_ws, size_t ws_bytes,
+                                      krill_stream_t stream) {
+  krill::clear_error();
+  if (B > 0 && (!dev_k_new || !dev_v_new)) return fail(KRILL_E_INVAL, "NULL new K/V pointer");
+  if (stride_b < 0 || stride_h < 0) return fail(KRILL_E_INVAL, "negative stride");
+  NewTokens nt;
+  nt.k = dev_k_new;
+  nt.v = dev_v_new;
+  nt.sb = stride_b;
+  nt.sh = stride_h;
+  return run_attention(pool, layer, dev_q, 1, dev_block_tables, dev_seq_lens, B, max_blocks, max_seq_len, Hq, scale,
+                       dev_out, out_dtype, dev_ws, ws_bytes, stream, nt);
 }
 
 int32_t krill_verify_attention(krill_pool_t pool, int32_t layer, const void *dev_q, int32_t Lq,

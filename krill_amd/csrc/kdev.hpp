@@ -239,4 +239,107 @@ __device__ __forceinline__ void settle(uint4 &x) {
 }
 __device__ __forceinline__ void settle(uint32_t &x) { asm volatile("; settle %0" : "+v"(x)); }
 
+// ---------------------------------------------------------- row quantizer
+// Wave-collective quantization of one token row (K or V of one head): lane l
+// owns the E = D/64 consecutive values d = l*E .. l*E+E-1, given as fp32
+// widened from the input dtype DT.  Every kernel that writes new tokens into
+// the pool goes through this function, so all of them store the same bytes.
+// MODE_REF: QuantizedKVCache.quantizePerHead
+// (Sources/KrillCache/QuantizedKVCache.swift:181-197):
+//   mn, mx = min/max over D; scale = f32(dt(mx - mn)) / 255; safe = max(scale, 1e-8)
+//   q = u8(trunc(clip(f32(dt(x - mn)) / safe, 0, 255))); (scale, zero) = (safe, mn)
+// MODE_AFFINE (group 64): values cast to fp16, per group
+//   s = max((max-min)/255, 1e-7) signed toward the larger-magnitude edge,
+//   q0 = rint(edge/s), s = edge/q0 and bias = edge when q0 != 0 (else bias 0),
+//   q = clip(rint((w - bias)/s), 0, 255); (scale, zero) = (s, bias).
+template <int D, int MODE, int DT>
+__device__ __forceinline__ void quantize_row(const float (&x)[D / 64], uint8_t (&qb)[D / 64], float &scale,
+                                             float &zero) {
+  constexpr int E = D / 64;
+  if constexpr (MODE == MODE_REF) {
+    float mn = x[0], mx = x[0];
+#pragma unroll
+    for (int e = 1; e < E; ++e) {
+      mn = fminf(mn, x[e]);
+      mx = fmaxf(mx, x[e]);
+    }
+    mn = wave_min_range<1, 32>(mn);
+    mx = wave_max_range<1, 32>(mx);
+    const float sc = round_dt<DT>(mx - mn) / 255.0f;
+    const float safe = sc > 1e-8f ? sc : 1e-8f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      float n = round_dt<DT>(x[e] - mn) / safe;
+      if (n < 0.0f) n = 0.0f;
+      if (n > 255.0f) n = 255.0f;
+      qb[e] = (uint8_t)(uint32_t)n;
+    }
+    scale = safe;
+    zero = mn;
+  } else {
+    constexpr int LPG = 64 / E;  // lanes per group of 64
+    float w[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) w[e] = DT == DT_F16 ? x[e] : f16_bits_to_f32(f32_to_f16_bits(x[e]));
+    float wmin = w[0], wmax = w[0];
+#pragma unroll
+    for (int e = 1; e < E; ++e) {
+      wmin = fminf(wmin, w[e]);
+      wmax = fmaxf(wmax, w[e]);
+    }
+    wmin = wave_min_range<1, LPG / 2>(wmin);
+    wmax = wave_max_range<1, LPG / 2>(wmax);
+    const bool side = fabsf(wmin) > fabsf(wmax);
+    float s = (wmax - wmin) / 255.0f;
+    if (!(s > 1e-7f)) s = 1e-7f;
+    s = side ? s : -s;
+    const float edge = side ? wmin : wmax;
+    const float q0 = rintf(edge / s);
+    float bias = 0.0f;
+    if (q0 != 0.0f) {
+      s = edge / q0;
+      bias = edge;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      float n = rintf((w[e] - bias) / s);
+      if (n > 255.0f) n = 255.0f;
+      if (n < 0.0f) n = 0.0f;
+      qb[e] = (uint8_t)(uint32_t)n;
+    }
+    scale = s;
+    zero = bias;
+  }
+}
+
+// Stores a row quantized by quantize_row (kv 0: K, 1: V) as token t of the
+// head region `reg`, with its fp16 (scale, zero) pair(s).
+template <int D, int MODE>
+__device__ __forceinline__ void store_row(uint8_t *reg, int kv, int t, int lane, const uint8_t (&qb)[D / 64],
+                                          float scale, float zero) {
+  constexpr int E = D / 64;
+  constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
+  const int d0 = lane * E;
+  if (kv == 0) {
+    uint8_t *dst = reg + k_byte(t, d0);
+    if constexpr (E == 1) {
+      dst[0] = qb[0];
+    } else if constexpr (E == 2) {
+      *reinterpret_cast<uint16_t *>(dst) = (uint16_t)(qb[0] | (qb[1] << 8));
+    } else {
+      *reinterpret_cast<uint32_t *>(dst) =
+          (uint32_t)qb[0] | ((uint32_t)qb[1] << 8) | ((uint32_t)qb[2] << 16) | ((uint32_t)qb[3] << 24);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) reg[v_byte(D, t, d0 + e)] = qb[e];
+  }
+  const int g = MODE == MODE_AFFINE ? d0 / 64 : 0;
+  if ((d0 & (MODE == MODE_AFFINE ? 63 : (D - 1))) == 0) {
+    const uint32_t meta = (uint32_t)f32_to_f16_bits(scale) | ((uint32_t)f32_to_f16_bits(zero) << 16);
+    const int off = (kv ? vm_offset(D, G) : km_offset(D)) + ((t * G + g) << 2);
+    *reinterpret_cast<uint32_t *>(reg + off) = meta;
+  }
+}
+
 }  // namespace krill

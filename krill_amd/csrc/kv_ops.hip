@@ -24,16 +24,9 @@ static inline LayerView layer_view(const PoolGeometry &g, int32_t layer) {
 }
 
 // ---------------------------------------------------------------------------
-// Fused quantize + paged append.
-// Reference semantics (MODE_REF): QuantizedKVCache.quantizePerHead
-// (Sources/KrillCache/QuantizedKVCache.swift:181-197):
-//   mn, mx = min/max over D; scale = f32(dt(mx - mn)) / 255; safe = max(scale, 1e-8)
-//   q = u8(trunc(clip(f32(dt(x - mn)) / safe, 0, 255))); stores f16(safe), f16(mn)
-// Affine group-64 (MODE_AFFINE): values cast to fp16, per 64-group
-//   s = max((max-min)/255, 1e-7) signed toward the larger-magnitude edge,
-//   q0 = rint(edge/s), s = edge/q0 and bias = edge when q0 != 0 (else bias 0),
-//   q = min(rint((w - bias)/s), 255); fp16 scale/bias.
-// One wave64 per (row, K|V); each lane owns D/64 consecutive elements.
+// Fused quantize + paged append (quantize_row / store_row: the reference's
+// row quantizer or the affine group-64 one).  One wave64 per (row, K|V);
+// each lane owns D/64 consecutive elements.
 // ---------------------------------------------------------------------------
 template <int D, int MODE, int DT>
 __global__ __launch_bounds__(256) void k_quantize_append(LayerView lv, const uint16_t *__restrict__ k,
@@ -42,7 +35,6 @@ __global__ __launch_bounds__(256) void k_quantize_append(LayerView lv, const uin
                                                          const int32_t *__restrict__ slots, int32_t B,
                                                          int32_t L, int32_t Hkv) {
   constexpr int E = D / 64;
-  constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
   const int lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int64_t nrows = (int64_t)B * Hkv * L;
@@ -56,91 +48,43 @@ __global__ __launch_bounds__(256) void k_quantize_append(LayerView lv, const uin
   if (slot < 0) return;
   const int blk = slot >> 6, t = slot & 63;
   if (blk >= lv.num_blocks) return;
-  const uint16_t *src = (kv ? v : k) + (int64_t)b * sb + (int64_t)h * sh + (int64_t)l * sl;
-  const int d0 = lane * E;
-
+  const uint16_t *src = (kv ? v : k) + (int64_t)b * sb + (int64_t)h * sh + (int64_t)l * sl + lane * E;
   float x[E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) x[e] = elem_to_f32<DT>(src[d0 + e]);
-
+  for (int e = 0; e < E; ++e) x[e] = elem_to_f32<DT>(src[e]);
   uint8_t qb[E];
   float scale, zero;
-  if constexpr (MODE == MODE_REF) {
-    float mn = x[0], mx = x[0];
-#pragma unroll
-    for (int e = 1; e < E; ++e) {
-      mn = fminf(mn, x[e]);
-      mx = fmaxf(mx, x[e]);
-    }
-    mn = wave_min_range<1, 32>(mn);
-    mx = wave_max_range<1, 32>(mx);
-    const float sc = round_dt<DT>(mx - mn) / 255.0f;
-    const float safe = sc > 1e-8f ? sc : 1e-8f;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      float n = round_dt<DT>(x[e] - mn) / safe;
-      if (n < 0.0f) n = 0.0f;
-      if (n > 255.0f) n = 255.0f;
-      qb[e] = (uint8_t)(uint32_t)n;
-    }
-    scale = safe;
-    zero = mn;
-  } else {
-    constexpr int LPG = 64 / E;  // lanes per group of 64
-    float w[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) w[e] = DT == DT_F16 ? x[e] : f16_bits_to_f32(f32_to_f16_bits(x[e]));
-    float wmin = w[0], wmax = w[0];
-#pragma unroll
-    for (int e = 1; e < E; ++e) {
-      wmin = fminf(wmin, w[e]);
-      wmax = fmaxf(wmax, w[e]);
-    }
-    wmin = wave_min_range<1, LPG / 2>(wmin);
-    wmax = wave_max_range<1, LPG / 2>(wmax);
-    const bool side = fabsf(wmin) > fabsf(wmax);
-    float s = (wmax - wmin) / 255.0f;
-    if (!(s > 1e-7f)) s = 1e-7f;
-    s = side ? s : -s;
-    const float edge = side ? wmin : wmax;
-    const float q0 = rintf(edge / s);
-    float bias = 0.0f;
-    if (q0 != 0.0f) {
-      s = edge / q0;
-      bias = edge;
-    }
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      float n = rintf((w[e] - bias) / s);
-      if (n > 255.0f) n = 255.0f;
-      if (n < 0.0f) n = 0.0f;
-      qb[e] = (uint8_t)(uint32_t)n;
-    }
-    scale = s;
-    zero = bias;
-  }
+  quantize_row<D, MODE, DT>(x, qb, scale, zero);
+  store_row<D, MODE>(head_region(lv, blk, h), kv, t, lane, qb, scale, zero);
+}
 
-  uint8_t *reg = head_region(lv, blk, h);
-  if (kv == 0) {
-    uint8_t *dst = reg + k_byte(t, d0);
-    if constexpr (E == 1) {
-      dst[0] = qb[0];
-    } else if constexpr (E == 2) {
-      *reinterpret_cast<uint16_t *>(dst) = (uint16_t)(qb[0] | (qb[1] << 8));
-    } else {
-      *reinterpret_cast<uint32_t *>(dst) =
-          (uint32_t)qb[0] | ((uint32_t)qb[1] << 8) | ((uint32_t)qb[2] << 16) | ((uint32_t)qb[3] << 24);
-    }
-  } else {
+// Append of each sequence's newest token, its position len - 1 located
+// through the block table (the decode step: lens count the new token).  A
+// token outside the blocks the attention reads (len = 0, or a block beyond
+// the table width / max_seq_len) is not written; this is the rule the fused
+// decode kernel follows too.  One wave64 per (sequence, head, K|V).
+template <int D, int MODE, int DT>
+__global__ __launch_bounds__(256) void k_append_newest(AttnArgs a) {
+  constexpr int E = D / 64;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wave >= 2 * (int64_t)a.B * a.Hkv) return;
+  const int kv = (int)(wave & 1);
+  const int h = (int)((wave >> 1) % a.Hkv);
+  const int b = (int)((wave >> 1) / a.Hkv);
+  const int len = a.lens[b];
+  const int nb = seq_blocks(a, len);
+  if (nb == 0 || ((len - 1) >> 6) != nb - 1) return;
+  const int phys = a.tables[(int64_t)b * a.max_blocks + nb - 1];
+  if ((unsigned)phys >= (unsigned)a.lv.num_blocks) return;
+  const uint16_t *src = (kv ? a.v_new : a.k_new) + (int64_t)b * a.kn_sb + (int64_t)h * a.kn_sh + lane * E;
+  float x[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) reg[v_byte(D, t, d0 + e)] = qb[e];
-  }
-  const int g = MODE == MODE_AFFINE ? d0 / 64 : 0;
-  if ((d0 & (MODE == MODE_AFFINE ? 63 : (D - 1))) == 0) {
-    const uint32_t meta = (uint32_t)f32_to_f16_bits(scale) | ((uint32_t)f32_to_f16_bits(zero) << 16);
-    const int off = (kv ? vm_offset(D, G) : km_offset(D)) + ((t * G + g) << 2);
-    *reinterpret_cast<uint32_t *>(reg + off) = meta;
-  }
+  for (int e = 0; e < E; ++e) x[e] = elem_to_f32<DT>(src[e]);
+  uint8_t qb[E];
+  float scale, zero;
+  quantize_row<D, MODE, DT>(x, qb, scale, zero);
+  store_row<D, MODE>(head_region(a.lv, phys, h), kv, (len - 1) & 63, lane, qb, scale, zero);
 }
 
 // ---------------------------------------------------------------------------
@@ -609,9 +553,35 @@ hipError_t launch_attn_merge(const PoolGeometry &g, int32_t layer, const AttnLau
   return hipGetLastError();
 }
 
+// The newest-token append as its own launch (the MFMA path does not fuse it).
+static hipError_t launch_append_newest(const PoolGeometry &g, int32_t layer, const AttnLaunch &a,
+                                       const AttnPlan &p, hipStream_t st) {
+  const int64_t waves = 2 * (int64_t)a.B * g.Hkv;
+  const AttnArgs args = make_attn_args(g, layer, a, p);
+  const dim3 grid(wave_blocks(waves)), block(256);
+  KRILL_DISPATCH_D(g.D, {
+    if (g.mode == MODE_REF) {
+      if (g.in_dtype == DT_BF16)
+        k_append_newest<D, MODE_REF, DT_BF16><<<grid, block, 0, st>>>(args);
+      else
+        k_append_newest<D, MODE_REF, DT_F16><<<grid, block, 0, st>>>(args);
+    } else {
+      if (g.in_dtype == DT_BF16)
+        k_append_newest<D, MODE_AFFINE, DT_BF16><<<grid, block, 0, st>>>(args);
+      else
+        k_append_newest<D, MODE_AFFINE, DT_F16><<<grid, block, 0, st>>>(args);
+    }
+  });
+  return hipGetLastError();
+}
+
 hipError_t launch_attention(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
                             hipStream_t st) {
   if (a.B == 0) return hipSuccess;
+  if (a.k_new && p.use_mfma) {
+    hipError_t e = launch_append_newest(g, layer, a, p, st);
+    if (e != hipSuccess) return e;
+  }
   hipError_t e = p.use_mfma ? launch_attn_mfma(g, layer, a, p, st) : launch_attn_valu(g, layer, a, p, st);
   if (e != hipSuccess) return e;
   return launch_attn_merge(g, layer, a, p, st);

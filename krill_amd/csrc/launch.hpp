@@ -29,6 +29,11 @@ struct AttnLaunch {
   size_t ws_bytes;
   int32_t split_blocks;  // 0 = automatic
   int32_t path;          // 0 auto, 1 VALU, 2 MFMA
+  // decode step with the append fused: each sequence's newest token (K/V
+  // rows [b][h][D] at element strides kn_sb, kn_sh) is written at position
+  // len - 1 before it is read; null for attention over the cache as it is
+  const void *k_new = nullptr, *v_new = nullptr;
+  int64_t kn_sb = 0, kn_sh = 0;
 };
 
 // Splits/rows plan shared by the workspace query and the launch.

@@ -340,6 +340,40 @@ class KVPool:
                                                    out.data_ptr(), code, ws.data_ptr(), ws.numel(), st))
         return out
 
+    def decode_append_attention(self, layer: int, q, k_new, v_new, tables, lens, max_seq_len: int, scale: float,
+                                out_dtype=None, ws=None, out=None, stream=None):
+        """Decode step with the append fused: writes each sequence's newest token
+        (k_new, v_new: [B, Hkv, 1, D] or [B, Hkv, D] in in_dtype) at position
+        lens[b] - 1, then attends q [B, Hq, 1, D] over the cache.  Same pool bytes
+        and output as quantize_append at those slots followed by attention."""
+        torch = _torch()
+        B, Hq, Lq, D = q.shape
+        if Lq != 1:
+            raise ValueError("decode_append_attention takes one query row per sequence")
+        self._check_dev("q", q, self.in_dtype)
+        Bt, mb = self._tables(tables, lens)
+        if Bt != B or D != self.head_dim:
+            raise ValueError("q batch/head_dim does not match the tables/pool")
+        H = self.num_kv_heads
+        for name, t in (("k_new", k_new), ("v_new", v_new)):
+            self._check_dev(name, t, self.in_dtype)
+            if t.numel() != B * H * D or t.shape[0] != B or t.shape[1] != H:
+                raise ValueError(f"{name} has shape {tuple(t.shape)}, expected [{B}, {H}, (1,) {D}]")
+        out_dtype = torch.float32 if out_dtype is None else out_dtype
+        code = _dtype_code(out_dtype)
+        if out is None:
+            out = torch.empty((B, Hq, 1, D), dtype=out_dtype, device=q.device)
+        else:
+            self._check_dev("out", out, out_dtype, (B, Hq, 1, D))
+        need = self.workspace_size(B, Hq, 1, max_seq_len)
+        if ws is None or ws.numel() < need:
+            ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+        L.check(L.lib().krill_decode_append_attention(
+            self._h, layer, q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), H * D, D, tables.data_ptr(),
+            lens.data_ptr(), B, mb, max_seq_len, Hq, float(scale), out.data_ptr(), code, ws.data_ptr(),
+            ws.numel(), self._stream(stream)))
+        return out
+
 
 def prefix_key(model_id: str, media_hash, dtype_tag: int, tokens) -> int:
     """PrefixCache.cacheKey (PrefixCache.swift:511-532) as computed by the library."""
