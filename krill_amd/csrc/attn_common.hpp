@@ -124,18 +124,20 @@ __device__ __forceinline__ int wave_allsum_int(int v) {
 }
 
 // Flat block order of the VALU path: the blocks of sequences 0, 1, .., B-1
-// one after another, split evenly over W = min(grid waves, T) waves (wave w
-// holds flat blocks [ceil(w T / W), ceil((w+1) T / W)), at least one).  Returns the total T and sets
-// start_out to the flat index of sequence b's first block.  Uniform across
-// the wave.
-__device__ __forceinline__ int flat_total_and_start(const AttnArgs &a, int b, int &start_out) {
+// one after another (T blocks per KV head).  Returns T and sets start_out /
+// nb_out to the flat index of sequence b's first block and its block count.
+// Uniform across the wave; one round of lens loads.
+__device__ __forceinline__ int flat_total_and_start(const AttnArgs &a, int b, int &start_out, int &nb_out) {
   const int lane = threadIdx.x & 63;
   int carry = 0;
   for (int c0 = 0; c0 < a.B; c0 += 64) {
     const int bb = c0 + lane;
     const int nbv = bb < a.B ? seq_blocks(a, a.lens[bb]) : 0;
     const int incl = wave_incl_scan(nbv) + carry;
-    if (b >= c0 && b < c0 + 64) start_out = __builtin_amdgcn_readlane(incl - nbv, b - c0);
+    if (b >= c0 && b < c0 + 64) {
+      start_out = __builtin_amdgcn_readlane(incl - nbv, b - c0);
+      nb_out = __builtin_amdgcn_readlane(nbv, b - c0);
+    }
     carry = __builtin_amdgcn_readlane(incl, 63);
   }
   return carry;

@@ -269,11 +269,12 @@ __global__ __launch_bounds__(256) void k_copy_pairs(uint8_t *base, int64_t layer
 // ---------------------------------------------------------------------------
 // Combines the n consecutive partial slots starting at `slot0` for row r.
 // The (m, l) pairs of the first 64 slots (lane s: slot s) and the o vectors
-// of the first 8 slots are loaded in one round; later slots (rare) loop.
+// of the first K0 slots (32 registers' worth) are loaded in one round; later
+// slots (rare) loop.
 template <int D>
 __device__ __forceinline__ void merge_slots(const AttnArgs &a, int64_t slot0, int n, int r, int64_t obase) {
   constexpr int E = D / 64;  // d = lane + 64 e
-  constexpr int K0 = 8;
+  constexpr int K0 = 32 / E;
   __shared__ float w_lds[64];
   const int lane = threadIdx.x;
   const float2 *ml2 = reinterpret_cast<const float2 *>(a.ws_ml);
@@ -344,14 +345,13 @@ __global__ __launch_bounds__(64) void k_attn_merge_flat(AttnArgs a) {
   const int r = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x;
   const int64_t obase = out_row_base(a, b, hk, r, D);
-  const int nb = seq_blocks(a, a.lens[b]);
+  int s = 0, nb = 0;
+  const int T = flat_total_and_start(a, b, s, nb);
   if (nb == 0) {
 #pragma unroll
     for (int e = 0; e < D / 64; ++e) store_out(a.out, obase + lane + 64 * e, 0.0f, a.out_dtype);
     return;
   }
-  int s = 0;
-  const int T = flat_total_and_start(a, b, s);
   const int Wt = min(a.waves, T);  // waves that took part (each holds >= 1 block)
   const int first = flat_wave_of(s, T, Wt), last = flat_wave_of(s + nb - 1, T, Wt);
   if (first == last) return;
