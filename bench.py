@@ -1,17 +1,24 @@
 """Benchmark of the int8 paged KV hot path on one MI355X.
 
-A step is one decode pass of the hot path over one batch: for every layer,
-quantize-append one new token per sequence into the paged pool, then paged
-int8 decode attention over each sequence's whole cache (split-K merge
-included); plus the host block-manager work of the step (slot reservation,
-block tables) and its small host->device copies.
+A step is one pass of the hot path over one batch, for every layer, plus the
+host block-manager work of the step (slot reservation, block tables, rollback)
+and its small host->device copies:
+- decode workloads: quantize-append one new token per sequence into the
+  paged pool and paged int8 decode attention over each sequence's whole
+  cache (one fused call per layer; --unfused: the two calls);
+- verify: quantize-append k draft tokens per sequence, causal verify
+  attention of the k rows over the cache (MFMA path), then the host rolls
+  each sequence back to its accepted length;
+- shared prefix: decode steps of sequences forked from one refcounted
+  prefix (copy-on-write of the shared partial block, LRU eviction of
+  unreferenced prefix entries at 90 % occupancy).
 
 Default workload: Qwen3-14B-shaped KV (40 layers, 40 query / 8 KV heads,
 head_dim 128), affine int8 in groups of 64 with fp16 scale/bias, batch 32,
 context lengths uniform in [512, 8192], 64-token blocks whose ids are a
 seeded random permutation of the pool, bf16 N(0,1) inputs resident in HBM.
 
-Prints one JSON line (see README/DESIGN for the fields).
+Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -29,13 +36,20 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
 METRIC = "int8-KV paged decode-attn GB/s (% HBM peak) + tokens/s, B=32 Qwen3-14B shape"
 
 WORKLOADS = {
-    # name: (layers, Hq, Hkv, D, B, lo, hi)
-    "qwen3-14b-b32": (40, 40, 8, 128, 32, 512, 8192),
-    "llama-3.2-1b-b1": (16, 32, 8, 64, 1, 2048, 2048),
-    "qwen3-30b-a3b-b8-128k": (48, 32, 4, 128, 8, 131072, 131072),
+    "qwen3-14b-b32": dict(kind="decode", layers=40, Hq=40, Hkv=8, D=128, B=32, lo=512, hi=8192),
+    "llama-3.2-1b-b1": dict(kind="decode", layers=16, Hq=32, Hkv=8, D=64, B=1, lo=2048, hi=2048),
+    "qwen3-30b-a3b-b8-128k": dict(kind="decode", layers=48, Hq=32, Hkv=4, D=128, B=8, lo=131072, hi=131072,
+                                  outlier_frac=0.01),
+    # 64 sequences forked from one prefix of 4096 + 24 tokens (the last block shared while partly
+    # filled, so each fork's first append copies it), unique suffixes U[0, 1024]
+    "llama-3-8b-shared-prefix-b64": dict(kind="shared_prefix", layers=32, Hq=32, Hkv=8, D=128, B=64, lo=0,
+                                         hi=1024, prefix=4096 + 24),
+    "llama-3-8b-verify-b16": dict(kind="verify", layers=32, Hq=32, Hkv=8, D=128, B=16, lo=1024, hi=8192,
+                                  draft=8),
 }
 
 
@@ -48,8 +62,8 @@ def parse():
     ap.add_argument("--quant", default="affine_g64", choices=["affine_g64", "ref_row"])
     ap.add_argument("--split-blocks", type=int, default=0)
     ap.add_argument("--unfused", action="store_true",
-                    help="step as two calls per layer (quantize-append, then decode attention) instead of the "
-                         "fused krill_decode_append_attention")
+                    help="decode step as two calls per layer (quantize-append, then decode attention) instead of "
+                         "the fused krill_decode_append_attention")
     ap.add_argument("--kernel-reps", type=int, default=5, help="repetitions of the attention-only timing loop")
     ap.add_argument("--cpu-baseline", type=int, default=1, help="1: time the CPU baseline sample on rank 0")
     ap.add_argument("--seed", type=int, default=20261203)
@@ -64,189 +78,105 @@ def algorithmic_bytes_per_token_layer(Hkv, D, G):
     return 2 * Hkv * D + 2 * Hkv * G * 4
 
 
+class Env:
+    """Pool, library handle, stream and RNG of one bench run."""
+
+    def __init__(self, args, w, num_blocks, **pool_kw):
+        import torch
+
+        import krill_amd
+        from krill_amd import _lib as KL
+
+        self.torch, self.KL = torch, KL
+        self.dev = torch.device("cuda:0")
+        self.args, self.w = args, w
+        self.G = w["D"] // 64 if args.quant == "affine_g64" else 1
+        self.per_tok = algorithmic_bytes_per_token_layer(w["Hkv"], w["D"], self.G)
+        self.pool = krill_amd.KVPool(w["layers"], w["Hkv"], w["D"], num_blocks, args.quant, "bf16",
+                                     free_list_seed=args.seed, **pool_kw)
+        if args.split_blocks:
+            self.pool.set_option(KL.OPT_SPLIT_BLOCKS, args.split_blocks)
+        self.lib = KL.lib()
+        self.h = self.pool.handle
+        self.stream = torch.cuda.current_stream()
+        self.sp = ctypes.c_void_p(self.stream.cuda_stream)
+        self.gen = torch.Generator(device=self.dev)
+        self.gen.manual_seed(args.seed)
+        self.i32p = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))  # noqa: E731
+
+    def randn_bf16(self, shape):
+        t = self.torch
+        return t.randn(shape, generator=self.gen, device=self.dev, dtype=t.float32).to(t.bfloat16)
+
+    def fill(self, seqs, counts, chunk=1024, outlier_frac=0.0, nrand=4):
+        """Append counts[b] tokens to seqs[b] in every layer through the product path
+        (reserve + strided quantize-append), cycling over nrand random chunks."""
+        t, w = self.torch, self.w
+        B, Hkv, D = len(seqs), w["Hkv"], w["D"]
+        Tmax = int(max(counts)) if len(counts) else 0
+        if Tmax == 0:
+            return
+        slots = np.full((B, Tmax), -1, np.int32)
+        for b in range(B):
+            if counts[b] > 0:
+                slots[b, : counts[b]] = self.pool.reserve_append(seqs[b], int(counts[b]))
+        slots_d = t.from_numpy(slots).to(self.dev)
+        C = min(chunk, Tmax)
+        scale = None
+        if outlier_frac > 0:
+            rng = np.random.default_rng(self.args.seed + 7)
+            ch = rng.choice(Hkv * D, size=max(1, int(round(outlier_frac * Hkv * D))), replace=False)
+            s = np.ones(Hkv * D, np.float32)
+            s[ch] = 20.0
+            scale = t.from_numpy(s.reshape(1, Hkv, 1, D)).to(self.dev)
+        pool_k, pool_v = [], []
+        for _ in range(nrand):
+            k = t.randn((B, Hkv, C, D), generator=self.gen, device=self.dev, dtype=t.float32)
+            v = t.randn((B, Hkv, C, D), generator=self.gen, device=self.dev, dtype=t.float32)
+            if scale is not None:
+                k, v = k * scale, v * scale
+            pool_k.append(k.to(t.bfloat16))
+            pool_v.append(v.to(t.bfloat16))
+        strides = (Hkv * C * D, C * D, D)
+        n = 0
+        for layer in range(w["layers"]):
+            for t0 in range(0, Tmax, C):
+                L = min(C, Tmax - t0)
+                sm = slots_d[:, t0: t0 + L].contiguous()
+                k, v = pool_k[n % nrand], pool_v[n % nrand]
+                n += 1
+                self.KL.check(self.lib.krill_quantize_append_strided(self.h, layer, k.data_ptr(), v.data_ptr(),
+                                                                     *strides, sm.data_ptr(), B, L, self.sp))
+        t.cuda.synchronize()
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: every box in this setup has one MI355X; --gpus {args.gpus} is not "
               "supported (the path would shard by sequence / KV head, see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
-
     import torch
 
-    import krill_amd
-    from krill_amd import _lib as KL
-
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
-    dev = torch.device("cuda:0")
-    layers, Hq, Hkv, D, B, lo, hi = WORKLOADS[args.workload]
-    G = D // 64 if args.quant == "affine_g64" else 1
-    R = Hq // Hkv
-    rng = np.random.default_rng(args.seed)
-    lens0 = rng.integers(lo, hi + 1, size=B).astype(np.int64)
-    total_steps = args.warmup + args.steps + 1
-    blocks_needed = int(sum((int(T) + total_steps + 63) // 64 for T in lens0))
-    num_blocks = blocks_needed + max(16, blocks_needed // 8)
-    max_len_final = int(lens0.max()) + total_steps
-    max_blocks = (max_len_final + 63) // 64
-
-    pool = krill_amd.KVPool(layers, Hkv, D, num_blocks, args.quant, "bf16", free_list_seed=args.seed)
-    if args.split_blocks:
-        pool.set_option(KL.OPT_SPLIT_BLOCKS, args.split_blocks)
-    lib = KL.lib()
-    h = pool.handle
-    stream = torch.cuda.current_stream()
-    sp = ctypes.c_void_p(stream.cuda_stream)
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(args.seed)
-
     if args.copy_calibration:
         n = args.copy_calibration * (1 << 20) // 4
-        x = torch.ones(n, dtype=torch.float32, device=dev)
+        x = torch.ones(n, dtype=torch.float32, device="cuda:0")
         y = torch.empty_like(x)
         for _ in range(3):
             torch.neg(x, out=y)
         torch.cuda.synchronize()
         del x, y
+    w = WORKLOADS[args.workload]
+    rec = {"decode": run_decode, "verify": run_verify, "shared_prefix": run_shared_prefix}[w["kind"]](args, w)
+    print(json.dumps(rec))
 
-    # ---- fill every layer with the initial contexts (product path: reserve + quantize-append)
-    seqs = [pool.seq_create() for _ in range(B)]
-    Tmax = int(lens0.max())
-    slots = np.full((B, Tmax), -1, np.int32)
-    for b in range(B):
-        slots[b, : lens0[b]] = pool.reserve_append(seqs[b], int(lens0[b]))
-    slots_d = torch.from_numpy(slots).to(dev)
-    chunk = 1024
-    for layer in range(layers):
-        for t0 in range(0, Tmax, chunk):
-            L = min(chunk, Tmax - t0)
-            k = torch.randn((B, Hkv, L, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
-            v = torch.randn((B, Hkv, L, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
-            sm = slots_d[:, t0: t0 + L].contiguous()
-            KL.check(lib.krill_quantize_append(h, layer, k.data_ptr(), v.data_ptr(), sm.data_ptr(), B, L, sp))
-    del slots_d
-    torch.cuda.synchronize()
 
-    # ---- per-step inputs, resident in HBM
-    q_all = torch.randn((layers, B, Hq, 1, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
-    k_new = torch.randn((layers, B, Hkv, 1, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
-    v_new = torch.randn((layers, B, Hkv, 1, D), generator=gen, device=dev, dtype=torch.float32).to(torch.bfloat16)
-    out = torch.empty((B, Hq, 1, D), dtype=torch.bfloat16, device=dev)
-    ws_bytes = pool.workspace_size(B, Hq, 1, max_len_final)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    scale = 1.0 / math.sqrt(D)
-
-    NBUF = 3
-    pin_slots = [torch.empty((B, 1), dtype=torch.int32).pin_memory() for _ in range(NBUF)]
-    pin_tables = [torch.empty((B, max_blocks), dtype=torch.int32).pin_memory() for _ in range(NBUF)]
-    pin_lens = [torch.empty((B,), dtype=torch.int32).pin_memory() for _ in range(NBUF)]
-    buf_events = [None] * NBUF
-    d_slots = torch.empty((B, 1), dtype=torch.int32, device=dev)
-    d_tables = torch.empty((B, max_blocks), dtype=torch.int32, device=dev)
-    d_lens = torch.empty((B,), dtype=torch.int32, device=dev)
-    seqs_np = np.array(seqs, np.int32)
-    one_slot = np.empty(1, np.int32)
-    i32p = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))  # noqa: E731
-    qp = [q_all[l].data_ptr() for l in range(layers)]
-    kp = [k_new[l].data_ptr() for l in range(layers)]
-    vp = [v_new[l].data_ptr() for l in range(layers)]
-    outp, wsp = out.data_ptr(), ws.data_ptr()
-    cur_len = [int(x) for x in lens0]
-
-    def fused_call(layer, mx):
-        # the token at position len - 1 (its slot reserved above) is written, then attended over
-        KL.check(lib.krill_decode_append_attention(h, layer, qp[layer], kp[layer], vp[layer], Hkv * D, D,
-                                                   d_tables.data_ptr(), d_lens.data_ptr(), B, max_blocks, mx, Hq,
-                                                   ctypes.c_float(scale), outp, KL.DTYPE_BF16, wsp, ws_bytes, sp))
-
-    def attn_call(layer, mx):
-        if args.unfused:
-            KL.check(lib.krill_decode_attention(h, layer, qp[layer], d_tables.data_ptr(), d_lens.data_ptr(), B,
-                                                max_blocks, mx, Hq, ctypes.c_float(scale), outp, KL.DTYPE_BF16,
-                                                wsp, ws_bytes, sp))
-        else:
-            fused_call(layer, mx)  # rewrites the same token: the pool does not change
-
-    def step(i):
-        j = i % NBUF
-        if buf_events[j] is not None:
-            buf_events[j].synchronize()
-        ps, pt, pl = pin_slots[j].numpy(), pin_tables[j].numpy(), pin_lens[j].numpy()
-        for b in range(B):
-            KL.check(lib.krill_seq_reserve_append(h, seqs[b], 1, i32p(one_slot)))
-            ps[b, 0] = one_slot[0]
-            cur_len[b] += 1
-        KL.check(lib.krill_batch_tables(h, i32p(seqs_np), B, max_blocks, i32p(pt), i32p(pl)))
-        if args.unfused:
-            d_slots.copy_(pin_slots[j], non_blocking=True)
-        d_tables.copy_(pin_tables[j], non_blocking=True)
-        d_lens.copy_(pin_lens[j], non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record(stream)
-        buf_events[j] = ev
-        mx = max(cur_len)
-        for layer in range(layers):
-            if args.unfused:
-                KL.check(lib.krill_quantize_append(h, layer, kp[layer], vp[layer], d_slots.data_ptr(), B, 1, sp))
-                KL.check(lib.krill_decode_attention(h, layer, qp[layer], d_tables.data_ptr(), d_lens.data_ptr(),
-                                                    B, max_blocks, mx, Hq, ctypes.c_float(scale), outp,
-                                                    KL.DTYPE_BF16, wsp, ws_bytes, sp))
-            else:
-                fused_call(layer, mx)
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    lens_start = list(cur_len)
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    wall0 = time.perf_counter()
-    t_start.record(stream)
-    for i in range(args.steps):
-        step(args.warmup + i)
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    ms_step = t_start.elapsed_time(t_end) / args.steps
-
-    per_tok = algorithmic_bytes_per_token_layer(Hkv, D, G)
-    # attention reads each sequence's cache (incl. the appended token); average over timed steps
-    avg_ctx = [(lens_start[b] + cur_len[b] + 1) / 2.0 for b in range(B)]
-    kv_bytes_layer = sum(avg_ctx) * per_tok
-    qo_bytes_layer = B * Hq * D * 2 * 2
-    step_bytes = layers * (kv_bytes_layer + qo_bytes_layer)
-    gbs_step = step_bytes / (ms_step * 1e-3) / 1e9
-    tok_s = B / (ms_step * 1e-3)
-
-    # ---- dominant kernel alone: paged decode attention (+ its split merge; with the append fused unless
-    # --unfused), all layers
-    mx = max(cur_len)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    for layer in range(layers):  # warm
-        attn_call(layer, mx)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(args.kernel_reps):
-        for layer in range(layers):
-            attn_call(layer, mx)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    attn_ms = e0.elapsed_time(e1) / (args.kernel_reps * layers)
-    launch_bytes = sum(cur_len) * per_tok + qo_bytes_layer
-    if not args.unfused:  # the new token: bf16 K/V rows in, quantized bytes out
-        launch_bytes += B * (2 * Hkv * D * 2 + per_tok)
-    achieved = launch_bytes / (attn_ms * 1e-3) / 1e9
-
-    # ---- CPU baseline: the reference's per-step algorithm on the host cores
-    cpu = None
-    if args.cpu_baseline:
-        cpu = cpu_baseline(args, Hq, Hkv, D, lens0, per_tok)
-
-    stats = pool.stats()
-    pool.close()
+def _record(args, w, env, value, ms_step, config, roofline, extra, cpu=None):
+    stats = env.pool.stats()
     rec = {
         "metric": METRIC,
-        "value": round(gbs_step, 2),
+        "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -257,42 +187,439 @@ def main():
         "vs_baseline": None,
         "dtype": "u8",
         "data": "synthetic",
-        "config": {
-            "workload": f"{args.workload}: {layers} layers, Hq {Hq}, Hkv {Hkv}, D {D}, B {B}, "
-                        f"context U[{lo},{hi}], 64-token blocks (permuted pool), {args.quant} int8, "
-                        "bf16 N(0,1) inputs; step = per layer quantize-append 1 token/seq + paged decode attention"
-                        + (" (two calls)" if args.unfused else " (one fused call)"),
-            "layers": layers, "Hq": Hq, "Hkv": Hkv, "head_dim": D, "batch": B, "quant": args.quant,
-            "context_mean": float(np.mean(lens0)), "num_blocks": num_blocks,
-        },
-        "tokens_per_s": round(tok_s, 1),
-        "hbm_frac_step": round(gbs_step / HBM_PEAK_GBS, 4),
-        "step_bytes": int(step_bytes),
-        "wall_s_timed": round(wall, 4),
-        "roofline": {
-            "bound": "hbm",
-            "kernel": ("paged decode attention call (k_attn_valu + k_attn_merge_flat), one layer" if args.unfused
-                       else "fused append + paged decode attention call (k_attn_valu + k_attn_merge_flat), "
-                            "one layer"),
-            "achieved": round(achieved, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(args),
-            "bytes_per_launch": int(launch_bytes),
-            "avg_launch_ms": round(attn_ms, 5),
-        },
-        "cpu_baseline": cpu,
-        "pool": {"cow_copies": stats["cow_copies"], "blocks_used": stats["blocks_used"]},
+        "config": config,
     }
-    print(json.dumps(rec))
+    rec.update(extra)
+    rec["roofline"] = roofline
+    rec["cpu_baseline"] = cpu
+    rec["pool"] = {k: stats[k] for k in ("cow_copies", "blocks_used", "blocks_shared", "evicted_entries",
+                                         "evicted_blocks", "num_blocks")}
+    return rec
 
 
-def measured_traffic(args):
+def _timed(env, step, warmup, steps):
+    t = env.torch
+    for i in range(warmup):
+        step(i)
+    t.cuda.synchronize()
+    t_start = t.cuda.Event(enable_timing=True)
+    t_end = t.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    t_start.record(env.stream)
+    for i in range(steps):
+        step(warmup + i)
+    t_end.record(env.stream)
+    t.cuda.synchronize()
+    return t_start.elapsed_time(t_end) / steps, time.perf_counter() - wall0
+
+
+def _time_calls(env, call, reps):
+    """Average time of one call(layer) over reps passes of all layers (HIP events on the library's stream)."""
+    t = env.torch
+    layers = env.w["layers"]
+    for layer in range(layers):
+        call(layer)
+    t.cuda.synchronize()
+    e0 = t.cuda.Event(enable_timing=True)
+    e1 = t.cuda.Event(enable_timing=True)
+    e0.record(env.stream)
+    for _ in range(reps):
+        for layer in range(layers):
+            call(layer)
+    e1.record(env.stream)
+    t.cuda.synchronize()
+    return e0.elapsed_time(e1) / (reps * layers)
+
+
+class StepTables:
+    """Pinned host buffers (ring of 3) and device copies of the step's block tables, lengths and slots."""
+
+    def __init__(self, env, B, max_blocks, slots_per_seq):
+        t = env.torch
+        self.env, self.B, self.mb = env, B, max_blocks
+        self.ring = [(t.empty((B, max(slots_per_seq, 1)), dtype=t.int32).pin_memory(),
+                      t.empty((B, max_blocks), dtype=t.int32).pin_memory(),
+                      t.empty((B,), dtype=t.int32).pin_memory()) for _ in range(3)]
+        self.events = [None] * 3
+        self.d_slots = t.empty((B, max(slots_per_seq, 1)), dtype=t.int32, device=env.dev)
+        self.d_tables = t.empty((B, max_blocks), dtype=t.int32, device=env.dev)
+        self.d_lens = t.empty((B,), dtype=t.int32, device=env.dev)
+
+    def host(self, i):
+        j = i % 3
+        if self.events[j] is not None:
+            self.events[j].synchronize()
+        return j, self.ring[j][0].numpy(), self.ring[j][1].numpy(), self.ring[j][2].numpy()
+
+    def upload(self, j, slots=True):
+        ps, pt, pl = self.ring[j]
+        if slots:
+            self.d_slots.copy_(ps, non_blocking=True)
+        self.d_tables.copy_(pt, non_blocking=True)
+        self.d_lens.copy_(pl, non_blocking=True)
+        ev = self.env.torch.cuda.Event()
+        ev.record(self.env.stream)
+        self.events[j] = ev
+
+
+def _decode_calls(env, seqs, st, max_len_final, Hq):
+    """The per-layer decode call(s) over the batch (fused unless --unfused)."""
+    args, w, KL, lib, h, sp = env.args, env.w, env.KL, env.lib, env.h, env.sp
+    B, Hkv, D, layers = len(seqs), w["Hkv"], w["D"], w["layers"]
+    q_all = env.randn_bf16((layers, B, Hq, 1, D))
+    k_new = env.randn_bf16((layers, B, Hkv, 1, D))
+    v_new = env.randn_bf16((layers, B, Hkv, 1, D))
+    out = env.torch.empty((B, Hq, 1, D), dtype=env.torch.bfloat16, device=env.dev)
+    ws_bytes = env.pool.workspace_size(B, Hq, 1, max_len_final)
+    ws = env.torch.empty(max(ws_bytes, 1), dtype=env.torch.uint8, device=env.dev)
+    qp = [q_all[l].data_ptr() for l in range(layers)]
+    kp = [k_new[l].data_ptr() for l in range(layers)]
+    vp = [v_new[l].data_ptr() for l in range(layers)]
+    scale = ctypes.c_float(1.0 / math.sqrt(D))
+    keep = (q_all, k_new, v_new, out, ws)
+
+    def append(layer):
+        KL.check(lib.krill_quantize_append(h, layer, kp[layer], vp[layer], st.d_slots.data_ptr(), B, 1, sp))
+
+    def attend(layer, mx):
+        KL.check(lib.krill_decode_attention(h, layer, qp[layer], st.d_tables.data_ptr(), st.d_lens.data_ptr(), B,
+                                            st.mb, mx, Hq, scale, out.data_ptr(), KL.DTYPE_BF16, ws.data_ptr(),
+                                            ws_bytes, sp))
+
+    def fused(layer, mx):
+        # the token at position len - 1 (its slot reserved by the step) is written, then attended over
+        KL.check(lib.krill_decode_append_attention(h, layer, qp[layer], kp[layer], vp[layer], Hkv * D, D,
+                                                   st.d_tables.data_ptr(), st.d_lens.data_ptr(), B, st.mb, mx, Hq,
+                                                   scale, out.data_ptr(), KL.DTYPE_BF16, ws.data_ptr(), ws_bytes,
+                                                   sp))
+
+    def step_layer(layer, mx):
+        if args.unfused:
+            append(layer)
+            attend(layer, mx)
+        else:
+            fused(layer, mx)
+
+    def call_only(layer, mx):  # the dominant call alone; the fused one rewrites the same token
+        if args.unfused:
+            attend(layer, mx)
+        else:
+            fused(layer, mx)
+
+    return step_layer, call_only, keep
+
+
+def run_decode(args, w):
+    layers, Hq, Hkv, D, B = w["layers"], w["Hq"], w["Hkv"], w["D"], w["B"]
+    rng = np.random.default_rng(args.seed)
+    lens0 = rng.integers(w["lo"], w["hi"] + 1, size=B).astype(np.int64)
+    total_steps = args.warmup + args.steps + 1
+    blocks_needed = int(sum((int(T) + total_steps + 63) // 64 for T in lens0))
+    num_blocks = blocks_needed + max(16, blocks_needed // 8)
+    max_len_final = int(lens0.max()) + total_steps
+    max_blocks = (max_len_final + 63) // 64
+    env = Env(args, w, num_blocks)
+    seqs = [env.pool.seq_create() for _ in range(B)]
+    env.fill(seqs, [int(x) for x in lens0], outlier_frac=w.get("outlier_frac", 0.0))
+
+    st = StepTables(env, B, max_blocks, 1)
+    step_layer, call_only, keep = _decode_calls(env, seqs, st, max_len_final, Hq)
+    seqs_np = np.array(seqs, np.int32)
+    one = np.empty(1, np.int32)
+    cur_len = [int(x) for x in lens0]
+
+    def step(i):
+        j, ps, pt, pl = st.host(i)
+        for b in range(B):
+            env.KL.check(env.lib.krill_seq_reserve_append(env.h, seqs[b], 1, env.i32p(one)))
+            ps[b, 0] = one[0]
+            cur_len[b] += 1
+        env.KL.check(env.lib.krill_batch_tables(env.h, env.i32p(seqs_np), B, max_blocks, env.i32p(pt), env.i32p(pl)))
+        st.upload(j, slots=args.unfused)
+        mx = max(cur_len)
+        for layer in range(layers):
+            step_layer(layer, mx)
+
+    for i in range(args.warmup):
+        step(i)
+    lens_start = None
+    # timed steps (lengths at their start recorded for the byte count)
+    env.torch.cuda.synchronize()
+    lens_start = list(cur_len)
+    ms_step, wall = _timed(env, lambda i: step(args.warmup + i), 0, args.steps)
+
+    per_tok = env.per_tok
+    avg_ctx = [(lens_start[b] + cur_len[b] + 1) / 2.0 for b in range(B)]
+    kv_bytes_layer = sum(avg_ctx) * per_tok
+    qo_bytes_layer = B * Hq * D * 2 * 2
+    step_bytes = layers * (kv_bytes_layer + qo_bytes_layer)
+    gbs_step = step_bytes / (ms_step * 1e-3) / 1e9
+
+    mx = max(cur_len)
+    attn_ms = _time_calls(env, lambda layer: call_only(layer, mx), args.kernel_reps)
+    launch_bytes = sum(cur_len) * per_tok + qo_bytes_layer
+    if not args.unfused:  # the new token: bf16 K/V rows in, quantized bytes out
+        launch_bytes += B * (2 * Hkv * D * 2 + per_tok)
+    achieved = launch_bytes / (attn_ms * 1e-3) / 1e9
+
+    cpu = None
+    if args.cpu_baseline and w["kind"] == "decode" and max(lens0) <= 16384:
+        cpu = cpu_baseline(args, w, lens0, per_tok)
+
+    config = {
+        "workload": f"{args.workload}: {layers} layers, Hq {Hq}, Hkv {Hkv}, D {D}, B {B}, "
+                    f"context U[{w['lo']},{w['hi']}], 64-token blocks (permuted pool), {args.quant} int8, "
+                    "bf16 N(0,1) inputs"
+                    + (f" ({w['outlier_frac']:.0%} of channels x20)" if w.get("outlier_frac") else "")
+                    + "; step = per layer quantize-append 1 token/seq + paged decode attention"
+                    + (" (two calls)" if args.unfused else " (one fused call)"),
+        "layers": layers, "Hq": Hq, "Hkv": Hkv, "head_dim": D, "batch": B, "quant": args.quant,
+        "context_mean": float(np.mean(lens0)), "num_blocks": num_blocks,
+    }
+    call = "decode_attn" if args.unfused else "decode_append_attn"
+    roofline = {
+        "bound": "hbm",
+        "kernel": ("paged decode attention call (k_attn_valu + k_attn_merge_flat), one layer" if args.unfused
+                   else "fused append + paged decode attention call (k_attn_valu + k_attn_merge_flat), one layer"),
+        "achieved": round(achieved, 2),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": measured_traffic(args, call),
+        "bytes_per_launch": int(launch_bytes),
+        "avg_launch_ms": round(attn_ms, 5),
+    }
+    extra = {"tokens_per_s": round(B / (ms_step * 1e-3), 1), "hbm_frac_step": round(gbs_step / HBM_PEAK_GBS, 4),
+             "step_bytes": int(step_bytes), "wall_s_timed": round(wall, 4)}
+    rec = _record(args, w, env, gbs_step, ms_step, config, roofline, extra, cpu)
+    del keep
+    env.pool.close()
+    return rec
+
+
+def run_shared_prefix(args, w):
+    """Decode steps of B sequences forked from one refcounted prefix.  The pool
+    is sized so that occupancy sits just under the 90 % watermark when the
+    timed steps start, with unreferenced prefix entries (stale cached
+    prompts) holding the slack: new blocks then evict them oldest first."""
+    layers, Hq, Hkv, D, B = w["layers"], w["Hq"], w["Hkv"], w["D"], w["B"]
+    rng = np.random.default_rng(args.seed)
+    P = w["prefix"]
+    suffix = rng.integers(w["lo"], w["hi"] + 1, size=B).astype(np.int64)
+    total_steps = args.warmup + args.steps + 1
+    pblocks = (P + 63) // 64
+    # blocks the live sequences end with: shared prefix blocks + each fork's own blocks (incl. its COW copy)
+    own = [((P + int(s) + total_steps + 63) // 64) - (P // 64) for s in suffix]
+    live_end = pblocks + sum(own)
+    live_start = pblocks + sum(((P + int(s) + 63) // 64) - (P // 64) if s > 0 else 0 for s in suffix)
+    stale_entries, stale_tokens = 8, 1024
+    stale_blocks = stale_entries * (stale_tokens // 64)
+    # num_blocks: (live_start + stale) just under 90 %; growth beyond it evicts stale entries
+    num_blocks = int(math.ceil((live_start + stale_blocks) / 0.895)) + 1
+    num_blocks = max(num_blocks, int(math.ceil(live_end / 0.9)) + 8)
+    env = Env(args, w, num_blocks, evict_watermark=0.9, max_prefix_entries=stale_entries + 4)
+    pool = env.pool
+    # stale cached prompts, unreferenced once their sequences are freed
+    for e in range(stale_entries):
+        s = pool.seq_create()
+        env.fill([s], [stale_tokens], chunk=stale_tokens, nrand=1)
+        assert pool.prefix_store(s, np.arange(stale_tokens) + 1000003 * (e + 1))
+        pool.seq_free(s)
+    # the shared prefix, stored as an entry too (the prompt cache of the reference)
+    base = pool.seq_create()
+    env.fill([base], [P], chunk=1024, nrand=2)
+    assert pool.prefix_store(base, np.arange(P))
+    seqs = [pool.seq_fork(base, P) for _ in range(B)]
+    pool.seq_free(base)
+    env.fill(seqs, [int(s) for s in suffix], chunk=256, nrand=2)  # first appends copy the shared partial block
+    lens0 = P + suffix
+    max_len_final = int(lens0.max()) + total_steps
+    max_blocks = (max_len_final + 63) // 64
+    st = StepTables(env, B, max_blocks, 1)
+    step_layer, call_only, keep = _decode_calls(env, seqs, st, max_len_final, Hq)
+    seqs_np = np.array(seqs, np.int32)
+    one = np.empty(1, np.int32)
+    cur_len = [int(x) for x in lens0]
+    stats0 = pool.stats()
+
+    def step(i):
+        j, ps, pt, pl = st.host(i)
+        for b in range(B):
+            env.KL.check(env.lib.krill_seq_reserve_append(env.h, seqs[b], 1, env.i32p(one)))
+            ps[b, 0] = one[0]
+            cur_len[b] += 1
+        env.KL.check(env.lib.krill_batch_tables(env.h, env.i32p(seqs_np), B, max_blocks, env.i32p(pt), env.i32p(pl)))
+        st.upload(j, slots=args.unfused)
+        mx = max(cur_len)
+        for layer in range(layers):
+            step_layer(layer, mx)
+
+    for i in range(args.warmup):
+        step(i)
+    env.torch.cuda.synchronize()
+    lens_start = list(cur_len)
+    ms_step, wall = _timed(env, lambda i: step(args.warmup + i), 0, args.steps)
+    per_tok = env.per_tok
+    avg_ctx = [(lens_start[b] + cur_len[b] + 1) / 2.0 for b in range(B)]
+    logical_layer = sum(avg_ctx) * per_tok
+    unique_layer = (P + sum(c - P for c in avg_ctx)) * per_tok
+    qo_layer = B * Hq * D * 2 * 2
+    unique_gbs = layers * (unique_layer + qo_layer) / (ms_step * 1e-3) / 1e9
+    logical_gbs = layers * (logical_layer + qo_layer) / (ms_step * 1e-3) / 1e9
+    mx = max(cur_len)
+    attn_ms = _time_calls(env, lambda layer: call_only(layer, mx), args.kernel_reps)
+    uniq_launch = (P + sum(c - P for c in cur_len)) * per_tok + qo_layer
+    stats1 = pool.stats()
+    config = {
+        "workload": f"{args.workload}: {layers} layers, Hq {Hq}, Hkv {Hkv}, D {D}, {B} sequences forked from one "
+                    f"{P}-token prefix (refcounted; last block shared while partly filled -> copy-on-write), "
+                    f"unique suffixes U[{w['lo']},{w['hi']}], {args.quant} int8, pool at the 90 % LRU watermark "
+                    f"with {stale_entries} unreferenced {stale_tokens}-token prefix entries; step = per layer "
+                    "quantize-append 1 token/seq + paged decode attention"
+                    + (" (two calls)" if args.unfused else " (one fused call)"),
+        "layers": layers, "Hq": Hq, "Hkv": Hkv, "head_dim": D, "batch": B, "quant": args.quant,
+        "prefix": P, "suffix_mean": float(np.mean(suffix)), "num_blocks": num_blocks,
+    }
+    roofline = {
+        "bound": "hbm",
+        "kernel": "fused append + paged decode attention call, one layer; unique bytes (shared prefix once)",
+        "achieved": round(uniq_launch / (attn_ms * 1e-3) / 1e9, 2),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(uniq_launch / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "bytes_per_launch": int(uniq_launch),
+        "avg_launch_ms": round(attn_ms, 5),
+    }
+    extra = {"tokens_per_s": round(B / (ms_step * 1e-3), 1), "hbm_frac_step": round(unique_gbs / HBM_PEAK_GBS, 4),
+             "effective_gbs_logical": round(logical_gbs, 2), "wall_s_timed": round(wall, 4),
+             "evictions_during_steps": {"entries": stats1["evicted_entries"] - stats0["evicted_entries"],
+                                        "blocks": stats1["evicted_blocks"] - stats0["evicted_blocks"]},
+             "occupancy_before_steps": round(stats0["blocks_used"] / num_blocks, 4)}
+    rec = _record(args, w, env, unique_gbs, ms_step, config, roofline, extra)
+    del keep
+    pool.close()
+    return rec
+
+
+def run_verify(args, w):
+    """Speculative verify: k draft tokens appended per sequence, causal verify
+    attention of the k rows (MFMA path), then rollback to the accepted length
+    (a ~ U[0, k] accepted: keep a + 1 rows on rejection, all k on full accept)."""
+    layers, Hq, Hkv, D, B, k = w["layers"], w["Hq"], w["Hkv"], w["D"], w["B"], w["draft"]
+    rng = np.random.default_rng(args.seed)
+    lens0 = rng.integers(w["lo"], w["hi"] + 1, size=B).astype(np.int64)
+    total_steps = args.warmup + args.steps + 1
+    blocks_needed = int(sum((int(T) + k * total_steps + 63) // 64 for T in lens0))
+    num_blocks = blocks_needed + max(16, blocks_needed // 8)
+    max_len_final = int(lens0.max()) + k * total_steps
+    max_blocks = (max_len_final + 63) // 64
+    env = Env(args, w, num_blocks)
+    KL, lib, h, sp, t = env.KL, env.lib, env.h, env.sp, env.torch
+    seqs = [env.pool.seq_create() for _ in range(B)]
+    env.fill(seqs, [int(x) for x in lens0])
+    st = StepTables(env, B, max_blocks, k)
+    q_all = env.randn_bf16((layers, B, Hq, k, D))
+    k_new = env.randn_bf16((layers, B, Hkv, k, D))
+    v_new = env.randn_bf16((layers, B, Hkv, k, D))
+    out = t.empty((B, Hq, k, D), dtype=t.bfloat16, device=env.dev)
+    ws_bytes = env.pool.workspace_size(B, Hq, k, max_len_final)
+    ws = t.empty(max(ws_bytes, 1), dtype=t.uint8, device=env.dev)
+    scale = ctypes.c_float(1.0 / math.sqrt(D))
+    seqs_np = np.array(seqs, np.int32)
+    slots_h = np.empty(k, np.int32)
+    cur_len = [int(x) for x in lens0]
+    acc_rng = np.random.default_rng(args.seed + 3)
+    accepted_total = [0]
+
+    def verify(layer, mx):
+        KL.check(lib.krill_verify_attention(h, layer, q_all[layer].data_ptr(), k, st.d_tables.data_ptr(),
+                                            st.d_lens.data_ptr(), B, max_blocks, mx, Hq, scale, out.data_ptr(),
+                                            KL.DTYPE_BF16, ws.data_ptr(), ws_bytes, sp))
+
+    def step(i):
+        j, ps, pt, pl = st.host(i)
+        for b in range(B):
+            KL.check(lib.krill_seq_reserve_append(h, seqs[b], k, env.i32p(slots_h)))
+            ps[b, :] = slots_h
+            cur_len[b] += k
+        KL.check(lib.krill_batch_tables(h, env.i32p(seqs_np), B, max_blocks, env.i32p(pt), env.i32p(pl)))
+        st.upload(j)
+        mx = max(cur_len)
+        for layer in range(layers):
+            KL.check(lib.krill_quantize_append(h, layer, k_new[layer].data_ptr(), v_new[layer].data_ptr(),
+                                               st.d_slots.data_ptr(), B, k, sp))
+            verify(layer, mx)
+        # rollback (SpeculativeDecoder.swift:309-318): keep a + 1 rows on rejection, k on full accept
+        for b in range(B):
+            a = int(acc_rng.integers(0, k + 1))
+            keep_rows = a + 1 if a < k else k
+            cur_len[b] += keep_rows - k
+            accepted_total[0] += keep_rows
+            KL.check(lib.krill_seq_truncate(h, seqs[b], cur_len[b]))
+
+    for i in range(args.warmup):
+        step(i)
+    t.cuda.synchronize()
+    lens_start = list(cur_len)
+    acc0 = accepted_total[0]
+    ms_step, wall = _timed(env, lambda i: step(args.warmup + i), 0, args.steps)
+    per_tok = env.per_tok
+    # per step: each sequence reads (len + k) tokens per layer
+    avg_ctx = [(lens_start[b] + cur_len[b]) / 2.0 + k for b in range(B)]
+    qo_layer = B * Hq * k * D * 2 * 2
+    step_bytes = layers * (sum(avg_ctx) * per_tok + qo_layer)
+    gbs_step = step_bytes / (ms_step * 1e-3) / 1e9
+
+    # the verify call alone at the current lengths (the drafts of the last step are still cached)
+    for b in range(B):
+        KL.check(lib.krill_seq_reserve_append(h, seqs[b], k, env.i32p(slots_h)))
+        cur_len[b] += k
+    j, ps, pt, pl = st.host(10 ** 6)
+    KL.check(lib.krill_batch_tables(h, env.i32p(seqs_np), B, max_blocks, env.i32p(pt), env.i32p(pl)))
+    st.upload(j, slots=False)
+    mx = max(cur_len)
+    attn_ms = _time_calls(env, lambda layer: verify(layer, mx), args.kernel_reps)
+    kv_launch = sum(cur_len) * per_tok + qo_layer
+    # causal: row r of sequence b sees len_b - k + r + 1 tokens; QK^T and PV 2 FLOP per MAC each
+    flops = sum(4.0 * Hq * D * sum(c - k + r + 1 for r in range(k)) for c in cur_len)
+    tflops = flops / (attn_ms * 1e-3) / 1e12
+    config = {
+        "workload": f"{args.workload}: {layers} layers, Hq {Hq}, Hkv {Hkv}, D {D}, B {B}, context "
+                    f"U[{w['lo']},{w['hi']}], {k} draft rows/seq (causal inside the window, "
+                    f"{Hq // Hkv * k} query rows per KV head -> MFMA path), accepted a ~ U[0,{k}] then rollback, "
+                    f"{args.quant} int8; step = per layer quantize-append {k} tokens/seq + verify attention",
+        "layers": layers, "Hq": Hq, "Hkv": Hkv, "head_dim": D, "batch": B, "draft": k, "quant": args.quant,
+        "context_mean": float(np.mean(lens0)), "num_blocks": num_blocks,
+    }
+    roofline = {
+        "bound": "hbm",
+        "kernel": "verify attention call (k_attn_mfma + k_attn_merge_split), one layer",
+        "achieved": round(kv_launch / (attn_ms * 1e-3) / 1e9, 2),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(kv_launch / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "traffic": measured_traffic(args, "verify_attn"),
+        "bytes_per_launch": int(kv_launch),
+        "avg_launch_ms": round(attn_ms, 5),
+        "mfma": {"achieved": round(tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                 "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "flops_per_launch": flops,
+                 "arith_intensity": round(flops / kv_launch, 1)},
+    }
+    accepted = accepted_total[0] - acc0
+    extra = {"tokens_per_s": round(accepted / args.steps / (ms_step * 1e-3), 1),
+             "hbm_frac_step": round(gbs_step / HBM_PEAK_GBS, 4), "step_bytes": int(step_bytes),
+             "wall_s_timed": round(wall, 4)}
+    rec = _record(args, w, env, gbs_step, ms_step, config, roofline, extra)
+    del q_all, k_new, v_new, out, ws
+    env.pool.close()
+    return rec
+
+
+def measured_traffic(args, call):
     """HBM bytes per call of the timed entry point from the committed
     rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, calibrated against a plain
     copy), when it was taken on this workload; None otherwise."""
-    call = "decode_attn" if args.unfused else "decode_append_attn"
     path = os.path.join(ROOT, "profiles", f"{call}_{args.workload}_{args.quant}_traffic.json")
     try:
         with open(path) as f:
@@ -302,11 +629,12 @@ def measured_traffic(args):
     return rec.get("traffic_bytes_per_call")
 
 
-def cpu_baseline(args, Hq, Hkv, D, lens0, per_tok):
+def cpu_baseline(args, w, lens0, per_tok):
     """Time the oracle's restatement of the reference step (quantize row ->
     concat -> full-cache fp16 dequant -> fp32 SDPA) on a bounded sample."""
     from oracle import oracle as O
 
+    Hq, Hkv, D = w["Hq"], w["Hkv"], w["D"]
     cores = len(os.sched_getaffinity(0))
     os.environ.setdefault("OMP_NUM_THREADS", str(cores))
     sample_layers = 2
@@ -331,7 +659,7 @@ def cpu_baseline(args, Hq, Hkv, D, lens0, per_tok):
     base.close()
     ctx = float(np.sum(lens0)) + 1.5 * B
     gbs = ctx * per_tok / per_layer_s / 1e9
-    layers = WORKLOADS[args.workload][0]
+    layers = w["layers"]
     return {
         "value": round(gbs, 3),
         "unit": "GB/s",

@@ -7,12 +7,14 @@
 
 namespace krill {
 
-// Workspace: `slots` partial results of NR query rows each, 256-byte aligned
-// pieces:
-//   o      float [slots][NR][D]   unnormalised partial outputs
-//   ml     float [slots][NR][2]   (running max m in log2 units, sum l)
-// MFMA path: slot = (b * Hkv + hk) * max_splits + split.
-// VALU path: slot = hk * (waves + B) + wave + b (see k_attn_valu).
+// Workspace: `slots` partial results of RR query rows each (RR = rows per
+// row group: all NR rows on the VALU path, 16 * nrt on the MFMA path),
+// 256-byte aligned pieces:
+//   o      float [slots][RR][D]   unnormalised partial outputs
+//   ml     float [slots][RR][2]   (running max m in log2 units, sum l)
+// slot = (hk * row_groups + rg) * (waves + B) + wave + b: the flat block
+// order of each (KV head, row group) split over `waves` waves, one slot per
+// (wave, sequence it touches).
 struct WsLayout {
   size_t o, ml, total;
 };
@@ -37,8 +39,9 @@ struct AttnArgs {
   int32_t nb_cap;  // blocks per sequence the plan covers (from max_seq_len)
   int32_t Hkv, R, Lq, Hq, NR;
   float scale_log2;  // softmax scale * log2(e)
-  int32_t split_blocks, max_splits;
-  int32_t waves;  // VALU path: waves per KV head
+  int32_t split_blocks;
+  int32_t row_groups, rows_per_group;  // query rows per wave (all NR on the VALU path)
+  int32_t waves;  // waves per (KV head, row group)
   float *ws_o;
   float *ws_ml;
   void *out;  // [B][Hq][Lq][D]
@@ -67,9 +70,10 @@ inline AttnArgs make_attn_args(const PoolGeometry &g, int32_t layer, const AttnL
   r.NR = p.NR;
   r.scale_log2 = a.scale * 1.4426950408889634f;
   r.split_blocks = p.split_blocks;
-  r.max_splits = p.max_splits;
+  r.row_groups = p.row_groups;
+  r.rows_per_group = p.rows_per_group;
   r.waves = p.waves;
-  const WsLayout w = ws_layout(p.slots, p.NR, g.D);
+  const WsLayout w = ws_layout(p.slots, p.rows_per_group, g.D);
   uint8_t *base = static_cast<uint8_t *>(a.ws);
   r.ws_o = reinterpret_cast<float *>(base + w.o);
   r.ws_ml = reinterpret_cast<float *>(base + w.ml);
@@ -102,9 +106,6 @@ __device__ __forceinline__ int64_t out_row_base(const AttnArgs &a, int b, int hk
   const int hq = hk * a.R + r % a.R, j = r / a.R;
   return (((int64_t)b * a.Hq + hq) * a.Lq + j) * D;
 }
-__device__ __forceinline__ int64_t part_index(const AttnArgs &a, int b, int hk, int split, int r) {
-  return (((int64_t)b * a.Hkv + hk) * a.max_splits + split) * a.NR + r;
-}
 
 // Inclusive prefix sum over the 64 lanes of a wave.
 __device__ __forceinline__ int wave_incl_scan(int v) {
@@ -123,16 +124,28 @@ __device__ __forceinline__ int wave_allsum_int(int v) {
   return v;
 }
 
-// Flat block order of the VALU path: the blocks of sequences 0, 1, .., B-1
-// one after another (T blocks per KV head).  Returns T and sets start_out /
+// Blocks of a sequence of length len that row group rg reads: with several
+// row groups (long query windows) a group stops at the block holding the
+// last key its last row sees (causal window); a single group reads them all.
+__device__ __forceinline__ int seq_blocks_rg(const AttnArgs &a, int len, int rg) {
+  const int nb = seq_blocks(a, len);
+  if (a.row_groups <= 1) return nb;
+  const int rlast = min(a.NR, (rg + 1) * a.rows_per_group) - 1;
+  const int lim = len - a.Lq + rlast / a.R + 1;
+  const int nv = lim > 0 ? (lim + 63) >> 6 : 0;
+  return nb < nv ? nb : nv;
+}
+
+// Flat block order of a (KV head, row group): the blocks of sequences 0, 1,
+// .., B-1 one after another (T blocks).  Returns T and sets start_out /
 // nb_out to the flat index of sequence b's first block and its block count.
 // Uniform across the wave; one round of lens loads.
-__device__ __forceinline__ int flat_total_and_start(const AttnArgs &a, int b, int &start_out, int &nb_out) {
+__device__ __forceinline__ int flat_total_and_start(const AttnArgs &a, int b, int rg, int &start_out, int &nb_out) {
   const int lane = threadIdx.x & 63;
   int carry = 0;
   for (int c0 = 0; c0 < a.B; c0 += 64) {
     const int bb = c0 + lane;
-    const int nbv = bb < a.B ? seq_blocks(a, a.lens[bb]) : 0;
+    const int nbv = bb < a.B ? seq_blocks_rg(a, a.lens[bb], rg) : 0;
     const int incl = wave_incl_scan(nbv) + carry;
     if (b >= c0 && b < c0 + 64) {
       start_out = __builtin_amdgcn_readlane(incl - nbv, b - c0);

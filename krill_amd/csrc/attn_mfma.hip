@@ -6,24 +6,35 @@
 // sees every cached key plus new keys 0..j), equivalently
 // Sources/KrillCore/LlamaModel.swift:186-202.
 //
-// One wave64 per (split of 64-token blocks, kv head x row group, sequence);
-// a row group holds NRT tiles of 16 query rows (NRT <= 2, register bound).  The kernel works
-// on transposed scores so no operand is ever transposed in registers:
+// Work split as on the decode path: per (KV head, row group of 16 * NRT
+// query rows) the blocks of all sequences are laid end to end and split
+// evenly over the waves of the grid, crossing sequence boundaries; a
+// sequence covered by several waves is combined by k_attn_merge_flat.  With
+// several row groups (long query windows) each group only walks the blocks
+// its rows can see.
+//
+// Memory: every block's head region (K, V and metadata, a whole number of
+// contiguous 1 KB runs in the pool layout) is copied verbatim into a
+// two-stage LDS ring with direct-to-LDS buffer loads (16 bytes per lane, no
+// registers involved), the next block in flight while the current one is
+// computed; MFMA operands are then read from LDS.
+//
+// Math: transposed scores, so no operand is ever transposed in registers:
 //   S^T[tok][row] = K[tok][d] . Q^T[d][row]      v_mfma_f32_16x16x32_f16
 //   O^T[d][row]  += V^T[d][tok] . P^T[tok][row]  v_mfma_f32_16x16x32_f16
-// K rows are stored 32-d-chunk major, so the A operand (8 d of one token per
-// lane) is one 8-byte load; V is stored token-contiguous per d in exactly the
-// token order in which the S^T accumulator hands P to the P.V B operand.
-// Bytes become exact fp16 with v_perm_b32 + one packed subtract; affine
-// scale/bias are applied to the fp32 scores (per group) and folded into the
-// fp16 weights P*s_v, which are split hi + lo so the weight rounding stays
-// below 2^-22 relative.  Rows beyond the causal limit of a whole row group
-// skip their blocks (chunked prefill does half the work of a dense mask).
+// The 16-byte K chunks hold the 8 d of an A operand contiguously; V is stored
+// per d in exactly the token order in which the S^T accumulator hands P to
+// the P.V B operand.  Bytes become exact fp16 with v_perm_b32 + one packed
+// subtract; affine scale/bias are applied to the fp32 scores (per group) and
+// folded into the fp16 weights P*s_v, which are split hi + lo so the weight
+// rounding stays below 2^-22 relative.
 #include <hip/hip_runtime.h>
 
 #include "attn_common.hpp"
 
 namespace krill {
+
+typedef __attribute__((address_space(3))) void lds_void_t;
 
 __device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -36,302 +47,430 @@ __device__ __forceinline__ half8_t bytes8_exact(uint2 w) {
   return half8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
+// LDS bytes of one staged block: the head region rounded up to whole 1 KB
+// runs (one 16-byte-per-lane direct load each).
+__host__ __device__ constexpr int mfma_stage_bytes(int D, int G) { return (head_region_bytes(D, G) + 1023) & ~1023; }
+
 template <int D, int MODE, int NRT>
-__global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a, int32_t row_groups) {
+__global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
   constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
-  constexpr int KS = D / 32;  // 32-d steps of Q.K^T
-  constexpr int NDT = D / 16; // 16-d tiles of P.V
+  constexpr int KS = D / 32;   // 32-d steps of Q.K^T
+  constexpr int NDT = D / 16;  // 16-d tiles of P.V
+  constexpr int RR = 16 * NRT; // query rows of this wave
+  constexpr int STAGE = mfma_stage_bytes(D, G);
+  constexpr int NCH = STAGE / 1024;  // direct loads per block
+  static_assert(NCH <= 62, "vmcnt immediate range");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[2 * STAGE];
+
   const int lane = threadIdx.x;
   const int n = lane & 15, q4 = lane >> 4;
-  const int split = blockIdx.x;
-  const int hk = blockIdx.y / row_groups, rg = blockIdx.y % row_groups;
-  const int b = blockIdx.z;
-  const int len = a.lens[b];
-  const int nb = seq_blocks(a, len);
-  const int rbase = rg * 16 * NRT;
+  const int RG = a.row_groups;
+  const int wv = blockIdx.x, hk = blockIdx.y / RG, rg = blockIdx.y % RG;
+  const int rbase = rg * RR;
 
-  int lim[NRT];
-  bool rvalid[NRT];
-#pragma unroll
-  for (int rt = 0; rt < NRT; ++rt) {
-    const int r = rbase + 16 * rt + n;
-    rvalid[rt] = r < a.NR;
-    lim[rt] = rvalid[rt] ? len - a.Lq + r / a.R + 1 : 0;
+  // ---- this wave's flat blocks [i0, iend) of the (head, row group) order
+  const int W = a.waves;
+  int c0 = 0, lenv = lane < a.B ? a.lens[lane] : 0;
+  int nbv = seq_blocks_rg(a, lenv, rg);
+  int incl = wave_incl_scan(nbv);
+  int T = __builtin_amdgcn_readlane(incl, 63);
+  for (int cc = 64; cc < a.B; cc += 64) {
+    const int bb = cc + lane;
+    T += __builtin_amdgcn_readfirstlane(wave_allsum_int(bb < a.B ? seq_blocks_rg(a, a.lens[bb], rg) : 0));
   }
-  if (nb == 0) {
-    if (split == 0) {
-#pragma unroll
-      for (int rt = 0; rt < NRT; ++rt)
-        if (rvalid[rt] && q4 == 0)
-          for (int d = 0; d < D; ++d)
-            store_out(a.out, out_row_base(a, b, hk, rbase + 16 * rt + n, D) + d, 0.0f, a.out_dtype);
+  const int Wt = min(W, T);  // every participating wave holds >= 1 block
+  if (wv >= Wt) return;
+  const int i0 = (int)(((int64_t)wv * T + Wt - 1) / Wt);
+  const int iend = (int)(((int64_t)(wv + 1) * T + Wt - 1) / Wt);
+  int b = -1, s = 0;
+  {
+    int carry = 0;
+    for (c0 = 0; c0 < a.B; c0 += 64) {
+      if (c0 > 0) {
+        const int bb = c0 + lane;
+        lenv = bb < a.B ? a.lens[bb] : 0;
+        nbv = seq_blocks_rg(a, lenv, rg);
+        incl = wave_incl_scan(nbv) + carry;
+      }
+      const unsigned long long m = __ballot(c0 + lane < a.B && incl > i0);
+      if (m) {
+        const int l = __builtin_ctzll(m);
+        b = c0 + l;
+        s = __builtin_amdgcn_readlane(incl - nbv, l);
+        break;
+      }
+      carry = __builtin_amdgcn_readlane(incl, 63);
     }
-    return;
   }
-  const int blk0 = split * a.split_blocks;
-  if (blk0 >= nb) return;
-  const int n_splits = (nb + a.split_blocks - 1) / a.split_blocks;
-  // causal extent of the whole row group
-  const int rlast = min(a.NR, rbase + 16 * NRT) - 1;
-  const int lim_max = len - a.Lq + rlast / a.R + 1;
-  const int nb_vis = min(nb, (lim_max + 63) >> 6);
-  const int blk1 = min(min(nb, blk0 + a.split_blocks), nb_vis);
+  if (b < 0) return;
+  auto seq_len = [&](int bs) -> int { return bs - c0 < 64 ? __builtin_amdgcn_readlane(lenv, bs - c0) : a.lens[bs]; };
 
-  // Q^T operands: lane holds q[row n][32*ks + 8*q4 .. +8] per row tile.
+  // block-table entries of flat blocks i0 .. iend-1 (<= 64), lane j: block i0 + j
+  int tab = 0, iend_eff = iend;
+  {
+    const int f = i0 + lane;
+    int bs = b, ss = s;
+    while (bs < a.B && ss < iend) {
+      const int nbs = seq_blocks_rg(a, seq_len(bs), rg);
+      if (f < iend && f >= ss && f < ss + nbs) {
+        const int phys = a.tables[(int64_t)bs * a.max_blocks + (f - ss)];
+        tab = (unsigned)phys < (unsigned)a.lv.num_blocks ? phys : 0;
+      }
+      ss += nbs;
+      ++bs;
+    }
+    if (ss < iend) iend_eff = ss;
+  }
+  // Copies flat block i into stage `buf` (after the wave's last block the
+  // resource is empty: the loads return zeros without a memory access).
+  auto issue = [&](int i, int buf) {
+    const bool ok = i < iend_eff;
+    const int phys = __builtin_amdgcn_readlane(tab, ok ? i - i0 : 0);
+    const __amdgpu_buffer_rsrc_t r = block_rsrc(head_region(a.lv, phys, hk), ok ? a.lv.head_bytes : 0);
+    uint8_t *dst = ring + buf * STAGE;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(dst + c * 1024), 16, c * 1024 + lane * 16, 0, 0, 2);
+  };
+
+  // ---- Q^T operands of sequence bq: lane holds q[row n][32 ks + 8 q4 .. +8]
   half8_t qB[NRT][KS];
   float qsum[NRT][G];
+  bool rvalid[NRT];
 #pragma unroll
-  for (int rt = 0; rt < NRT; ++rt) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) qsum[rt][g] = 0.0f;
-    const int r = rbase + 16 * rt + n;
-    const int hq = hk * a.R + r % a.R, j = r / a.R;
-    const uint16_t *qp = a.q + (((int64_t)b * a.Hq + hq) * a.Lq + j) * D;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      half8_t v;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const _Float16 h = rvalid[rt] ? (_Float16)load_q(qp + 32 * ks + 8 * q4 + e, a.q_dtype) : (_Float16)0.0f;
-        v[e] = h;
-        qsum[rt][MODE == MODE_AFFINE ? ks / 2 : 0] += (float)h;
-      }
-      qB[rt][ks] = v;
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      qsum[rt][g] += shfl_xor(qsum[rt][g], 16);
-      qsum[rt][g] += shfl_xor(qsum[rt][g], 32);
-    }
-  }
-
-  float m_run[NRT], l_part[NRT], c_part[NRT][G];
-  float4_t oacc[NRT][NDT];
-#pragma unroll
-  for (int rt = 0; rt < NRT; ++rt) {
-    m_run[rt] = -INFINITY;
-    l_part[rt] = 0.0f;
-#pragma unroll
-    for (int g = 0; g < G; ++g) c_part[rt][g] = 0.0f;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) oacc[rt][dt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  }
-  const half2_t m1024 = half2_t{(_Float16)-1024.0f, (_Float16)-1024.0f};
-
-  for (int blk = blk0; blk < blk1; ++blk) {
-    int phys = a.tables[(int64_t)b * a.max_blocks + blk];
-    phys = (unsigned)phys < (unsigned)a.lv.num_blocks ? phys : 0;
-    const uint8_t *reg = head_region(a.lv, phys, hk);
-    const int tbase = blk << 6;
-
-    // ---- S^T = K . Q^T, four 16-token tiles
-    float sc[4][NRT][4];
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const int tokA = 16 * tt + n;  // A-operand row
-      half2_t ks2 = half2_t{(_Float16)0.0f, (_Float16)0.0f}, kz2 = ks2;
-      if constexpr (MODE == MODE_REF) {
-        const uint32_t km = *reinterpret_cast<const uint32_t *>(reg + km_offset(D) + (tokA << 2));
-        const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)(km & 0xffffu));
-        const _Float16 z = __builtin_bit_cast(_Float16, (uint16_t)(km >> 16));
-        ks2 = half2_t{s, s};
-        kz2 = half2_t{z, z};
-      }
-      float4_t sacc[NRT][G];
-#pragma unroll
-      for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-        for (int g = 0; g < G; ++g) sacc[rt][g] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const uint2 kb = *reinterpret_cast<const uint2 *>(reg + k_byte(tokA, 32 * ks + 8 * q4));
-        half8_t A;
-        if constexpr (MODE == MODE_REF) {
-          half2_t p0 = (bytes01_plus1024(kb.x) + m1024) * ks2 + kz2;
-          half2_t p1 = (bytes23_plus1024(kb.x) + m1024) * ks2 + kz2;
-          half2_t p2 = (bytes01_plus1024(kb.y) + m1024) * ks2 + kz2;
-          half2_t p3 = (bytes23_plus1024(kb.y) + m1024) * ks2 + kz2;
-          A = half8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-        } else {
-          A = bytes8_exact(kb);
-        }
-        const int g = MODE == MODE_AFFINE ? ks / 2 : 0;
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) sacc[rt][g] = mfma16x16x32(A, qB[rt][ks], sacc[rt][g]);
-      }
-      // lane holds tokens 16*tt + 4*q4 + e for row n
-      const int tok0 = 16 * tt + 4 * q4;
-      float kss[4][G], kzz[4][G];
-      if constexpr (MODE == MODE_AFFINE) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const uint32_t km = *reinterpret_cast<const uint32_t *>(reg + km_offset(D) + (((tok0 + e) * G + g) << 2));
-            kss[e][g] = f16_bits_to_f32((uint16_t)(km & 0xffffu));
-            kzz[e][g] = f16_bits_to_f32((uint16_t)(km >> 16));
-          }
-      }
-#pragma unroll
-      for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float s;
-          if constexpr (MODE == MODE_AFFINE) {
-            s = 0.0f;
-#pragma unroll
-            for (int g = 0; g < G; ++g) s += kss[e][g] * sacc[rt][g][e] + kzz[e][g] * qsum[rt][g];
-          } else {
-            s = sacc[rt][0][e];
-          }
-          sc[tt][rt][e] = (tbase + tok0 + e < lim[rt]) ? s * a.scale_log2 : -INFINITY;
-        }
-    }
-
-    // ---- online softmax (row n of each tile; its 64 scores live in the
-    // four lanes n, n+16, n+32, n+48)
+  for (int rt = 0; rt < NRT; ++rt) rvalid[rt] = rbase + 16 * rt + n < a.NR;
+  uint4 qraw[NRT][KS];
+  auto load_q = [&](int bq) {
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
-      float mb = -INFINITY;
+      const int r = rvalid[rt] ? rbase + 16 * rt + n : 0;
+      const int hq = hk * a.R + r % a.R, j = r / a.R;
+      const uint16_t *qp = a.q + (((int64_t)bq * a.Hq + hq) * a.Lq + j) * D;
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
+      for (int ks = 0; ks < KS; ++ks) qraw[rt][ks] = *reinterpret_cast<const uint4 *>(qp + 32 * ks + 8 * q4);
+    }
+  };
+  auto finish_q = [&]() {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) mb = fmaxf(mb, sc[tt][rt][e]);
-      mb = fmaxf(mb, shfl_xor(mb, 16));
-      mb = fmaxf(mb, shfl_xor(mb, 32));
-      const float mn = fmaxf(m_run[rt], mb);
-      const float mu = mn == -INFINITY ? 0.0f : mn;
-      const float al = fast_exp2(m_run[rt] - mu);
-      m_run[rt] = mn;
-      float ps = 0.0f;
+    for (int rt = 0; rt < NRT; ++rt) {
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
+      for (int g = 0; g < G; ++g) qsum[rt][g] = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const uint32_t w4[4] = {qraw[rt][ks].x, qraw[rt][ks].y, qraw[rt][ks].z, qraw[rt][ks].w};
+        half8_t v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          sc[tt][rt][e] = fast_exp2(sc[tt][rt][e] - mu);
-          ps += sc[tt][rt][e];
+          _Float16 lo, hi;
+          if (a.q_dtype == DT_BF16) {
+            lo = (_Float16)__builtin_bit_cast(float, w4[e] << 16);
+            hi = (_Float16)__builtin_bit_cast(float, w4[e] & 0xffff0000u);
+          } else {
+            lo = __builtin_bit_cast(_Float16, (uint16_t)(w4[e] & 0xffffu));
+            hi = __builtin_bit_cast(_Float16, (uint16_t)(w4[e] >> 16));
+          }
+          if (!rvalid[rt]) lo = hi = (_Float16)0.0f;
+          v[2 * e] = lo;
+          v[2 * e + 1] = hi;
+          qsum[rt][MODE == MODE_AFFINE ? ks / 2 : 0] += (float)lo + (float)hi;
         }
-      l_part[rt] = l_part[rt] * al + ps;
+        qB[rt][ks] = v;
+      }
 #pragma unroll
-      for (int g = 0; g < G; ++g) c_part[rt][g] *= al;
+      for (int g = 0; g < G; ++g) {
+        qsum[rt][g] += shfl_xor(qsum[rt][g], 16);
+        qsum[rt][g] += shfl_xor(qsum[rt][g], 32);
+      }
+    }
+  };
+
+  // queries first, then the first two blocks: waits on the queries do not
+  // cover the block copies
+  load_q(b);
+  issue(i0, 0);
+  issue(i0 + 1, 1);
+  finish_q();
+
+  const half2_t m1024 = half2_t{(_Float16)-1024.0f, (_Float16)-1024.0f};
+  int i = i0;
+  while (true) {
+    const int len = seq_len(b);
+    const int e = s + seq_blocks_rg(a, len, rg);
+    const int seg_end = min(e, iend_eff);
+    int lim[NRT];
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) oacc[rt][dt] *= al;
+    for (int rt = 0; rt < NRT; ++rt) {
+      const int r = rbase + 16 * rt + n;
+      lim[rt] = rvalid[rt] ? len - a.Lq + r / a.R + 1 : 0;
+    }
+    float m_run[NRT], l_part[NRT], c_part[NRT][G];
+    float4_t oacc[NRT][NDT];
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt) {
+      m_run[rt] = -INFINITY;
+      l_part[rt] = 0.0f;
+#pragma unroll
+      for (int g = 0; g < G; ++g) c_part[rt][g] = 0.0f;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) oacc[rt][dt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    // ---- O^T += V^T . P^T over two 32-token groups
+    for (; i < seg_end; ++i) {
+      const int buf = (i - i0) & 1;
+      // stage `buf` holds block i once every load but the NCH youngest (the
+      // other stage's copy) has completed
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCH) : "memory");
+      const uint8_t *st = ring + buf * STAGE;
+      const int tbase = (i - s) << 6;
+
+      // ---- S^T = K . Q^T, four 16-token tiles
+      float sc[4][NRT][4];
 #pragma unroll
-    for (int tg = 0; tg < 2; ++tg) {
-      // logical k = 8*q4 + i  <->  token 32*tg + (i < 4 ? 4*q4 + i : 16 + 4*q4 + i - 4)
-      float vss[8][G], vzz[8][G];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int tok = 32 * tg + (i < 4 ? 4 * q4 + i : 16 + 4 * q4 + (i - 4));
-        const bool valid = tbase + tok < len;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const uint32_t vm =
-              valid ? *reinterpret_cast<const uint32_t *>(reg + vm_offset(D, G) + ((tok * G + g) << 2)) : 0u;
-          vss[i][g] = f16_bits_to_f32((uint16_t)(vm & 0xffffu));
-          vzz[i][g] = f16_bits_to_f32((uint16_t)(vm >> 16));
+      for (int tt = 0; tt < 4; ++tt) {
+        const int tokA = 16 * tt + n;  // A-operand row
+        half2_t ks2 = half2_t{(_Float16)0.0f, (_Float16)0.0f}, kz2 = ks2;
+        if constexpr (MODE == MODE_REF) {
+          const uint32_t km = *reinterpret_cast<const uint32_t *>(st + km_offset(D) + (tokA << 2));
+          const _Float16 sk = __builtin_bit_cast(_Float16, (uint16_t)(km & 0xffffu));
+          const _Float16 zk = __builtin_bit_cast(_Float16, (uint16_t)(km >> 16));
+          ks2 = half2_t{sk, sk};
+          kz2 = half2_t{zk, zk};
         }
+        float4_t sacc[NRT][G];
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+          for (int g = 0; g < G; ++g) sacc[rt][g] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const uint2 kb = *reinterpret_cast<const uint2 *>(st + k_byte(tokA, 32 * ks + 8 * q4));
+          half8_t A;
+          if constexpr (MODE == MODE_REF) {
+            half2_t p0 = (bytes01_plus1024(kb.x) + m1024) * ks2 + kz2;
+            half2_t p1 = (bytes23_plus1024(kb.x) + m1024) * ks2 + kz2;
+            half2_t p2 = (bytes01_plus1024(kb.y) + m1024) * ks2 + kz2;
+            half2_t p3 = (bytes23_plus1024(kb.y) + m1024) * ks2 + kz2;
+            A = half8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+          } else {
+            A = bytes8_exact(kb);
+          }
+          const int g = MODE == MODE_AFFINE ? ks / 2 : 0;
+#pragma unroll
+          for (int rt = 0; rt < NRT; ++rt) sacc[rt][g] = mfma16x16x32(A, qB[rt][ks], sacc[rt][g]);
+        }
+        // lane holds tokens 16*tt + 4*q4 + e for row n
+        const int tok0 = 16 * tt + 4 * q4;
+        float kss[4][G], kzz[4][G];
+        if constexpr (MODE == MODE_AFFINE) {
+          // (scale, zero) pairs of tokens tok0 .. tok0+3, G per token: 16 G contiguous bytes
+          uint32_t km[4 * G];
+#pragma unroll
+          for (int c = 0; c < G; ++c) {
+            const uint4 w = *reinterpret_cast<const uint4 *>(st + km_offset(D) + ((tok0 * G) << 2) + 16 * c);
+            km[4 * c] = w.x;
+            km[4 * c + 1] = w.y;
+            km[4 * c + 2] = w.z;
+            km[4 * c + 3] = w.w;
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              kss[e][g] = f16_bits_to_f32((uint16_t)(km[e * G + g] & 0xffffu));
+              kzz[e][g] = f16_bits_to_f32((uint16_t)(km[e * G + g] >> 16));
+            }
+        }
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float sv;
+            if constexpr (MODE == MODE_AFFINE) {
+              sv = 0.0f;
+#pragma unroll
+              for (int g = 0; g < G; ++g) sv += kss[e][g] * sacc[rt][g][e] + kzz[e][g] * qsum[rt][g];
+            } else {
+              sv = sacc[rt][0][e];
+            }
+            sc[tt][rt][e] = (tbase + tok0 + e < lim[rt]) ? sv * a.scale_log2 : -INFINITY;
+          }
       }
-      half8_t Bhi[NRT][G], Blo[NRT][G];
+
+      // ---- online softmax (row n of each tile; its 64 scores live in the
+      // four lanes n, n+16, n+32, n+48)
 #pragma unroll
       for (int rt = 0; rt < NRT; ++rt) {
+        float mb = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float p = sc[2 * tg + (i >> 2)][rt][i & 3];
+        for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const float w = MODE == MODE_AFFINE ? p * vss[i][g] : p;
-            const _Float16 hi = (_Float16)w;
-            const _Float16 lo = (_Float16)(w - (float)hi);
-            Bhi[rt][g][i] = hi;
-            Blo[rt][g][i] = lo;
-            if constexpr (MODE == MODE_AFFINE) c_part[rt][g] += p * vzz[i][g];
+          for (int e = 0; e < 4; ++e) mb = fmaxf(mb, sc[tt][rt][e]);
+        mb = fmaxf(mb, shfl_xor(mb, 16));
+        mb = fmaxf(mb, shfl_xor(mb, 32));
+        const float mn = fmaxf(m_run[rt], mb);
+        const float mu = mn == -INFINITY ? 0.0f : mn;
+        const float al = fast_exp2(m_run[rt] - mu);
+        m_run[rt] = mn;
+        float ps = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            sc[tt][rt][e] = fast_exp2(sc[tt][rt][e] - mu);
+            ps += sc[tt][rt][e];
+          }
+        l_part[rt] = l_part[rt] * al + ps;
+#pragma unroll
+        for (int g = 0; g < G; ++g) c_part[rt][g] *= al;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) oacc[rt][dt] *= al;
+      }
+
+      // ---- O^T += V^T . P^T over two 32-token groups
+#pragma unroll
+      for (int tg = 0; tg < 2; ++tg) {
+        // logical k = 8*q4 + i  <->  token 32*tg + (i < 4 ? 4*q4 + i : 16 + 4*q4 + i - 4)
+        float vss[8][G], vzz[8][G];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int tokh = 32 * tg + 16 * h + 4 * q4;  // 4 tokens, G pairs each: 16 G bytes
+          uint32_t vm[4 * G];
+#pragma unroll
+          for (int c = 0; c < G; ++c) {
+            const uint4 w = *reinterpret_cast<const uint4 *>(st + vm_offset(D, G) + ((tokh * G) << 2) + 16 * c);
+            vm[4 * c] = w.x;
+            vm[4 * c + 1] = w.y;
+            vm[4 * c + 2] = w.z;
+            vm[4 * c + 3] = w.w;
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const bool valid = tbase + tokh + e < len;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              const uint32_t w = valid ? vm[e * G + g] : 0u;
+              vss[4 * h + e][g] = f16_bits_to_f32((uint16_t)(w & 0xffffu));
+              vzz[4 * h + e][g] = f16_bits_to_f32((uint16_t)(w >> 16));
+            }
+          }
+        }
+        half8_t Bhi[NRT][G], Blo[NRT][G];
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const float p = sc[2 * tg + (k >> 2)][rt][k & 3];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              const float w = MODE == MODE_AFFINE ? p * vss[k][g] : p;
+              const _Float16 hi = (_Float16)w;
+              const _Float16 lo = (_Float16)(w - (float)hi);
+              Bhi[rt][g][k] = hi;
+              Blo[rt][g][k] = lo;
+              if constexpr (MODE == MODE_AFFINE) c_part[rt][g] += p * vzz[k][g];
+            }
+          }
+        }
+        half2_t sp[4], zp[4];
+        if constexpr (MODE == MODE_REF) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            sp[k] = half2_t{(_Float16)vss[2 * k][0], (_Float16)vss[2 * k + 1][0]};
+            zp[k] = half2_t{(_Float16)vzz[2 * k][0], (_Float16)vzz[2 * k + 1][0]};
+          }
+        }
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const int d = 16 * dt + n;
+          const uint2 vb = *reinterpret_cast<const uint2 *>(st + v_pos_byte(D, tg, d, 8 * q4));
+          half8_t A;
+          if constexpr (MODE == MODE_REF) {
+            half2_t p0 = (bytes01_plus1024(vb.x) + m1024) * sp[0] + zp[0];
+            half2_t p1 = (bytes23_plus1024(vb.x) + m1024) * sp[1] + zp[1];
+            half2_t p2 = (bytes01_plus1024(vb.y) + m1024) * sp[2] + zp[2];
+            half2_t p3 = (bytes23_plus1024(vb.y) + m1024) * sp[3] + zp[3];
+            A = half8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+          } else {
+            A = bytes8_exact(vb);
+          }
+          const int g = MODE == MODE_AFFINE ? dt / 4 : 0;
+#pragma unroll
+          for (int rt = 0; rt < NRT; ++rt) {
+            oacc[rt][dt] = mfma16x16x32(A, Bhi[rt][g], oacc[rt][dt]);
+            oacc[rt][dt] = mfma16x16x32(A, Blo[rt][g], oacc[rt][dt]);
           }
         }
       }
-      half2_t sp[4], zp[4];
-      if constexpr (MODE == MODE_REF) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sp[i] = half2_t{(_Float16)vss[2 * i][0], (_Float16)vss[2 * i + 1][0]};
-          zp[i] = half2_t{(_Float16)vzz[2 * i][0], (_Float16)vzz[2 * i + 1][0]};
-        }
-      }
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const int d = 16 * dt + n;
-        const uint2 vb = *reinterpret_cast<const uint2 *>(reg + v_pos_byte(D, tg, d, 8 * q4));
-        half8_t A;
-        if constexpr (MODE == MODE_REF) {
-          half2_t p0 = (bytes01_plus1024(vb.x) + m1024) * sp[0] + zp[0];
-          half2_t p1 = (bytes23_plus1024(vb.x) + m1024) * sp[1] + zp[1];
-          half2_t p2 = (bytes01_plus1024(vb.y) + m1024) * sp[2] + zp[2];
-          half2_t p3 = (bytes23_plus1024(vb.y) + m1024) * sp[3] + zp[3];
-          A = half8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-        } else {
-          A = bytes8_exact(vb);
-        }
-        const int g = MODE == MODE_AFFINE ? dt / 4 : 0;
-#pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-          oacc[rt][dt] = mfma16x16x32(A, Bhi[rt][g], oacc[rt][dt]);
-          oacc[rt][dt] = mfma16x16x32(A, Blo[rt][g], oacc[rt][dt]);
-        }
-      }
+      // every LDS read of this stage has returned: refill it two blocks ahead
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue(i + 2, buf);
     }
-  }
 
-  // ---- epilogue: lane holds O^T[d = 16*dt + 4*q4 + e][row n]
+    // ---- end of the segment: lane holds O^T[d = 16*dt + 4*q4 + e][row n].
+    // The whole sequence in this wave -> output; otherwise a partial in slot
+    // (hk * row_groups + rg) * (waves + B) + wave + b.
+    const bool whole = s >= i0 && e <= iend;
+    const int64_t slot = ((int64_t)hk * RG + rg) * (a.waves + a.B) + wv + b;
 #pragma unroll
-  for (int rt = 0; rt < NRT; ++rt) {
-    float l = l_part[rt];
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
-    float cg[G];
+    for (int rt = 0; rt < NRT; ++rt) {
+      float l = l_part[rt];
+      l += shfl_xor(l, 16);
+      l += shfl_xor(l, 32);
+      float cg[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float c = c_part[rt][g];
-      c += shfl_xor(c, 16);
-      c += shfl_xor(c, 32);
-      cg[g] = c;
-    }
-    if (!rvalid[rt]) continue;
-    const int r = rbase + 16 * rt + n;
-    if (n_splits == 1) {
-      const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-      const int64_t ob = out_row_base(a, b, hk, r, D);
+      for (int g = 0; g < G; ++g) {
+        float c = c_part[rt][g];
+        c += shfl_xor(c, 16);
+        c += shfl_xor(c, 32);
+        cg[g] = c;
+      }
+      if (!rvalid[rt]) continue;
+      const int r = rbase + 16 * rt + n;
+      if (whole) {
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        const int64_t ob = out_row_base(a, b, hk, r, D);
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
+        for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int d = 16 * dt + 4 * q4 + e;
-          store_out(a.out, ob + d, (oacc[rt][dt][e] + cg[MODE == MODE_AFFINE ? d / 64 : 0]) * inv, a.out_dtype);
+          for (int e2 = 0; e2 < 4; ++e2) {
+            const int d = 16 * dt + 4 * q4 + e2;
+            store_out(a.out, ob + d, (oacc[rt][dt][e2] + cg[MODE == MODE_AFFINE ? d / 64 : 0]) * inv, a.out_dtype);
+          }
+      } else {
+        const int64_t pi = slot * RR + 16 * rt + n;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          float4 o;
+          const int d = 16 * dt + 4 * q4;
+          const float c = cg[MODE == MODE_AFFINE ? d / 64 : 0];
+          o.x = oacc[rt][dt][0] + c;
+          o.y = oacc[rt][dt][1] + c;
+          o.z = oacc[rt][dt][2] + c;
+          o.w = oacc[rt][dt][3] + c;
+          *reinterpret_cast<float4 *>(a.ws_o + pi * D + d) = o;
         }
-    } else {
-      const int64_t pi = part_index(a, b, hk, split, r);
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int d = 16 * dt + 4 * q4 + e;
-          a.ws_o[pi * D + d] = oacc[rt][dt][e] + cg[MODE == MODE_AFFINE ? d / 64 : 0];
-        }
-      if (q4 == 0) {
-        a.ws_ml[pi * 2] = m_run[rt];
-        a.ws_ml[pi * 2 + 1] = l;
+        if (q4 == 0) reinterpret_cast<float2 *>(a.ws_ml)[pi] = float2{m_run[rt], l};
       }
     }
+    if (i >= iend_eff) break;
+    // next sequence with blocks for this row group (the merge zero-fills the others)
+    ++b;
+    s = e;
+    while (b < a.B && seq_blocks_rg(a, seq_len(b), rg) == 0) ++b;
+    if (b >= a.B) break;
+    load_q(b);
+    finish_q();
   }
+  // the loads issued after the last block (empty resources) still write the
+  // ring: let them land before the wave ends
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 template <int D, int MODE>
-static hipError_t launch_mfma_nrt(const AttnArgs &args, int NRT, int row_groups, dim3 grid, hipStream_t st) {
+static hipError_t launch_mfma_nrt(const AttnArgs &args, int NRT, dim3 grid, hipStream_t st) {
   switch (NRT) {
-    case 1: k_attn_mfma<D, MODE, 1><<<grid, dim3(64), 0, st>>>(args, row_groups); break;
-    case 2: k_attn_mfma<D, MODE, 2><<<grid, dim3(64), 0, st>>>(args, row_groups); break;
+    case 1: k_attn_mfma<D, MODE, 1><<<grid, dim3(64), 0, st>>>(args); break;
+    case 2: k_attn_mfma<D, MODE, 2><<<grid, dim3(64), 0, st>>>(args); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -339,22 +478,59 @@ static hipError_t launch_mfma_nrt(const AttnArgs &args, int NRT, int row_groups,
 
 hipError_t launch_attn_mfma(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
                             hipStream_t st) {
+  // one VGPR of block-table entries per wave
+  if (p.waves < 1 || (int64_t)p.waves * 64 < (int64_t)a.B * p.nb_cap) return hipErrorInvalidValue;
+  if (p.nrt < 1 || p.nrt > 2 || (g.D >= 256 && p.nrt != 1) || p.rows_per_group != 16 * p.nrt ||
+      p.row_groups * p.rows_per_group < p.NR)
+    return hipErrorInvalidValue;
   const AttnArgs args = make_attn_args(g, layer, a, p);
-  const int NRT = p.nrt;
-  const dim3 grid((unsigned)p.max_splits, (unsigned)(g.Hkv * p.row_groups), (unsigned)a.B);
+  const dim3 grid((unsigned)p.waves, (unsigned)(g.Hkv * p.row_groups));
   switch (g.D) {
     case 64:
-      return g.mode == MODE_REF ? launch_mfma_nrt<64, MODE_REF>(args, NRT, p.row_groups, grid, st)
-                                : launch_mfma_nrt<64, MODE_AFFINE>(args, NRT, p.row_groups, grid, st);
+      return g.mode == MODE_REF ? launch_mfma_nrt<64, MODE_REF>(args, p.nrt, grid, st)
+                                : launch_mfma_nrt<64, MODE_AFFINE>(args, p.nrt, grid, st);
     case 128:
-      return g.mode == MODE_REF ? launch_mfma_nrt<128, MODE_REF>(args, NRT, p.row_groups, grid, st)
-                                : launch_mfma_nrt<128, MODE_AFFINE>(args, NRT, p.row_groups, grid, st);
+      return g.mode == MODE_REF ? launch_mfma_nrt<128, MODE_REF>(args, p.nrt, grid, st)
+                                : launch_mfma_nrt<128, MODE_AFFINE>(args, p.nrt, grid, st);
     case 256:
-      return g.mode == MODE_REF ? launch_mfma_nrt<256, MODE_REF>(args, NRT, p.row_groups, grid, st)
-                                : launch_mfma_nrt<256, MODE_AFFINE>(args, NRT, p.row_groups, grid, st);
+      return g.mode == MODE_REF ? launch_mfma_nrt<256, MODE_REF>(args, p.nrt, grid, st)
+                                : launch_mfma_nrt<256, MODE_AFFINE>(args, p.nrt, grid, st);
     default:
       return hipErrorInvalidValue;
   }
+}
+
+template <int D, int MODE>
+static int32_t occupancy_mfma(int nrt) {
+  int n = 0;
+  hipError_t e = nrt == 2 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                                &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, 2>), 64, 0)
+                          : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                                &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, 1>), 64, 0);
+  if (e != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    n = (160 * 1024) / (2 * mfma_stage_bytes(D, MODE == MODE_AFFINE ? D / 64 : 1));
+  }
+  return n;
+}
+
+int32_t mfma_waves_per_cu(const PoolGeometry &g, int32_t nrt) {
+  const int dsel = g.D == 64 ? 0 : g.D == 128 ? 1 : 2;
+  if (nrt < 1 || nrt > 2) return 4;
+  if (g.num_cus <= 0) {  // host-only pool: the LDS bound (two stages per wave, 160 KB per CU)
+    static const int est[3] = {8, 4, 2};
+    return est[dsel];
+  }
+  static int cache[2][3][3] = {};  // [mode][D][nrt], filled on first use per process
+  int &c = cache[g.mode == MODE_AFFINE][dsel][nrt];
+  if (c == 0) {
+    int v = 4;
+    if (g.D == 64) v = g.mode == MODE_REF ? occupancy_mfma<64, MODE_REF>(nrt) : occupancy_mfma<64, MODE_AFFINE>(nrt);
+    else if (g.D == 128) v = g.mode == MODE_REF ? occupancy_mfma<128, MODE_REF>(nrt) : occupancy_mfma<128, MODE_AFFINE>(nrt);
+    else v = g.mode == MODE_REF ? occupancy_mfma<256, MODE_REF>(nrt) : occupancy_mfma<256, MODE_AFFINE>(nrt);
+    c = v;
+  }
+  return c;
 }
 
 }  // namespace krill

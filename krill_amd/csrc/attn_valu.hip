@@ -77,12 +77,6 @@ __device__ __forceinline__ void dot8_bcast(float &acc, uint32_t q, const half2_t
 #undef KRILL_DOT8_BODY
 #undef KRILL_DOT8_OPERANDS
 
-// Block region of the pool as a buffer resource: loads past `bytes` return
-// zero without touching memory, so the prefetch after a wave's last block is
-// free (bytes = 0).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const uint8_t *p, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p), (short)0, bytes, 0x00020000);
-}
 // Streaming (non-temporal) loads: each block byte is read once per launch.
 __device__ __forceinline__ uint4 ld_stream16(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));

@@ -64,6 +64,13 @@ __device__ __forceinline__ uint8_t *head_region(const LayerView &lv, int32_t blo
   return lv.base + (int64_t)block * lv.block_stride + (int64_t)h * lv.head_bytes;
 }
 
+// Block region of the pool as a buffer resource: loads past `bytes` return
+// zero without touching memory, so the prefetch after a wave's last block is
+// free (bytes = 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const uint8_t *p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p), (short)0, bytes, 0x00020000);
+}
+
 // ---------------------------------------------------------------- dtypes
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {

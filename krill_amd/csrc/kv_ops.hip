@@ -268,18 +268,20 @@ __global__ __launch_bounds__(256) void k_copy_pairs(uint8_t *base, int64_t layer
 // saw no visible key carry m = -inf and contribute nothing.
 // ---------------------------------------------------------------------------
 // Combines the n consecutive partial slots starting at `slot0` for row r.
-// The (m, l) pairs of the first 64 slots (lane s: slot s) and the o vectors
-// of the first K0 slots (32 registers' worth) are loaded in one round; later
-// slots (rare) loop.
+// Merge of the n consecutive partial slots slot0 .. slot0+n-1 of one query
+// row (row rr of RR rows per slot) into the output row at obase.  The (m, l)
+// pairs of the first 64 slots (lane s: slot s) and the o vectors of the
+// first K0 slots (32 registers' worth) are loaded in one round; later slots
+// (rare) loop.
 template <int D>
-__device__ __forceinline__ void merge_slots(const AttnArgs &a, int64_t slot0, int n, int r, int64_t obase) {
+__device__ __forceinline__ void merge_slots(const AttnArgs &a, int64_t slot0, int n, int rr, int RR, int64_t obase) {
   constexpr int E = D / 64;  // d = lane + 64 e
   constexpr int K0 = 32 / E;
   __shared__ float w_lds[64];
   const int lane = threadIdx.x;
   const float2 *ml2 = reinterpret_cast<const float2 *>(a.ws_ml);
-  auto orow = [&](int k) { return a.ws_o + ((slot0 + k) * a.NR + r) * (int64_t)D + lane; };
-  float2 ml = lane < n ? ml2[(slot0 + lane) * a.NR + r] : float2{-INFINITY, 0.0f};
+  auto orow = [&](int k) { return a.ws_o + ((slot0 + k) * RR + rr) * (int64_t)D + lane; };
+  float2 ml = lane < n ? ml2[(slot0 + lane) * RR + rr] : float2{-INFINITY, 0.0f};
   float ov[K0][E];
 #pragma unroll
   for (int k = 0; k < K0; ++k)
@@ -287,14 +289,14 @@ __device__ __forceinline__ void merge_slots(const AttnArgs &a, int64_t slot0, in
     for (int e = 0; e < E; ++e) ov[k][e] = k < n ? orow(k)[64 * e] : 0.0f;
   float M = ml.x;
   for (int s0 = 64; s0 < n; s0 += 64)
-    if (s0 + lane < n) M = fmaxf(M, ml2[(slot0 + s0 + lane) * a.NR + r].x);
+    if (s0 + lane < n) M = fmaxf(M, ml2[(slot0 + s0 + lane) * RR + rr].x);
   M = wave_allmax(M);
   float acc[E], lpart = 0.0f;
 #pragma unroll
   for (int e = 0; e < E; ++e) acc[e] = 0.0f;
   for (int s0 = 0; s0 < n; s0 += 64) {
     const int cnt = min(64, n - s0);
-    if (s0 > 0) ml = lane < cnt ? ml2[(slot0 + s0 + lane) * a.NR + r] : float2{-INFINITY, 0.0f};
+    if (s0 > 0) ml = lane < cnt ? ml2[(slot0 + s0 + lane) * RR + rr] : float2{-INFINITY, 0.0f};
     const float w = lane < cnt && ml.x != -INFINITY ? fast_exp2(ml.x - M) : 0.0f;
     lpart += w * ml.y;
     w_lds[lane] = w;
@@ -324,29 +326,20 @@ __device__ __forceinline__ void merge_slots(const AttnArgs &a, int64_t slot0, in
   for (int e = 0; e < E; ++e) store_out(a.out, obase + lane + 64 * e, acc[e] * inv, a.out_dtype);
 }
 
-// After the MFMA kernel: splits of split_blocks blocks per sequence.  A
-// sequence with one split (or none) was written by the attention kernel.
-template <int D>
-__global__ __launch_bounds__(64) void k_attn_merge_split(AttnArgs a) {
-  const int r = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
-  const int nb = seq_blocks(a, a.lens[b]);
-  const int n_splits = (nb + a.split_blocks - 1) / a.split_blocks;
-  if (n_splits <= 1) return;
-  merge_slots<D>(a, part_index(a, b, hk, 0, 0) / a.NR, n_splits, r, out_row_base(a, b, hk, r, D));
-}
-
-// After the VALU kernel (flat block order, T blocks split evenly over the
-// waves): sequence b's blocks are flat [s, s + nb), covered by waves
-// flat_wave_of(s) .. flat_wave_of(s + nb - 1), whose partials sit in
-// consecutive slots wave + b.  A sequence inside one wave was written by the
-// attention kernel; an empty one gets zeros here.
+// After either attention kernel (flat block order per (KV head, row group),
+// T blocks split evenly over the waves): sequence b's blocks are flat
+// [s, s + nb), covered by waves flat_wave_of(s) .. flat_wave_of(s + nb - 1),
+// whose partials sit in consecutive slots wave + b.  A sequence inside one
+// wave was written by the attention kernel; one with no blocks for this row
+// gets zeros here.
 template <int D>
 __global__ __launch_bounds__(64) void k_attn_merge_flat(AttnArgs a) {
   const int r = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x;
   const int64_t obase = out_row_base(a, b, hk, r, D);
+  const int rg = r / a.rows_per_group, rr = r % a.rows_per_group;
   int s = 0, nb = 0;
-  const int T = flat_total_and_start(a, b, s, nb);
+  const int T = flat_total_and_start(a, b, rg, s, nb);
   if (nb == 0) {
 #pragma unroll
     for (int e = 0; e < D / 64; ++e) store_out(a.out, obase + lane + 64 * e, 0.0f, a.out_dtype);
@@ -355,7 +348,8 @@ __global__ __launch_bounds__(64) void k_attn_merge_flat(AttnArgs a) {
   const int Wt = min(a.waves, T);  // waves that took part (each holds >= 1 block)
   const int first = flat_wave_of(s, T, Wt), last = flat_wave_of(s + nb - 1, T, Wt);
   if (first == last) return;
-  merge_slots<D>(a, (int64_t)hk * (a.waves + a.B) + first + b, last - first + 1, r, obase);
+  const int64_t slot0 = ((int64_t)hk * a.row_groups + rg) * (a.waves + a.B) + first + b;
+  merge_slots<D>(a, slot0, last - first + 1, rr, a.rows_per_group, obase);
 }
 
 // ---------------------------------------------------------------------------
@@ -493,47 +487,40 @@ int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq,
   p.use_mfma = path == 2 || (path == 0 && p.NR > 8);
   if (!p.use_mfma && p.NR > 8) return -2;
   const int32_t nb_max = std::max(1, (max_seq_len + 63) / 64);
+  const int64_t tmax = (int64_t)B * nb_max;
+  const int64_t cus = g.num_cus > 0 ? g.num_cus : 256;
   if (p.use_mfma) {
     // MFMA: at most 32 query rows per wave (16 for D = 256) keeps the score,
-    // output and operand tiles in registers without spilling.
+    // output and operand tiles in registers; more rows form row groups.
     const int32_t max_tiles = g.D >= 256 ? 1 : 2;
     p.nrt = std::min(max_tiles, (p.NR + 15) / 16);
-    p.row_groups = (p.NR + 16 * p.nrt - 1) / (16 * p.nrt);
-    int32_t sb = split_blocks;
-    if (sb <= 0) {
-      // about 4096 workgroups over the longest sequence; at least 2 blocks
-      const int64_t units = (int64_t)B * g.Hkv * p.row_groups;
-      sb = (int32_t)std::max<int64_t>(2, ((int64_t)nb_max * units + 4095) / 4096);
-    }
-    sb = std::min(sb, nb_max);
-    p.split_blocks = sb;
-    p.max_splits = (nb_max + sb - 1) / sb;
-    p.nb_cap = p.max_splits * sb;
-    p.slots = (int64_t)B * g.Hkv * p.max_splits;
+    p.rows_per_group = 16 * p.nrt;
+    p.row_groups = (p.NR + p.rows_per_group - 1) / p.rows_per_group;
   } else {
-    // VALU: the blocks of all sequences in flat order, split evenly over a
-    // grid of waves per KV head.  Automatic: the GPU's resident wave
-    // capacity (every SIMD gets the same load, one round); with
-    // split_blocks set: enough waves for that many blocks each when every
-    // sequence is max_seq_len long.  Never more than 64 blocks per wave (one
-    // VGPR of block-table entries).
-    const int64_t tmax = (int64_t)B * nb_max;
-    int64_t waves;
-    if (split_blocks > 0) {
-      const int64_t pw = std::min(split_blocks, 64);
-      waves = (tmax + pw - 1) / pw;
-    } else {
-      const int64_t cus = g.num_cus > 0 ? g.num_cus : 256;
-      waves = std::max<int64_t>(1, cus * valu_waves_per_cu(g, p.NR) / g.Hkv);
-    }
-    waves = std::max<int64_t>(waves, (tmax + 63) / 64);
-    p.split_blocks = (int32_t)std::min<int64_t>(64, (tmax + waves - 1) / waves);
-    p.max_splits = 0;
-    p.nb_cap = nb_max;
-    p.waves = (int32_t)waves;
-    p.slots = (int64_t)g.Hkv * (p.waves + B);
+    p.nrt = 0;
+    p.rows_per_group = p.NR;
+    p.row_groups = 1;
   }
-  p.ws_bytes = ws_layout(p.slots, p.NR, g.D).total;
+  // Both kernels: per (KV head, row group) the blocks of all sequences in
+  // flat order, split evenly over a grid of waves.  Automatic: the GPU's
+  // resident wave capacity for the kernel instantiation (every SIMD gets the
+  // same load, one round); with split_blocks set: enough waves for that many
+  // blocks each when every sequence is max_seq_len long.  Never more than 64
+  // blocks per wave (one VGPR of block-table entries).
+  int64_t waves;
+  if (split_blocks > 0) {
+    const int64_t pw = std::min(split_blocks, 64);
+    waves = (tmax + pw - 1) / pw;
+  } else {
+    const int64_t per_cu = p.use_mfma ? mfma_waves_per_cu(g, p.nrt) : valu_waves_per_cu(g, p.NR);
+    waves = std::max<int64_t>(1, cus * per_cu / ((int64_t)g.Hkv * p.row_groups));
+  }
+  waves = std::max<int64_t>(waves, (tmax + 63) / 64);
+  p.split_blocks = split_blocks > 0 ? std::min(split_blocks, 64) : 0;
+  p.nb_cap = nb_max;
+  p.waves = (int32_t)waves;
+  p.slots = (int64_t)g.Hkv * p.row_groups * (p.waves + B);
+  p.ws_bytes = ws_layout(p.slots, p.rows_per_group, g.D).total;
   *plan = p;
   return 0;
 }
@@ -541,15 +528,9 @@ int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq,
 hipError_t launch_attn_merge(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
                              hipStream_t st) {
   if (a.B == 0) return hipSuccess;
-  if (p.use_mfma && p.max_splits <= 1) return hipSuccess;
   const AttnArgs args = make_attn_args(g, layer, a, p);
   const dim3 grid((unsigned)p.NR, (unsigned)g.Hkv, (unsigned)a.B);
-  KRILL_DISPATCH_D(g.D, {
-    if (p.use_mfma)
-      k_attn_merge_split<D><<<grid, dim3(64), 0, st>>>(args);
-    else
-      k_attn_merge_flat<D><<<grid, dim3(64), 0, st>>>(args);
-  });
+  KRILL_DISPATCH_D(g.D, { k_attn_merge_flat<D><<<grid, dim3(64), 0, st>>>(args); });
   return hipGetLastError();
 }
 

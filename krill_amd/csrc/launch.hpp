@@ -38,15 +38,15 @@ struct AttnLaunch {
 
 // Splits/rows plan shared by the workspace query and the launch.
 struct AttnPlan {
-  int32_t NR;           // query rows per KV head = (Hq/Hkv) * Lq
-  int32_t use_mfma;     // 1 when the MFMA kernel runs
-  int32_t split_blocks; // blocks per split (MFMA) / per wave (VALU)
-  int32_t max_splits;   // MFMA: splits per sequence
-  int32_t waves;        // VALU: waves per KV head
-  int32_t nb_cap;       // blocks per sequence covered (from max_seq_len)
-  int64_t slots;        // partial results the workspace holds
-  int32_t row_groups;   // MFMA: row groups of nrt 16-row tiles
-  int32_t nrt;          // MFMA: 16-row tiles per wave (register budget bound)
+  int32_t NR;             // query rows per KV head = (Hq/Hkv) * Lq
+  int32_t use_mfma;       // 1 when the MFMA kernel runs
+  int32_t split_blocks;   // option value: blocks per wave (<= 64), 0 automatic
+  int32_t waves;          // waves per (KV head, row group)
+  int32_t nb_cap;         // blocks per sequence covered (from max_seq_len)
+  int64_t slots;          // partial results the workspace holds
+  int32_t row_groups;     // row groups per KV head (1 on the VALU path)
+  int32_t rows_per_group; // query rows per wave: NR (VALU), 16 * nrt (MFMA)
+  int32_t nrt;            // MFMA: 16-row tiles per wave (register budget bound)
   size_t ws_bytes;
 };
 
@@ -74,6 +74,9 @@ hipError_t launch_attention(const PoolGeometry &g, int32_t layer, const AttnLaun
 // mode), from the runtime's occupancy query on a device pool, else the
 // register-budget design point.
 int32_t valu_waves_per_cu(const PoolGeometry &g, int32_t NR);
+// Resident waves per compute unit of the MFMA kernel for (D, nrt, mode)
+// (bound by its LDS ring), from the occupancy query on a device pool.
+int32_t mfma_waves_per_cu(const PoolGeometry &g, int32_t nrt);
 
 // Per-configuration kernels, defined in the attention translation units.
 hipError_t launch_attn_valu(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
