@@ -594,7 +594,7 @@ def run_verify(args, w):
     }
     roofline = {
         "bound": "hbm",
-        "kernel": "verify attention call (k_attn_mfma + k_attn_merge_split), one layer",
+        "kernel": "verify attention call (k_attn_mfma + k_attn_merge_flat), one layer",
         "achieved": round(kv_launch / (attn_ms * 1e-3) / 1e9, 2),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",

@@ -14,21 +14,24 @@
 // its rows can see.
 //
 // Memory: every block's head region (K, V and metadata, a whole number of
-// contiguous 1 KB runs in the pool layout) is copied verbatim into a
-// two-stage LDS ring with direct-to-LDS buffer loads (16 bytes per lane, no
-// registers involved), the next block in flight while the current one is
-// computed; MFMA operands are then read from LDS.
+// contiguous 1 KB runs in the pool layout) is copied verbatim into an LDS
+// ring with direct-to-LDS buffer loads (16 bytes per lane, no registers
+// involved), the next blocks in flight while the current one is computed;
+// MFMA operands are then read from LDS.
 //
 // Math: transposed scores, so no operand is ever transposed in registers:
 //   S^T[tok][row] = K[tok][d] . Q^T[d][row]      v_mfma_f32_16x16x32_f16
 //   O^T[d][row]  += V^T[d][tok] . P^T[tok][row]  v_mfma_f32_16x16x32_f16
 // The 16-byte K chunks hold the 8 d of an A operand contiguously; V is stored
 // per d in exactly the token order in which the S^T accumulator hands P to
-// the P.V B operand.  Bytes become exact fp16 with v_perm_b32 + one packed
-// subtract; affine scale/bias are applied to the fp32 scores (per group) and
-// folded into the fp16 weights P*s_v, which are split hi + lo so the weight
-// rounding stays below 2^-22 relative.
+// the P.V B operand.  Bytes become fp16 with one v_perm_b32 per pair (1024 + u,
+// the offset folded into the affine zero point for K, subtracted for V);
+// affine scale/bias are applied to the fp32 scores (per group) and folded
+// into the fp16 weights P*s_v.  The softmax max is raised lazily, so the
+// weights stay below 2^8 and most blocks skip the accumulator rescale.
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "attn_common.hpp"
 
@@ -50,6 +53,9 @@ __device__ __forceinline__ half8_t bytes8_exact(uint2 w) {
 // LDS bytes of one staged block: the head region rounded up to whole 1 KB
 // runs (one 16-byte-per-lane direct load each).
 __host__ __device__ constexpr int mfma_stage_bytes(int D, int G) { return (head_region_bytes(D, G) + 1023) & ~1023; }
+// Ring depth: two stages (measured: a third stage per wave costs a wave per
+// compute unit, which costs more than the deeper prefetch gains).
+__host__ __device__ constexpr int mfma_stages(int D) { return 2; }
 
 template <int D, int MODE, int NRT>
 __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
@@ -59,8 +65,10 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
   constexpr int RR = 16 * NRT; // query rows of this wave
   constexpr int STAGE = mfma_stage_bytes(D, G);
   constexpr int NCH = STAGE / 1024;  // direct loads per block
-  static_assert(NCH <= 62, "vmcnt immediate range");
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[2 * STAGE];
+  constexpr int NST = mfma_stages(D);
+  constexpr int NK = 64 * D / 1024;  // runs holding the K bytes
+  static_assert((NST - 1) * NCH <= 63, "vmcnt immediate range");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NST * STAGE];
 
   const int lane = threadIdx.x;
   const int n = lane & 15, q4 = lane >> 4;
@@ -121,17 +129,22 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
     }
     if (ss < iend) iend_eff = ss;
   }
-  // Copies flat block i into stage `buf` (after the wave's last block the
-  // resource is empty: the loads return zeros without a memory access).
-  auto issue = [&](int i, int buf) {
+  // Copies 1 KB runs [C0, C1) of flat block i into stage `buf` (after the
+  // wave's last block the resource is empty: the loads return zeros without
+  // a memory access).  Runs [0, NK) are the K bytes, the rest V and metadata.
+  auto issue = [&](int i, int buf, auto c0_, auto c1_) {
+    constexpr int C0 = decltype(c0_)::value, C1 = decltype(c1_)::value;
     const bool ok = i < iend_eff;
     const int phys = __builtin_amdgcn_readlane(tab, ok ? i - i0 : 0);
     const __amdgpu_buffer_rsrc_t r = block_rsrc(head_region(a.lv, phys, hk), ok ? a.lv.head_bytes : 0);
     uint8_t *dst = ring + buf * STAGE;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
+    for (int c = C0; c < C1; ++c)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(dst + c * 1024), 16, c * 1024 + lane * 16, 0, 0, 2);
   };
+  using KRuns0 = std::integral_constant<int, 0>;
+  using KRuns1 = std::integral_constant<int, NK>;
+  using AllRuns = std::integral_constant<int, NCH>;
 
   // ---- Q^T operands of sequence bq: lane holds q[row n][32 ks + 8 q4 .. +8]
   half8_t qB[NRT][KS];
@@ -184,11 +197,11 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
     }
   };
 
-  // queries first, then the first two blocks: waits on the queries do not
+  // queries first, then the first NST blocks: waits on the queries do not
   // cover the block copies
   load_q(b);
-  issue(i0, 0);
-  issue(i0 + 1, 1);
+#pragma unroll
+  for (int k = 0; k < NST; ++k) issue(i0 + k, k, KRuns0{}, AllRuns{});
   finish_q();
 
   const half2_t m1024 = half2_t{(_Float16)-1024.0f, (_Float16)-1024.0f};
@@ -203,6 +216,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
       const int r = rbase + 16 * rt + n;
       lim[rt] = rvalid[rt] ? len - a.Lq + r / a.R + 1 : 0;
     }
+    const int lim_lo = len - a.Lq + rbase / a.R + 1;  // keys seen by the group's first row
     float m_run[NRT], l_part[NRT], c_part[NRT][G];
     float4_t oacc[NRT][NDT];
 #pragma unroll
@@ -216,14 +230,20 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
     }
 
     for (; i < seg_end; ++i) {
-      const int buf = (i - i0) & 1;
-      // stage `buf` holds block i once every load but the NCH youngest (the
-      // other stage's copy) has completed
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NCH) : "memory");
+      const int buf = (i - i0) % NST;
+      // stage `buf` holds block i once every load but the (NST - 1) * NCH
+      // youngest (the other stages' copies, issued in the same K-then-rest
+      // order) has completed
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NST - 1) * NCH) : "memory");
       const uint8_t *st = ring + buf * STAGE;
       const int tbase = (i - s) << 6;
+      // some row of this group does not see every token of the block (causal
+      // edge or the sequence's last block): only then are scores masked
+      const bool edge = tbase + 64 > lim_lo;
 
-      // ---- S^T = K . Q^T, four 16-token tiles
+      // ---- S^T = K . Q^T, four 16-token tiles.  Affine mode feeds the bytes
+      // as exact fp16 1024 + u and folds the offset into the zero point:
+      // q.k = s * (q.(1024 + u)) + (z - 1024 s) * sum q (per 64-d group).
       float sc[4][NRT][4];
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
@@ -252,7 +272,9 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
             half2_t p3 = (bytes23_plus1024(kb.y) + m1024) * ks2 + kz2;
             A = half8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
           } else {
-            A = bytes8_exact(kb);
+            const half2_t p0 = bytes01_plus1024(kb.x), p1 = bytes23_plus1024(kb.x);
+            const half2_t p2 = bytes01_plus1024(kb.y), p3 = bytes23_plus1024(kb.y);
+            A = half8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
           }
           const int g = MODE == MODE_AFFINE ? ks / 2 : 0;
 #pragma unroll
@@ -260,7 +282,6 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
         }
         // lane holds tokens 16*tt + 4*q4 + e for row n
         const int tok0 = 16 * tt + 4 * q4;
-        float kss[4][G], kzz[4][G];
         if constexpr (MODE == MODE_AFFINE) {
           // (scale, zero) pairs of tokens tok0 .. tok0+3, G per token: 16 G contiguous bytes
           uint32_t km[4 * G];
@@ -273,44 +294,74 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
             km[4 * c + 3] = w.w;
           }
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
+          for (int e = 0; e < 4; ++e) {
+            float kss[G], kzz[G];
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-              kss[e][g] = f16_bits_to_f32((uint16_t)(km[e * G + g] & 0xffffu));
-              kzz[e][g] = f16_bits_to_f32((uint16_t)(km[e * G + g] >> 16));
+              kss[g] = f16_bits_to_f32((uint16_t)(km[e * G + g] & 0xffffu));
+              kzz[g] = fmaf(-1024.0f, kss[g], f16_bits_to_f32((uint16_t)(km[e * G + g] >> 16)));
             }
-        }
 #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt)
+            for (int rt = 0; rt < NRT; ++rt) {
+              float sv = 0.0f;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float sv;
-            if constexpr (MODE == MODE_AFFINE) {
-              sv = 0.0f;
-#pragma unroll
-              for (int g = 0; g < G; ++g) sv += kss[e][g] * sacc[rt][g][e] + kzz[e][g] * qsum[rt][g];
-            } else {
-              sv = sacc[rt][0][e];
+              for (int g = 0; g < G; ++g) sv = fmaf(kss[g], sacc[rt][g][e], fmaf(kzz[g], qsum[rt][g], sv));
+              sc[tt][rt][e] = sv * a.scale_log2;
             }
-            sc[tt][rt][e] = (tbase + tok0 + e < lim[rt]) ? sv * a.scale_log2 : -INFINITY;
           }
-      }
-
-      // ---- online softmax (row n of each tile; its 64 scores live in the
-      // four lanes n, n+16, n+32, n+48)
+        } else {
 #pragma unroll
-      for (int rt = 0; rt < NRT; ++rt) {
-        float mb = -INFINITY;
+          for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sc[tt][rt][e] = sacc[rt][0][e] * a.scale_log2;
+        }
+      }
+      // the K bytes of this stage are consumed: refill them NST blocks ahead
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue(i + NST, buf, KRuns0{}, KRuns1{});
+      if (edge) {
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) mb = fmaxf(mb, sc[tt][rt][e]);
-        mb = fmaxf(mb, shfl_xor(mb, 16));
-        mb = fmaxf(mb, shfl_xor(mb, 32));
-        const float mn = fmaxf(m_run[rt], mb);
-        const float mu = mn == -INFINITY ? 0.0f : mn;
-        const float al = fast_exp2(m_run[rt] - mu);
-        m_run[rt] = mn;
+          for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (tbase + 16 * tt + 4 * q4 + e >= lim[rt]) sc[tt][rt][e] = -INFINITY;
+      }
+
+      // ---- online softmax with a lazily raised running max (row n of each
+      // tile; its 64 scores live in the four lanes n, n+16, n+32, n+48): the
+      // max only moves when some score exceeds it by more than 2^8, so the
+      // weights stay below 2^8 and most blocks skip the rescale
+      float mb[NRT];
+      bool over = false;
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt) {
+        float v = -INFINITY;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+          v = fmaxf(v, fmaxf(fmaxf(sc[tt][rt][0], sc[tt][rt][1]), fmaxf(sc[tt][rt][2], sc[tt][rt][3])));
+        v = fmaxf(v, shfl_xor(v, 16));
+        v = fmaxf(v, shfl_xor(v, 32));
+        mb[rt] = v;
+        over |= v > m_run[rt] + 8.0f;
+      }
+      if (__any(over)) {
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+          const float mn = fmaxf(m_run[rt], mb[rt]);
+          const float al = m_run[rt] == -INFINITY ? 0.0f : fast_exp2(m_run[rt] - mn);
+          m_run[rt] = mn;
+          l_part[rt] *= al;
+#pragma unroll
+          for (int g = 0; g < G; ++g) c_part[rt][g] *= al;
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) oacc[rt][dt] *= al;
+        }
+      }
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt) {
+        const float mu = m_run[rt] == -INFINITY ? 0.0f : m_run[rt];
         float ps = 0.0f;
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt)
@@ -319,14 +370,12 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
             sc[tt][rt][e] = fast_exp2(sc[tt][rt][e] - mu);
             ps += sc[tt][rt][e];
           }
-        l_part[rt] = l_part[rt] * al + ps;
-#pragma unroll
-        for (int g = 0; g < G; ++g) c_part[rt][g] *= al;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) oacc[rt][dt] *= al;
+        l_part[rt] += ps;
       }
 
-      // ---- O^T += V^T . P^T over two 32-token groups
+      // ---- O^T += V^T . P^T over two 32-token groups; weights p * s_v in
+      // fp16 (below 2^8 * s_v), V bytes as exact fp16 u, the zero points summed
+      // on the side
 #pragma unroll
       for (int tg = 0; tg < 2; ++tg) {
         // logical k = 8*q4 + i  <->  token 32*tg + (i < 4 ? 4*q4 + i : 16 + 4*q4 + i - 4)
@@ -343,18 +392,22 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
             vm[4 * c + 2] = w.z;
             vm[4 * c + 3] = w.w;
           }
+          if (edge) {  // metadata past the sequence's end is not data
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const bool valid = tbase + tokh + e < len;
+            for (int e = 0; e < 4; ++e)
+              if (tbase + tokh + e >= len)
+#pragma unroll
+                for (int g = 0; g < G; ++g) vm[e * G + g] = 0u;
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-              const uint32_t w = valid ? vm[e * G + g] : 0u;
-              vss[4 * h + e][g] = f16_bits_to_f32((uint16_t)(w & 0xffffu));
-              vzz[4 * h + e][g] = f16_bits_to_f32((uint16_t)(w >> 16));
+              vss[4 * h + e][g] = f16_bits_to_f32((uint16_t)(vm[e * G + g] & 0xffffu));
+              vzz[4 * h + e][g] = f16_bits_to_f32((uint16_t)(vm[e * G + g] >> 16));
             }
-          }
         }
-        half8_t Bhi[NRT][G], Blo[NRT][G];
+        half8_t Bw[NRT][G];
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
 #pragma unroll
@@ -362,12 +415,8 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
             const float p = sc[2 * tg + (k >> 2)][rt][k & 3];
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-              const float w = MODE == MODE_AFFINE ? p * vss[k][g] : p;
-              const _Float16 hi = (_Float16)w;
-              const _Float16 lo = (_Float16)(w - (float)hi);
-              Bhi[rt][g][k] = hi;
-              Blo[rt][g][k] = lo;
-              if constexpr (MODE == MODE_AFFINE) c_part[rt][g] += p * vzz[k][g];
+              Bw[rt][g][k] = (_Float16)(MODE == MODE_AFFINE ? p * vss[k][g] : p);
+              if constexpr (MODE == MODE_AFFINE) c_part[rt][g] = fmaf(p, vzz[k][g], c_part[rt][g]);
             }
           }
         }
@@ -395,15 +444,12 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
           }
           const int g = MODE == MODE_AFFINE ? dt / 4 : 0;
 #pragma unroll
-          for (int rt = 0; rt < NRT; ++rt) {
-            oacc[rt][dt] = mfma16x16x32(A, Bhi[rt][g], oacc[rt][dt]);
-            oacc[rt][dt] = mfma16x16x32(A, Blo[rt][g], oacc[rt][dt]);
-          }
+          for (int rt = 0; rt < NRT; ++rt) oacc[rt][dt] = mfma16x16x32(A, Bw[rt][g], oacc[rt][dt]);
         }
       }
-      // every LDS read of this stage has returned: refill it two blocks ahead
+      // every LDS read of this stage has returned: refill the rest
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      issue(i + 2, buf);
+      issue(i + NST, buf, KRuns1{}, AllRuns{});
     }
 
     // ---- end of the segment: lane holds O^T[d = 16*dt + 4*q4 + e][row n].
@@ -509,7 +555,7 @@ static int32_t occupancy_mfma(int nrt) {
                                 &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, 1>), 64, 0);
   if (e != hipSuccess || n <= 0) {
     (void)hipGetLastError();
-    n = (160 * 1024) / (2 * mfma_stage_bytes(D, MODE == MODE_AFFINE ? D / 64 : 1));
+    n = (160 * 1024) / (mfma_stages(D) * mfma_stage_bytes(D, MODE == MODE_AFFINE ? D / 64 : 1));
   }
   return n;
 }
@@ -517,8 +563,8 @@ static int32_t occupancy_mfma(int nrt) {
 int32_t mfma_waves_per_cu(const PoolGeometry &g, int32_t nrt) {
   const int dsel = g.D == 64 ? 0 : g.D == 128 ? 1 : 2;
   if (nrt < 1 || nrt > 2) return 4;
-  if (g.num_cus <= 0) {  // host-only pool: the LDS bound (two stages per wave, 160 KB per CU)
-    static const int est[3] = {8, 4, 2};
+  if (g.num_cus <= 0) {  // host-only pool: the LDS bound (the ring per wave, 160 KB per CU)
+    static const int est[3] = {5, 3, 2};
     return est[dsel];
   }
   static int cache[2][3][3] = {};  // [mode][D][nrt], filled on first use per process
