@@ -259,6 +259,47 @@ __device__ __forceinline__ void settle(uint32_t &x) { asm volatile("; settle %0"
 //   s = max((max-min)/255, 1e-7) signed toward the larger-magnitude edge,
 //   q0 = rint(edge/s), s = edge/q0 and bias = edge when q0 != 0 (else bias 0),
 //   q = clip(rint((w - bias)/s), 0, 255); (scale, zero) = (s, bias).
+// Scalar steps of the two quantizers, shared by the wave-collective and the
+// lane-local forms so both produce the same bytes.
+template <int DT>
+__device__ __forceinline__ float ref_safe_scale(float mn, float mx) {
+  const float sc = round_dt<DT>(mx - mn) / 255.0f;
+  return sc > 1e-8f ? sc : 1e-8f;
+}
+template <int DT>
+__device__ __forceinline__ uint8_t ref_q(float x, float mn, float safe) {
+  float n = round_dt<DT>(x - mn) / safe;
+  if (n < 0.0f) n = 0.0f;
+  if (n > 255.0f) n = 255.0f;
+  return (uint8_t)(uint32_t)n;
+}
+// affine input: the element rounded to fp16 (bf16 inputs are cast first)
+template <int DT>
+__device__ __forceinline__ float affine_w(float x) {
+  return DT == DT_F16 ? x : f16_bits_to_f32(f32_to_f16_bits(x));
+}
+__device__ __forceinline__ void affine_params(float wmin, float wmax, float &s_out, float &bias_out) {
+  const bool side = fabsf(wmin) > fabsf(wmax);
+  float s = (wmax - wmin) / 255.0f;
+  if (!(s > 1e-7f)) s = 1e-7f;
+  s = side ? s : -s;
+  const float edge = side ? wmin : wmax;
+  const float q0 = rintf(edge / s);
+  float bias = 0.0f;
+  if (q0 != 0.0f) {
+    s = edge / q0;
+    bias = edge;
+  }
+  s_out = s;
+  bias_out = bias;
+}
+__device__ __forceinline__ uint8_t affine_q(float w, float s, float bias) {
+  float n = rintf((w - bias) / s);
+  if (n > 255.0f) n = 255.0f;
+  if (n < 0.0f) n = 0.0f;
+  return (uint8_t)(uint32_t)n;
+}
+
 template <int D, int MODE, int DT>
 __device__ __forceinline__ void quantize_row(const float (&x)[D / 64], uint8_t (&qb)[D / 64], float &scale,
                                              float &zero) {
@@ -272,22 +313,16 @@ __device__ __forceinline__ void quantize_row(const float (&x)[D / 64], uint8_t (
     }
     mn = wave_min_range<1, 32>(mn);
     mx = wave_max_range<1, 32>(mx);
-    const float sc = round_dt<DT>(mx - mn) / 255.0f;
-    const float safe = sc > 1e-8f ? sc : 1e-8f;
+    const float safe = ref_safe_scale<DT>(mn, mx);
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      float n = round_dt<DT>(x[e] - mn) / safe;
-      if (n < 0.0f) n = 0.0f;
-      if (n > 255.0f) n = 255.0f;
-      qb[e] = (uint8_t)(uint32_t)n;
-    }
+    for (int e = 0; e < E; ++e) qb[e] = ref_q<DT>(x[e], mn, safe);
     scale = safe;
     zero = mn;
   } else {
     constexpr int LPG = 64 / E;  // lanes per group of 64
     float w[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) w[e] = DT == DT_F16 ? x[e] : f16_bits_to_f32(f32_to_f16_bits(x[e]));
+    for (int e = 0; e < E; ++e) w[e] = affine_w<DT>(x[e]);
     float wmin = w[0], wmax = w[0];
 #pragma unroll
     for (int e = 1; e < E; ++e) {
@@ -296,26 +331,9 @@ __device__ __forceinline__ void quantize_row(const float (&x)[D / 64], uint8_t (
     }
     wmin = wave_min_range<1, LPG / 2>(wmin);
     wmax = wave_max_range<1, LPG / 2>(wmax);
-    const bool side = fabsf(wmin) > fabsf(wmax);
-    float s = (wmax - wmin) / 255.0f;
-    if (!(s > 1e-7f)) s = 1e-7f;
-    s = side ? s : -s;
-    const float edge = side ? wmin : wmax;
-    const float q0 = rintf(edge / s);
-    float bias = 0.0f;
-    if (q0 != 0.0f) {
-      s = edge / q0;
-      bias = edge;
-    }
+    affine_params(wmin, wmax, scale, zero);
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      float n = rintf((w[e] - bias) / s);
-      if (n > 255.0f) n = 255.0f;
-      if (n < 0.0f) n = 0.0f;
-      qb[e] = (uint8_t)(uint32_t)n;
-    }
-    scale = s;
-    zero = bias;
+    for (int e = 0; e < E; ++e) qb[e] = affine_q(w[e], scale, zero);
   }
 }
 

@@ -58,6 +58,164 @@ __global__ __launch_bounds__(256) void k_quantize_append(LayerView lv, const uin
   store_row<D, MODE>(head_region(lv, blk, h), kv, t, lane, qb, scale, zero);
 }
 
+// Token owning byte `o` of a head region (pool layout in kdev.hpp).
+template <int D, int G>
+__device__ __forceinline__ int region_byte_token(int o) {
+  if (o < 64 * D) return (o >> 4) & 63;  // K: ((d/16)*64 + t)*16 + d%16
+  if (o < 128 * D) {                     // V: tg*32*D + ((2*(d%DPL) + p/16)*64 + d/DPL)*16 + p%16
+    const int ov = o - 64 * D;
+    const int tg = ov / (32 * D);
+    const int piece = (ov % (32 * D)) >> 4;
+    const int p = ((piece >> 6) & 1) * 16 + (o & 15);
+    return 32 * tg + vtok(p);
+  }
+  if (o < 128 * D + 256 * G) return ((o - 128 * D) >> 2) / G;  // K (scale, zero): (t*G + g)*4
+  return ((o - 128 * D - 256 * G) >> 2) / G;                    // V (scale, zero)
+}
+
+// Bulk append (prefill, chunked appends): one workgroup (256 threads) per
+// (sequence, head, 64 consecutive rows).  Each thread quantizes one scale
+// group of one row of K or V on its own (64 elements in affine mode, the
+// whole row in the reference's row mode) with the same scalar steps as
+// quantize_row (ref_safe_scale / ref_q, affine_w / affine_params / affine_q),
+// so the bytes are the same as the per-row kernel's.  When the rows' slots
+// are consecutive positions (the block manager hands them out that way) they
+// fall into at most two blocks: K bytes (16-byte pieces per token) and the
+// (scale, zero) words go straight to the pool, the transposed V rows to an
+// LDS image of those blocks' V regions, whose new bytes are then written out
+// in region order -- whole 16-byte pieces where every byte belongs to a new
+// token, single bytes at the edges of the token range -- instead of one-byte
+// scattered stores.  Other slot patterns (and slots < 0) store each group
+// straight to its block.
+template <int D, int MODE, int DT>
+__global__ __launch_bounds__(256) void k_quantize_append_blocks(LayerView lv, const uint16_t *__restrict__ k,
+                                                                const uint16_t *__restrict__ v, int64_t sb,
+                                                                int64_t sh, int64_t sl,
+                                                                const int32_t *__restrict__ slots, int32_t L) {
+  constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
+  constexpr int GE = D / G;  // elements per scale group
+  constexpr int VB = 64 * D;         // V bytes of a block (region offset v_offset(D))
+  constexpr int ITEMS = 64 * G * 2;  // (row, group, K|V)
+  __shared__ __attribute__((aligned(16))) uint8_t img[2][VB];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int l0 = blockIdx.x * 64;
+  const int nrows = min(64, L - l0);
+  const int32_t *srow = slots + (int64_t)b * L + l0;
+
+  // the chunk's layout, computed by every wave (uniform)
+  const int sv = lane < nrows ? srow[lane] : -1;
+  const int prev = __shfl_up(sv, 1, 64);
+  bool bad = lane < nrows && (sv < 0 || (sv >> 6) >= lv.num_blocks);
+  if (lane > 0 && lane < nrows && !bad && sv != prev + 1) bad = !((prev & 63) == 63 && (sv & 63) == 0);
+  const bool brk = lane > 0 && lane < nrows && (sv >> 6) != (prev >> 6);
+  const unsigned long long brks = __ballot(brk);
+  const bool fast = __ballot(bad) == 0 && __popcll(brks) <= 1;
+  const int slot0 = __builtin_amdgcn_readfirstlane(sv);
+  const int nA = brks ? (int)__builtin_ctzll(brks) : nrows;  // rows in the first block
+  const int blkA = slot0 >> 6, tA = slot0 & 63;
+  const int blkB = brks ? __builtin_amdgcn_readlane(sv, nA) >> 6 : -1;
+
+#pragma unroll 1
+  for (int item = tid; item < ITEMS; item += 256) {
+    const int kv = item / (64 * G), r = (item / G) % 64, g = item % G;
+    const int slot = __shfl(sv, r, 64);
+    if (r >= nrows || slot < 0 || (slot >> 6) >= lv.num_blocks) continue;
+    const int t = slot & 63;
+    const uint16_t *src = (kv ? v : k) + (int64_t)b * sb + (int64_t)h * sh + (int64_t)(l0 + r) * sl + g * GE;
+    uint4 raw[GE / 8];
+#pragma unroll
+    for (int c = 0; c < GE / 8; ++c) raw[c] = *reinterpret_cast<const uint4 *>(src + 8 * c);
+    auto elem = [&](int e) -> float {
+      const uint4 w = raw[e >> 3];
+      const uint32_t u = ((e & 7) >> 1) == 0 ? w.x : ((e & 7) >> 1) == 1 ? w.y : ((e & 7) >> 1) == 2 ? w.z : w.w;
+      return elem_to_f32<DT>((uint16_t)((e & 1) ? (u >> 16) : (u & 0xffffu)));
+    };
+    uint32_t qw[GE / 4];
+    float scale, zero;
+    if constexpr (MODE == MODE_REF) {
+      float mn = elem(0), mx = mn;
+#pragma unroll
+      for (int e = 1; e < GE; ++e) {
+        mn = fminf(mn, elem(e));
+        mx = fmaxf(mx, elem(e));
+      }
+      const float safe = ref_safe_scale<DT>(mn, mx);
+#pragma unroll
+      for (int c = 0; c < GE / 4; ++c) {
+        uint32_t wv = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wv |= (uint32_t)ref_q<DT>(elem(4 * c + e), mn, safe) << (8 * e);
+        qw[c] = wv;
+      }
+      scale = safe;
+      zero = mn;
+    } else {
+      float wmin = affine_w<DT>(elem(0)), wmax = wmin;
+#pragma unroll
+      for (int e = 1; e < GE; ++e) {
+        const float w = affine_w<DT>(elem(e));
+        wmin = fminf(wmin, w);
+        wmax = fmaxf(wmax, w);
+      }
+      affine_params(wmin, wmax, scale, zero);
+#pragma unroll
+      for (int c = 0; c < GE / 4; ++c) {
+        uint32_t wv = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wv |= (uint32_t)affine_q(affine_w<DT>(elem(4 * c + e)), scale, zero) << (8 * e);
+        qw[c] = wv;
+      }
+    }
+    uint8_t *reg = head_region(lv, slot >> 6, h);
+    const int d0 = g * GE;
+    if (kv == 0) {
+#pragma unroll
+      for (int c = 0; c < GE / 16; ++c)
+        *reinterpret_cast<uint4 *>(reg + k_byte(t, d0 + 16 * c)) =
+            uint4{qw[4 * c], qw[4 * c + 1], qw[4 * c + 2], qw[4 * c + 3]};
+    } else {
+      // V: into the LDS image of the block's V region or straight to the block.
+      // Offsets are taken relative to the V region (v_byte - v_offset, in
+      // [0, 64 D)): an LDS pointer moved below its array would wrap in the
+      // 32-bit LDS address space before its conversion to a flat address.
+      uint8_t *vdst = fast ? img[r < nA ? 0 : 1] : reg + v_offset(D);
+#pragma unroll
+      for (int e = 0; e < GE; ++e)
+        vdst[v_byte(D, t, d0 + e) - v_offset(D)] = (uint8_t)(qw[e >> 2] >> (8 * (e & 3)));
+    }
+    const uint32_t meta = (uint32_t)f32_to_f16_bits(scale) | ((uint32_t)f32_to_f16_bits(zero) << 16);
+    *reinterpret_cast<uint32_t *>(reg + (kv ? vm_offset(D, G) : km_offset(D)) + ((t * G + g) << 2)) = meta;
+  }
+  if (!fast) return;  // uniform across the workgroup
+  __syncthreads();
+
+  // V write-out in region order: block A holds tokens [tA, tA + nA), block B [0, nrows - nA)
+#pragma unroll 1
+  for (int ib = 0; ib < (blkB >= 0 ? 2 : 1); ++ib) {
+    const int tlo = ib == 0 ? tA : 0, thi = ib == 0 ? tA + nA : nrows - nA;
+    uint8_t *reg = head_region(lv, ib == 0 ? blkA : blkB, h) + v_offset(D);
+    const uint8_t *im = img[ib];
+#pragma unroll 1
+    for (int q = tid; q < VB / 16; q += 256) {
+      const int o = q * 16;
+      unsigned mask = 0;
+#pragma unroll
+      for (int x = 0; x < 16; ++x) {
+        const int tk = region_byte_token<D, G>(v_offset(D) + o + x);
+        mask |= (unsigned)(tk >= tlo && tk < thi) << x;
+      }
+      if (mask == 0xffffu) {
+        *reinterpret_cast<uint4 *>(reg + o) = *reinterpret_cast<const uint4 *>(im + o);
+      } else if (mask) {
+#pragma unroll
+        for (int x = 0; x < 16; ++x)
+          if (mask & (1u << x)) reg[o + x] = im[o + x];
+      }
+    }
+  }
+}
+
 // Append of each sequence's newest token, its position len - 1 located
 // through the block table (the decode step: lens count the new token).  A
 // token outside the blocks the attention reads (len = 0, or a block beyond
@@ -382,6 +540,25 @@ hipError_t launch_quantize_append(const PoolGeometry &g, int32_t layer, const vo
   if (waves == 0) return hipSuccess;
   const LayerView lv = layer_view(g, layer);
   const uint16_t *kk = static_cast<const uint16_t *>(k), *vv = static_cast<const uint16_t *>(v);
+  if (L >= 32 && B <= 65535 && g.Hkv <= 65535 && !(g.mode == MODE_REF && g.D > 128)) {
+    // chunks of 64 rows staged per block in LDS (the row mode at D = 256 --
+    // a 256-element group per thread -- stays on the per-row kernel)
+    const dim3 grid((unsigned)((L + 63) / 64), (unsigned)g.Hkv, (unsigned)B), block(256);
+    KRILL_DISPATCH_D(g.D, {
+      if (g.mode == MODE_REF) {
+        if (g.in_dtype == DT_BF16)
+          k_quantize_append_blocks<D, MODE_REF, DT_BF16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, L);
+        else
+          k_quantize_append_blocks<D, MODE_REF, DT_F16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, L);
+      } else {
+        if (g.in_dtype == DT_BF16)
+          k_quantize_append_blocks<D, MODE_AFFINE, DT_BF16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, L);
+        else
+          k_quantize_append_blocks<D, MODE_AFFINE, DT_F16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, L);
+      }
+    });
+    return hipGetLastError();
+  }
   const dim3 grid(wave_blocks(waves)), block(256);
   KRILL_DISPATCH_D(g.D, {
     if (g.mode == MODE_REF) {

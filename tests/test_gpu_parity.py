@@ -59,6 +59,22 @@ def test_quantize_append_bit_exact(mode, dt, D):
 
 
 @pytest.mark.parametrize("mode", ["ref_row", "affine_g64"])
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_bulk_append_block_staging_bit_exact(mode, D):
+    # appends of up to 200 rows (the 64-row chunks staged per block in LDS):
+    # sequences starting at block edges and inside blocks, chunks straddling
+    # two blocks, short sequences padded with slot -1 (the per-row path)
+    print(f"\ncase bulk_append mode={mode} D={D}", flush=True)
+    rng = np.random.default_rng(300 + D)
+    pool = make_pool(2, D, mode, "bf16", blocks=64)
+    f = Filled(pool, [1, 63, 64, 65, 127, 300, 517], rng, "bf16", max_chunk=200, outlier_frac=0.02)
+    tables, lens, _ = f.tables()
+    torch.cuda.synchronize()
+    check_snapshot(pool.gather(0, tables, lens, max(f.lens)), f, 0)
+    pool.close()
+
+
+@pytest.mark.parametrize("mode", ["ref_row", "affine_g64"])
 def test_gather_left_padded_matches_reference_stack(mode):
     print(f"\ncase gather_left_pad mode={mode}", flush=True)
     rng = np.random.default_rng(5)
