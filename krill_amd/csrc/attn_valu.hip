@@ -121,13 +121,20 @@ __device__ __forceinline__ void load_new_rows(const AttnArgs &a, int b, int hk, 
   }
 }
 
-// Quantizes rows loaded by load_new_rows and writes them as token t of
-// physical block `phys`: the same quantize_row / store_row as the append
-// kernels, so the bytes are the same.
+// Quantizes rows loaded by load_new_rows with the append kernels'
+// quantize_row, leaving the K row's D bytes and then the V row's in `newrow`
+// (LDS) and the (scale, zero) words of each group in pkm / pvm (uniform).
+// The wave patches the token into its registers when it reaches its block
+// and stores it (store_newest) at the end of the segment, where the
+// segment's output stores go too: a store issued mid-segment would hold up
+// every later wait on the in-order memory counter.
 template <int D, int MODE, int DT>
-__device__ __forceinline__ void write_new_rows(const AttnArgs &a, int hk, int phys, int t,
-                                               const uint16_t (&rk)[D / 64], const uint16_t (&rv)[D / 64]) {
+__device__ __forceinline__ void prepare_newest(const uint16_t (&rk)[D / 64], const uint16_t (&rv)[D / 64],
+                                               uint8_t *newrow, uint32_t (&pkm)[MODE == MODE_AFFINE ? D / 64 : 1],
+                                               uint32_t (&pvm)[MODE == MODE_AFFINE ? D / 64 : 1]) {
   constexpr int E = D / 64;
+  constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
+  constexpr int LPG = MODE == MODE_AFFINE ? 64 / E : 64;  // lanes per scale group
   const int lane = threadIdx.x & 63;
   float xk[E], xv[E];
 #pragma unroll
@@ -139,17 +146,51 @@ __device__ __forceinline__ void write_new_rows(const AttnArgs &a, int hk, int ph
   float ks, kz, vs, vz;
   quantize_row<D, MODE, DT>(xk, qk, ks, kz);
   quantize_row<D, MODE, DT>(xv, qv, vs, vz);
-  uint8_t *reg = head_region(a.lv, phys, hk);
-  store_row<D, MODE>(reg, 0, t, lane, qk, ks, kz);
-  store_row<D, MODE>(reg, 1, t, lane, qv, vs, vz);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    newrow[lane * E + e] = qk[e];
+    newrow[D + lane * E + e] = qv[e];
+  }
+  const uint32_t mk = (uint32_t)f32_to_f16_bits(ks) | ((uint32_t)f32_to_f16_bits(kz) << 16);
+  const uint32_t mv = (uint32_t)f32_to_f16_bits(vs) | ((uint32_t)f32_to_f16_bits(vz) << 16);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    pkm[g] = __builtin_amdgcn_readlane(mk, g * LPG);
+    pvm[g] = __builtin_amdgcn_readlane(mv, g * LPG);
+  }
 }
 
-// Whether the wave reading flat blocks up to iend (exclusive) writes the
-// newest token of a sequence of length len whose nbs read blocks start at
-// flat index ss: it reads the last of them, and that block holds position
-// len - 1 (not so for len = 0, or when the blocks read stop short of it).
-__device__ __forceinline__ bool owns_newest(int len, int nbs, int ss, int iend) {
-  return nbs > 0 && ss + nbs - 1 < iend && ((len - 1) >> 6) == nbs - 1;
+// Stores the token prepared by prepare_newest as token t of physical block
+// phys: the bytes and words store_row writes for the same rows.
+template <int D, int MODE>
+__device__ __forceinline__ void store_newest(const AttnArgs &a, int hk, int phys, int t, const uint8_t *newrow,
+                                             const uint32_t (&pkm)[MODE == MODE_AFFINE ? D / 64 : 1],
+                                             const uint32_t (&pvm)[MODE == MODE_AFFINE ? D / 64 : 1]) {
+  constexpr int E = D / 64;
+  constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
+  const int lane = threadIdx.x & 63;
+  uint8_t *reg = head_region(a.lv, phys, hk);
+  const int d0 = lane * E;
+  uint8_t *kd = reg + k_byte(t, d0);
+  if constexpr (E == 1) {
+    kd[0] = newrow[d0];
+  } else if constexpr (E == 2) {
+    *reinterpret_cast<uint16_t *>(kd) = *reinterpret_cast<const uint16_t *>(newrow + d0);
+  } else {
+    *reinterpret_cast<uint32_t *>(kd) = *reinterpret_cast<const uint32_t *>(newrow + d0);
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) reg[v_byte(D, t, d0 + e)] = newrow[D + d0 + e];
+  uint32_t mk = pkm[0], mv = pvm[0];  // lane g < G stores group g's words
+#pragma unroll
+  for (int g = 1; g < G; ++g) {
+    mk = lane == g ? pkm[g] : mk;
+    mv = lane == g ? pvm[g] : mv;
+  }
+  if (lane < G) {
+    *reinterpret_cast<uint32_t *>(reg + km_offset(D) + ((t * G + lane) << 2)) = mk;
+    *reinterpret_cast<uint32_t *>(reg + vm_offset(D, G) + ((t * G + lane) << 2)) = mv;
+  }
 }
 
 template <int D, int NR, int MODE>
@@ -212,27 +253,18 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   auto seq_len = [&](int bs) -> int { return bs - c0 < 64 ? __builtin_amdgcn_readlane(lenv, bs - c0) : a.lens[bs]; };
 
   // Decode step with the append fused: the wave that reads a sequence's last
-  // block writes the sequence's newest token there (position len - 1) and
-  // waits for the stores before its first pool load, so it reads the token
-  // back like any cached one; no other wave reads that block for this head.
-  // The rows of the first such sequence are loaded here, alongside the block
-  // table; further ones (short sequences) one after another below.
+  // block writes the sequence's newest token there (position len - 1; not
+  // written when that block lies beyond the blocks read).  The token is
+  // quantized and stored while the wave's block loads are in flight, and the
+  // wave patches it into its registers when it reaches that block.  The raw
+  // rows of the first segment's sequence are loaded alongside the block table.
   constexpr int E = D / 64;
-  int own_b = -1, own_ss = 0;
   uint16_t rk[E], rv[E];
+  bool own = false;
   if (a.k_new) {
-    int bs = b, ss = s;
-    while (bs < a.B && ss < iend) {
-      const int len = seq_len(bs), nbs = seq_blocks(a, len);
-      if (owns_newest(len, nbs, ss, iend)) {
-        own_b = bs;
-        own_ss = ss;
-        break;
-      }
-      ss += nbs;
-      ++bs;
-    }
-    if (own_b >= 0) load_new_rows<D>(a, own_b, hk, rk, rv);
+    const int len0 = seq_len(b), nb0 = seq_blocks(a, len0);
+    own = nb0 > 0 && s + nb0 <= iend && ((len0 - 1) >> 6) == nb0 - 1;
+    if (own) load_new_rows<D>(a, b, hk, rk, rv);
   }
 
   // Physical block ids of flat blocks i0 .. iend-1 (at most 64): lane j holds
@@ -256,30 +288,23 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     }
     if (ss < iend) iend_eff = ss;  // the last sequence ends inside this range
   }
-
-  if (own_b >= 0) {
-    const uint64_t ok = __ballot(tab_ok);
-    bool wrote = false;
-    int bs = own_b, ss = own_ss;
-    while (bs < a.B && ss < iend) {
-      const int len = seq_len(bs), nbs = seq_blocks(a, len);
-      if (owns_newest(len, nbs, ss, iend)) {
-        if (bs != own_b) load_new_rows<D>(a, bs, hk, rk, rv);
-        const int f = ss + nbs - 1;  // flat index of the sequence's last block
-        if ((ok >> (f - i0)) & 1) {
-          const int phys = __builtin_amdgcn_readlane(tab, f - i0);
-          if (a.q_dtype == DT_BF16)
-            write_new_rows<D, MODE, DT_BF16>(a, hk, phys, (len - 1) & 63, rk, rv);
-          else
-            write_new_rows<D, MODE, DT_F16>(a, hk, phys, (len - 1) & 63, rk, rv);
-          wrote = true;
-        }
-      }
-      ss += nbs;
-      ++bs;
-    }
-    if (wrote) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  }
+  const uint64_t tab_okm = __ballot(tab_ok);
+  __shared__ __attribute__((aligned(16))) uint8_t newrow[2 * D];
+  int patch_i = -1, patch_t = 0;  // flat block holding the segment's newest token, its position
+  uint32_t pkm[G], pvm[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) pkm[g] = pvm[g] = 0u;
+  // the newest token of sequence bs (its rows loaded), last block at flat f
+  auto prepare = [&](int bs, int f) {
+    const int len2 = seq_len(bs);
+    if (!((tab_okm >> (f - i0)) & 1)) return;
+    if (a.q_dtype == DT_BF16)
+      prepare_newest<D, MODE, DT_BF16>(rk, rv, newrow, pkm, pvm);
+    else
+      prepare_newest<D, MODE, DT_F16>(rk, rv, newrow, pkm, pvm);
+    patch_i = f;
+    patch_t = (len2 - 1) & 63;
+  };
   auto rsrc_of = [&](int i) -> __amdgpu_buffer_rsrc_t {
     const bool ok = i < iend_eff;
     const int phys = __builtin_amdgcn_readlane(tab, ok ? i - i0 : 0);
@@ -363,6 +388,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     load_meta(r0, km, vm);
     load_v(r0);
   }
+  if (own) prepare(b, s + seq_blocks(a, seq_len(b)) - 1);
 #pragma unroll
   for (int p = 0; p < NP; ++p) settle(kr[p]);
 #pragma unroll
@@ -402,6 +428,22 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   for (; i < seg_end; ++i) {
     const int tbase = (i - s) << 6;
     const __amdgpu_buffer_rsrc_t nrs = rsrc_of(i + 1);
+    if (i == patch_i) {
+      // the block holding the segment's newest token: its K row and both
+      // (scale, zero) words go to lane patch_t
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const uint4 x = *reinterpret_cast<const uint4 *>(newrow + 16 * p);
+        if (lane == patch_t) kr[p] = x;
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        if (lane == patch_t) {
+          km[g] = pkm[g];
+          vm[g] = pvm[g];
+        }
+      }
+    }
 
     // ---- scores: this lane's token against every query row; the query
     // pair of each dot comes from lane (pair & 15) of the lane's 16-lane row
@@ -527,6 +569,28 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       sz_lds[64 + pos] = valid ? (uint16_t)(vm[0] >> 16) : (uint16_t)0;
     }
     __syncthreads();
+    if (i == patch_i) {
+      // the newest token's V bytes: position p of group tg, byte p % 16 of the
+      // piece (2 (d % DPL) + p / 16) of every lane's d rows
+      const int tg = patch_t >> 5, p = vpos(patch_t & 31), hi = p >> 4, bp = p & 15;
+      const int sh = 8 * (bp & 3);
+      const uint32_t keep = ~(0xffu << sh);
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        const uint32_t nv = (uint32_t)newrow[D + DPL * lane + e] << sh;
+#pragma unroll
+        for (int tgi = 0; tgi < 2; ++tgi)
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)
+            if (tgi == tg && h2 == hi) {
+              uint4 &x = vr[tgi][2 * e + h2];
+              if ((bp >> 2) == 0) x.x = (x.x & keep) | nv;
+              else if ((bp >> 2) == 1) x.y = (x.y & keep) | nv;
+              else if ((bp >> 2) == 2) x.z = (x.z & keep) | nv;
+              else x.w = (x.w & keep) | nv;
+            }
+      }
+    }
 
     // ---- P.V: lane owns V^T rows d = DPL*lane .. +DPL.  Chunks of 8 tokens
     // (4 pairs): the chunk's V bytes become fp16 pairs once and serve every
@@ -586,6 +650,9 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     __syncthreads();
   }
 
+    // the segment's newest token goes to the pool with the segment's output
+    if (patch_i >= 0) store_newest<D, MODE>(a, hk, __builtin_amdgcn_readlane(tab, patch_i - i0), patch_t, newrow, pkm, pvm);
+
     // ---- end of the segment: the whole sequence in this wave -> output;
     // otherwise a partial in slot hk * (waves + B) + wave + b
     float lsum[NR];
@@ -628,6 +695,14 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     while (b < a.B && seq_blocks(a, seq_len(b)) == 0) ++b;
     if (b >= a.B) break;
     load_q(b);
+    patch_i = -1;
+    if (a.k_new) {
+      const int len2 = seq_len(b), nb2 = seq_blocks(a, len2);
+      if (s + nb2 <= iend && ((len2 - 1) >> 6) == nb2 - 1) {
+        load_new_rows<D>(a, b, hk, rk, rv);
+        prepare(b, s + nb2 - 1);
+      }
+    }
     finish_q();
   }
 }
