@@ -478,7 +478,7 @@ __device__ __forceinline__ void merge_slots(const AttnArgs &a, int64_t slot0, in
     }
     __syncthreads();
   }
-  const float Lsum = wave_allsum(lpart);
+  const float Lsum = uniform_f32(wave_allsum(lpart));  // lane 0's rounding of the sum in every lane
   const float inv = (M == -INFINITY || !(Lsum > 0.0f)) ? 0.0f : 1.0f / Lsum;
 #pragma unroll
   for (int e = 0; e < E; ++e) store_out(a.out, obase + lane + 64 * e, acc[e] * inv, a.out_dtype);
