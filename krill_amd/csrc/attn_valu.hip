@@ -403,6 +403,12 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   finish_q();
 
   int i = i0;
+  // Issue priority falls as the wave works through its range (3 in its
+  // first quarter .. 0 in its last), so a wave that is ahead yields to the
+  // other waves of its SIMD and the SIMD's waves finish together.
+  const int nblk = iend_eff - i0;
+  const int pq1 = i0 + (nblk + 3) / 4, pq2 = i0 + (nblk + 1) / 2, pq3 = i0 + (3 * nblk + 3) / 4;
+  __builtin_amdgcn_s_setprio(3);
   // one pass per sequence segment [max(s, i0), min(s + nb, iend)); the
   // queries of sequence b are ready on entry
   while (true) {
@@ -426,6 +432,9 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     }
 
   for (; i < seg_end; ++i) {
+    if (i == pq1) __builtin_amdgcn_s_setprio(2);
+    if (i == pq2) __builtin_amdgcn_s_setprio(1);
+    if (i == pq3) __builtin_amdgcn_s_setprio(0);
     const int tbase = (i - s) << 6;
     const __amdgpu_buffer_rsrc_t nrs = rsrc_of(i + 1);
     if (i == patch_i) {
