@@ -57,7 +57,7 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="qwen3-14b-b32", choices=sorted(WORKLOADS))
     ap.add_argument("--quant", default="affine_g64", choices=["affine_g64", "ref_row"])
     ap.add_argument("--split-blocks", type=int, default=0)
