@@ -190,12 +190,29 @@ def make_quantized_kv_caches(pool: KVPool, seq: int | None = None):
 class PrefixCache:
     """int8 prefix entries of one pool (PrefixCache.swift int8 API).
 
-    Entries are frozen forks of a sequence: storing shares its blocks
-    (refcounted, no copy) and a hit forks a new sequence from the entry."""
+    Memory tier: the library's entries, frozen forks of a sequence: storing
+    shares its blocks (refcounted, no copy) and a hit forks a new sequence
+    from the entry.  Disk tier (``cache_dir`` set): every stored entry is also
+    written as ``<key>.q8.safetensors`` (krill_amd.q8file), and a lookup that
+    misses in memory at a length tries the file of that length before the
+    next shorter one (PrefixCache.swift:273-308); a file hit is restored into
+    fresh blocks and becomes a memory entry again.  The reference always has
+    a disk tier (default ~/.krill/cache); here it is off unless a directory
+    is given.  A restored entry keeps its tokens (the lookup knows them), so
+    unlike the reference's disk-hydrated entries it can also serve
+    longest-prefix hits."""
 
-    def __init__(self, pool: KVPool, model_id: str = ""):
+    def __init__(self, pool: KVPool, model_id: str = "", cache_dir=None, disk_budget_gb=None,
+                 max_entry_gb=None, min_prefix_len: int = 8):
+        from .q8file import DiskTier, _env_gb
+
         self.pool = pool
         self.model_id = model_id
+        self.min_prefix_len = min_prefix_len  # the pool's min_prefix_len (PrefixCache minPrefixLength)
+        self.disk = DiskTier(cache_dir, disk_budget_gb) if cache_dir is not None else None
+        gb = max_entry_gb if max_entry_gb is not None else _env_gb("KRILL_PREFIX_CACHE_MAX_ENTRY_GB")
+        gb = 4.0 if gb is None else gb
+        self.max_entry_bytes = -1 if gb <= 0 else int(gb * 1_000_000_000)
 
     @staticmethod
     def common_prefix_length(a, b) -> int:
@@ -206,12 +223,44 @@ class PrefixCache:
             i += 1
         return i
 
+    def _key(self, tokens, media_hash) -> int:
+        from .pool import prefix_key
+
+        return prefix_key(self.model_id, media_hash, 2, tokens)  # KVDtype.int8 = 2
+
+    def _entry_bytes(self, n: int) -> int:
+        p = self.pool
+        return p.num_layers * p.num_kv_heads * n * (2 * p.head_dim + 8 * p.groups)
+
     def store_quantized(self, tokens, seq: int, media_hash=None) -> bool:
-        return self.pool.prefix_store(seq, tokens, self.model_id, media_hash)
+        """storeQuantized (PrefixCache.swift:369-400): memory entry, then the file."""
+        if len(tokens) < self.min_prefix_len:
+            return False
+        if 0 < self.max_entry_bytes < self._entry_bytes(len(tokens)):
+            return False
+        stored = self.pool.prefix_store(seq, tokens, self.model_id, media_hash)
+        if stored and self.disk is not None and self.disk.enabled:
+            self.disk.write(self._key(tokens, media_hash), self._layers_of(seq, len(tokens)))
+        return stored
 
     def lookup_quantized(self, tokens, media_hash=None):
         """(prefix_len, entry_seq) of an exact entry, or (0, None)."""
-        return self.pool.prefix_lookup(tokens, self.model_id, media_hash)
+        if self.disk is None or not self.disk.enabled:
+            return self.pool.prefix_lookup(tokens, self.model_id, media_hash)
+        n_max = len(tokens)
+        step = max(1, self.min_prefix_len // 2)
+        n = n_max
+        while n >= self.min_prefix_len:
+            got, entry = self.pool.prefix_lookup(tokens[:n], self.model_id, media_hash)
+            if got == n:
+                return got, entry
+            layers = self.disk.load(self._key(tokens[:n], media_hash))
+            if layers is not None and self._restore(tokens[:n], layers, media_hash):
+                got, entry = self.pool.prefix_lookup(tokens[:n], self.model_id, media_hash)
+                if got == n:
+                    return got, entry
+            n -= step
+        return 0, None
 
     def lookup_longest_prefix_quantized(self, tokens, media_hash=None):
         return self.pool.prefix_lookup_longest(tokens, self.model_id, media_hash)
@@ -220,5 +269,49 @@ class PrefixCache:
     def memory_count(self) -> int:
         return self.pool.prefix_count()
 
+    @property
+    def disk_count(self) -> int:
+        return self.disk.count if self.disk is not None else 0
+
     def clear(self):
         self.pool.prefix_clear()
+        if self.disk is not None:
+            self.disk.clear()
+
+    # ------------------------------------------------------------ files
+    def _layers_of(self, seq: int, n: int) -> list:
+        """The first n tokens of seq, every layer, as host snapshot arrays."""
+        s = SequenceKV(self.pool, seq)
+        tables, lens = s.tables()
+        lens.fill_(n)
+        out = []
+        for layer in range(self.pool.num_layers):
+            snap = self.pool.gather(layer, tables, lens, n)
+            out.append({k: v.cpu().numpy() for k, v in snap.items()})
+        return out
+
+    def _restore(self, tokens, layers, media_hash) -> bool:
+        """A file's layers into fresh blocks, stored as a memory entry."""
+        torch = _torch()
+        p = self.pool
+        n = len(tokens)
+        want = {"keys": (1, p.num_kv_heads, n, p.head_dim), "key_scales": (1, p.num_kv_heads, n, p.groups)}
+        if len(layers) != p.num_layers:
+            return False
+        for snap in layers:
+            for f, shape in (("keys", want["keys"]), ("values", want["keys"]), ("key_scales", want["key_scales"]),
+                             ("key_zeros", want["key_scales"]), ("value_scales", want["key_scales"]),
+                             ("value_zeros", want["key_scales"])):
+                if tuple(snap[f].shape) != shape:
+                    return False
+        seq = p.seq_create()
+        try:
+            slots = p.reserve_append(seq, n)
+            sm = torch.as_tensor(slots.reshape(1, n), device="cuda")
+            zero = torch.zeros(1, dtype=torch.int32, device="cuda")
+            for layer, snap in enumerate(layers):
+                d = {k: torch.from_numpy(np.ascontiguousarray(v)).to("cuda") for k, v in snap.items()}
+                p.scatter(layer, d, zero, sm)
+            return p.prefix_store(seq, tokens, self.model_id, media_hash)
+        finally:
+            p.seq_free(seq)
