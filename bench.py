@@ -61,6 +61,8 @@ def parse():
     ap.add_argument("--workload", default="qwen3-14b-b32", choices=sorted(WORKLOADS))
     ap.add_argument("--quant", default="affine_g64", choices=["affine_g64", "ref_row"])
     ap.add_argument("--split-blocks", type=int, default=0)
+    ap.add_argument("--rope-fill", action="store_true",
+                    help="prefill K with RoPE fused into the append (krill_quantize_append_rope)")
     ap.add_argument("--unfused", action="store_true",
                     help="decode step as two calls per layer (quantize-append, then decode attention) instead of "
                          "the fused krill_decode_append_attention")
@@ -138,6 +140,12 @@ class Env:
             pool_k.append(k.to(t.bfloat16))
             pool_v.append(v.to(t.bfloat16))
         strides = (Hkv * C * D, C * D, D)
+        rope = getattr(self.args, "rope_fill", False)
+        if rope:
+            from krill_amd.pool import rope_table
+
+            cs = t.from_numpy(rope_table(Tmax, D, 1.0e6)).to(self.dev)  # Qwen3 rope_theta
+            pos_d = t.arange(Tmax, dtype=t.int32, device=self.dev).expand(B, Tmax)
         n = 0
         for layer in range(w["layers"]):
             for t0 in range(0, Tmax, C):
@@ -145,8 +153,14 @@ class Env:
                 sm = slots_d[:, t0: t0 + L].contiguous()
                 k, v = pool_k[n % nrand], pool_v[n % nrand]
                 n += 1
-                self.KL.check(self.lib.krill_quantize_append_strided(self.h, layer, k.data_ptr(), v.data_ptr(),
-                                                                     *strides, sm.data_ptr(), B, L, self.sp))
+                if rope:
+                    ps = pos_d[:, t0: t0 + L].contiguous()
+                    self.KL.check(self.lib.krill_quantize_append_rope(
+                        self.h, layer, k.data_ptr(), v.data_ptr(), *strides, sm.data_ptr(), ps.data_ptr(),
+                        cs.data_ptr(), Tmax, B, L, self.sp))
+                else:
+                    self.KL.check(self.lib.krill_quantize_append_strided(self.h, layer, k.data_ptr(), v.data_ptr(),
+                                                                         *strides, sm.data_ptr(), B, L, self.sp))
         t.cuda.synchronize()
 
 

@@ -199,6 +199,22 @@ int32_t krill_quantize_append_strided(krill_pool_t pool, int32_t layer, const vo
                                       const void *dev_v, int64_t stride_b, int64_t stride_h,
                                       int64_t stride_l, const int32_t *dev_slot_mapping, int32_t B,
                                       int32_t L, krill_stream_t stream);
+/* RoPE fused into the append: krill_quantize_append_strided with every K row
+ * rotated first, the applyRoPEPerRow (Attention.swift:13-20) that precedes
+ * update() (Attention.swift:85-86 with the cache update after it): MLX RoPE,
+ * traditional = false, over all D dims (element i < D/2 pairs with i + D/2).
+ * Row (b, l) turns by position dev_positions[b*L + l] with the fp32 table
+ * dev_cos_sin[max_pos][D] (D/2 cosines of the pair angles, then their sines):
+ *   k'[i] = k[i]*c_i - k[i+D/2]*s_i,  k'[i+D/2] = k[i]*s_i + k[i+D/2]*c_i
+ * in fp32, each product and sum rounded once, then rounded to in_dtype -- the
+ * tensor the unrotated call would be handed -- and quantized; V as is.  Rows
+ * whose position lies outside [0, max_pos) are not written, like rows with a
+ * negative slot. */
+int32_t krill_quantize_append_rope(krill_pool_t pool, int32_t layer, const void *dev_k, const void *dev_v,
+                                   int64_t stride_b, int64_t stride_h, int64_t stride_l,
+                                   const int32_t *dev_slot_mapping, const int32_t *dev_positions,
+                                   const float *dev_cos_sin, int32_t max_pos, int32_t B, int32_t L,
+                                   krill_stream_t stream);
 
 /* Paged -> contiguous snapshot.  left_pad = 0: quantizedSnapshot()
  * (QuantizedKVCache.swift:106-115), tokens at [0, len), zeros after;

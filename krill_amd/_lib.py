@@ -143,6 +143,7 @@ SIGNATURES = {
     "krill_prefix_key": [STR, STR, I32, PI64, I64, ctypes.POINTER(U64)],
     "krill_quantize_append": [P, I32, P, P, P, I32, I32, P],
     "krill_quantize_append_strided": [P, I32, P, P, I64, I64, I64, P, I32, I32, P],
+    "krill_quantize_append_rope": [P, I32, P, P, I64, I64, I64, P, P, P, I32, I32, I32, P],
     "krill_gather": [P, I32, P, P, I32, I32, I32, I32, ctypes.POINTER(Snapshot), P],
     "krill_gather_dequant": [P, I32, P, P, I32, I32, I32, I32, P, P, P],
     "krill_scatter": [P, I32, ctypes.POINTER(Snapshot), I32, I32, P, P, I32, P],

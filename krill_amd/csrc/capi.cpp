@@ -365,6 +365,28 @@ int32_t krill_quantize_append_strided(krill_pool_t pool, int32_t layer, const vo
   return KRILL_OK;
 }
 
+int32_t krill_quantize_append_rope(krill_pool_t pool, int32_t layer, const void *dev_k, const void *dev_v,
+                                   int64_t stride_b, int64_t stride_h, int64_t stride_l,
+                                   const int32_t *dev_slot_mapping, const int32_t *dev_positions,
+                                   const float *dev_cos_sin, int32_t max_pos, int32_t B, int32_t L,
+                                   krill_stream_t stream) {
+  krill::clear_error();
+  if (int32_t rc = check_device_pool(pool, layer)) return rc;
+  if (B < 0 || L < 0) return fail(KRILL_E_INVAL, "negative B or L");
+  if (B == 0 || L == 0) return KRILL_OK;
+  if (!dev_k || !dev_v || !dev_slot_mapping || !dev_positions || !dev_cos_sin)
+    return fail(KRILL_E_INVAL, "NULL device pointer");
+  if (stride_b < 0 || stride_h < 0 || stride_l < 0) return fail(KRILL_E_INVAL, "negative stride");
+  if (max_pos < 1) return fail(KRILL_E_INVAL, "max_pos %d: the table needs at least one position", max_pos);
+  DeviceGuard dg(pool->device);
+  hipStream_t st = pick_stream(pool, stream);
+  if (int32_t rc = flush_pending(pool, st)) return rc;
+  hipError_t e = krill::launch_quantize_append(pool->geom, layer, dev_k, dev_v, stride_b, stride_h, stride_l,
+                                               dev_slot_mapping, B, L, st, dev_positions, dev_cos_sin, max_pos);
+  if (e != hipSuccess) return hip_fail(e, "RoPE quantize-append launch");
+  return KRILL_OK;
+}
+
 int32_t krill_quantize_append(krill_pool_t pool, int32_t layer, const void *dev_k, const void *dev_v,
                               const int32_t *dev_slot_mapping, int32_t B, int32_t L, krill_stream_t stream) {
   if (!pool) return fail(KRILL_E_INVAL, "pool is NULL");

@@ -27,13 +27,29 @@ static inline LayerView layer_view(const PoolGeometry &g, int32_t layer) {
 // Fused quantize + paged append (quantize_row / store_row: the reference's
 // row quantizer or the affine group-64 one).  One wave64 per (row, K|V);
 // each lane owns D/64 consecutive elements.
+//
+// RoPE (rope.pos set): K rows are rotated first, as MLX RoPE with
+// traditional = false over all D dims (element i < D/2 pairs with i + D/2),
+// at position pos[b * L + l] from the fp32 table cs[pos][D] (cos of angle i,
+// then sin of angle i):
+//   k'[i] = k[i] c_i - k[i + D/2] s_i,   k'[i + D/2] = k[i] s_i + k[i + D/2] c_i
+// in fp32 (each product and sum rounded once), then rounded to the element
+// dtype -- the bf16/f16 tensor the unfused path would hand to the quantizer.
+// Rows whose position lies outside [0, max_pos) are not written (K nor V),
+// like rows with a negative slot.
 // ---------------------------------------------------------------------------
-template <int D, int MODE, int DT>
+struct RopeArgs {
+  const int32_t *pos;  // [B][L] token positions (null: no rotation)
+  const float *cs;     // [max_pos][D]
+  int32_t max_pos;
+};
+
+template <int D, int MODE, int DT, bool ROPE>
 __global__ __launch_bounds__(256) void k_quantize_append(LayerView lv, const uint16_t *__restrict__ k,
                                                          const uint16_t *__restrict__ v, int64_t sb,
                                                          int64_t sh, int64_t sl,
                                                          const int32_t *__restrict__ slots, int32_t B,
-                                                         int32_t L, int32_t Hkv) {
+                                                         int32_t L, int32_t Hkv, RopeArgs rope) {
   constexpr int E = D / 64;
   const int lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -52,6 +68,22 @@ __global__ __launch_bounds__(256) void k_quantize_append(LayerView lv, const uin
   float x[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) x[e] = elem_to_f32<DT>(src[e]);
+  if constexpr (ROPE) {
+    const int p = rope.pos[(int64_t)b * L + l];
+    if ((unsigned)p >= (unsigned)rope.max_pos) return;  // uniform per wave
+    if (kv == 0) {
+      // lane owns d = lane*E + e; its partner d +- D/2 sits in lane ^ 32
+      const float *c = rope.cs + (int64_t)p * D;
+      const bool hi = lane >= 32;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const int i = (lane & 31) * E + e;
+        const float o = __shfl_xor(x[e], 32, 64);
+        const float cv = c[i], sv = c[D / 2 + i];
+        x[e] = round_dt<DT>(hi ? o * sv + x[e] * cv : x[e] * cv - o * sv);
+      }
+    }
+  }
   uint8_t qb[E];
   float scale, zero;
   quantize_row<D, MODE, DT>(x, qb, scale, zero);
@@ -87,11 +119,12 @@ __device__ __forceinline__ int region_byte_token(int o) {
 // token, single bytes at the edges of the token range -- instead of one-byte
 // scattered stores.  Other slot patterns (and slots < 0) store each group
 // straight to its block.
-template <int D, int MODE, int DT>
+template <int D, int MODE, int DT, bool ROPE>
 __global__ __launch_bounds__(256) void k_quantize_append_blocks(LayerView lv, const uint16_t *__restrict__ k,
                                                                 const uint16_t *__restrict__ v, int64_t sb,
                                                                 int64_t sh, int64_t sl,
-                                                                const int32_t *__restrict__ slots, int32_t L) {
+                                                                const int32_t *__restrict__ slots, int32_t L,
+                                                                RopeArgs rope) {
   constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
   constexpr int GE = D / G;  // elements per scale group
   constexpr int VB = 64 * D;         // V bytes of a block (region offset v_offset(D))
@@ -105,8 +138,10 @@ __global__ __launch_bounds__(256) void k_quantize_append_blocks(LayerView lv, co
 
   // the chunk's layout, computed by every wave (uniform)
   const int sv = lane < nrows ? srow[lane] : -1;
+  const int pv = ROPE && lane < nrows ? rope.pos[(int64_t)b * L + l0 + lane] : 0;  // row's position
+  const bool pos_ok = !ROPE || (unsigned)pv < (unsigned)rope.max_pos;
   const int prev = __shfl_up(sv, 1, 64);
-  bool bad = lane < nrows && (sv < 0 || (sv >> 6) >= lv.num_blocks);
+  bool bad = lane < nrows && (sv < 0 || (sv >> 6) >= lv.num_blocks || !pos_ok);
   if (lane > 0 && lane < nrows && !bad && sv != prev + 1) bad = !((prev & 63) == 63 && (sv & 63) == 0);
   const bool brk = lane > 0 && lane < nrows && (sv >> 6) != (prev >> 6);
   const unsigned long long brks = __ballot(brk);
@@ -116,13 +151,57 @@ __global__ __launch_bounds__(256) void k_quantize_append_blocks(LayerView lv, co
   const int blkA = slot0 >> 6, tA = slot0 & 63;
   const int blkB = brks ? __builtin_amdgcn_readlane(sv, nA) >> 6 : -1;
 
+  // RoPE: the chunk's K rows rotated by the whole workgroup into LDS (four
+  // pairs (i, i + D/2) per thread step, element dtype bits), then quantized
+  // from there like unrotated rows from memory.
+  __shared__ __attribute__((aligned(16))) uint16_t krot[ROPE ? 64 * D : 8];
+  if constexpr (ROPE) {
+    constexpr int QPR = D / 8;  // quads of pairs per row
+#pragma unroll 1
+    for (int q = tid; q < 64 * QPR; q += 256) {
+      const int r = q / QPR, i4 = 4 * (q % QPR);
+      const int p = __shfl(pv, r, 64);
+      if (r >= nrows || (unsigned)p >= (unsigned)rope.max_pos) continue;
+      const uint16_t *row = k + (int64_t)b * sb + (int64_t)h * sh + (int64_t)(l0 + r) * sl;
+      const uint2 w1 = *reinterpret_cast<const uint2 *>(row + i4);
+      const uint2 w2 = *reinterpret_cast<const uint2 *>(row + D / 2 + i4);
+      const float4 c4 = *reinterpret_cast<const float4 *>(rope.cs + (int64_t)p * D + i4);
+      const float4 s4 = *reinterpret_cast<const float4 *>(rope.cs + (int64_t)p * D + D / 2 + i4);
+      const uint16_t a[4] = {(uint16_t)(w1.x & 0xffffu), (uint16_t)(w1.x >> 16), (uint16_t)(w1.y & 0xffffu),
+                             (uint16_t)(w1.y >> 16)};
+      const uint16_t c[4] = {(uint16_t)(w2.x & 0xffffu), (uint16_t)(w2.x >> 16), (uint16_t)(w2.y & 0xffffu),
+                             (uint16_t)(w2.y >> 16)};
+      const float cv[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
+      uint16_t o1[4], o2[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float x1 = elem_to_f32<DT>(a[j]), x2 = elem_to_f32<DT>(c[j]);
+        const float y1 = x1 * cv[j] - x2 * sn[j], y2 = x1 * sn[j] + x2 * cv[j];
+        o1[j] = DT == DT_BF16 ? f32_to_bf16_bits(y1) : f32_to_f16_bits(y1);
+        o2[j] = DT == DT_BF16 ? f32_to_bf16_bits(y2) : f32_to_f16_bits(y2);
+      }
+      *reinterpret_cast<uint2 *>(krot + r * D + i4) =
+          uint2{(uint32_t)o1[0] | ((uint32_t)o1[1] << 16), (uint32_t)o1[2] | ((uint32_t)o1[3] << 16)};
+      *reinterpret_cast<uint2 *>(krot + r * D + D / 2 + i4) =
+          uint2{(uint32_t)o2[0] | ((uint32_t)o2[1] << 16), (uint32_t)o2[2] | ((uint32_t)o2[3] << 16)};
+    }
+    __syncthreads();
+  }
+
 #pragma unroll 1
   for (int item = tid; item < ITEMS; item += 256) {
     const int kv = item / (64 * G), r = (item / G) % 64, g = item % G;
+    // both reads before any lane leaves the iteration: a lane-crossing read
+    // from a lane that is switched off returns 0, not that lane's value
     const int slot = __shfl(sv, r, 64);
+    const int p = __shfl(pv, r, 64);
     if (r >= nrows || slot < 0 || (slot >> 6) >= lv.num_blocks) continue;
+    if (ROPE && (unsigned)p >= (unsigned)rope.max_pos) continue;
     const int t = slot & 63;
-    const uint16_t *src = (kv ? v : k) + (int64_t)b * sb + (int64_t)h * sh + (int64_t)(l0 + r) * sl + g * GE;
+    // K with RoPE: the group's rotated elements from the LDS copy
+    const uint16_t *src = (ROPE && kv == 0)
+                              ? krot + r * D + g * GE
+                              : (kv ? v : k) + (int64_t)b * sb + (int64_t)h * sh + (int64_t)(l0 + r) * sl + g * GE;
     uint4 raw[GE / 8];
 #pragma unroll
     for (int c = 0; c < GE / 8; ++c) raw[c] = *reinterpret_cast<const uint4 *>(src + 8 * c);
@@ -533,9 +612,10 @@ __global__ __launch_bounds__(64) void k_attn_merge_flat(AttnArgs a) {
 
 static inline unsigned wave_blocks(int64_t waves) { return (unsigned)((waves + 3) / 4); }
 
-hipError_t launch_quantize_append(const PoolGeometry &g, int32_t layer, const void *k, const void *v,
-                                  int64_t sb, int64_t sh, int64_t sl, const int32_t *slots, int32_t B,
-                                  int32_t L, hipStream_t st) {
+template <bool ROPE>
+static hipError_t launch_append_rope(const PoolGeometry &g, int32_t layer, const void *k, const void *v, int64_t sb,
+                                     int64_t sh, int64_t sl, const int32_t *slots, int32_t B, int32_t L,
+                                     const RopeArgs &rope, hipStream_t st) {
   const int64_t waves = 2 * (int64_t)B * g.Hkv * L;
   if (waves == 0) return hipSuccess;
   const LayerView lv = layer_view(g, layer);
@@ -547,14 +627,14 @@ hipError_t launch_quantize_append(const PoolGeometry &g, int32_t layer, const vo
     KRILL_DISPATCH_D(g.D, {
       if (g.mode == MODE_REF) {
         if (g.in_dtype == DT_BF16)
-          k_quantize_append_blocks<D, MODE_REF, DT_BF16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, L);
+          k_quantize_append_blocks<D, MODE_REF, DT_BF16, ROPE><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, L, rope);
         else
-          k_quantize_append_blocks<D, MODE_REF, DT_F16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, L);
+          k_quantize_append_blocks<D, MODE_REF, DT_F16, ROPE><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, L, rope);
       } else {
         if (g.in_dtype == DT_BF16)
-          k_quantize_append_blocks<D, MODE_AFFINE, DT_BF16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, L);
+          k_quantize_append_blocks<D, MODE_AFFINE, DT_BF16, ROPE><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, L, rope);
         else
-          k_quantize_append_blocks<D, MODE_AFFINE, DT_F16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, L);
+          k_quantize_append_blocks<D, MODE_AFFINE, DT_F16, ROPE><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, L, rope);
       }
     });
     return hipGetLastError();
@@ -563,17 +643,26 @@ hipError_t launch_quantize_append(const PoolGeometry &g, int32_t layer, const vo
   KRILL_DISPATCH_D(g.D, {
     if (g.mode == MODE_REF) {
       if (g.in_dtype == DT_BF16)
-        k_quantize_append<D, MODE_REF, DT_BF16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, B, L, g.Hkv);
+        k_quantize_append<D, MODE_REF, DT_BF16, ROPE><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, B, L, g.Hkv, rope);
       else
-        k_quantize_append<D, MODE_REF, DT_F16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, B, L, g.Hkv);
+        k_quantize_append<D, MODE_REF, DT_F16, ROPE><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, B, L, g.Hkv, rope);
     } else {
       if (g.in_dtype == DT_BF16)
-        k_quantize_append<D, MODE_AFFINE, DT_BF16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, B, L, g.Hkv);
+        k_quantize_append<D, MODE_AFFINE, DT_BF16, ROPE><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, B, L, g.Hkv, rope);
       else
-        k_quantize_append<D, MODE_AFFINE, DT_F16><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, B, L, g.Hkv);
+        k_quantize_append<D, MODE_AFFINE, DT_F16, ROPE><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, B, L, g.Hkv, rope);
     }
   });
   return hipGetLastError();
+}
+
+hipError_t launch_quantize_append(const PoolGeometry &g, int32_t layer, const void *k, const void *v,
+                                  int64_t sb, int64_t sh, int64_t sl, const int32_t *slots, int32_t B,
+                                  int32_t L, hipStream_t st, const int32_t *rope_pos, const float *rope_cs,
+                                  int32_t rope_max_pos) {
+  const RopeArgs rope{rope_pos, rope_cs, rope_max_pos};
+  return rope_pos ? launch_append_rope<true>(g, layer, k, v, sb, sh, sl, slots, B, L, rope, st)
+                  : launch_append_rope<false>(g, layer, k, v, sb, sh, sl, slots, B, L, rope, st);
 }
 
 hipError_t launch_gather(const PoolGeometry &g, int32_t layer, const int32_t *tables, const int32_t *lens,

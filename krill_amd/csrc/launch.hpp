@@ -53,9 +53,12 @@ struct AttnPlan {
 int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq, int32_t max_seq_len,
                        int32_t split_blocks, int32_t path, AttnPlan *plan);
 
+// rope_pos non-null: K rows rotated first (MLX RoPE, traditional = false)
+// at positions rope_pos[b][l] from the fp32 table rope_cs[rope_max_pos][D].
 hipError_t launch_quantize_append(const PoolGeometry &g, int32_t layer, const void *k, const void *v,
                                   int64_t sb, int64_t sh, int64_t sl, const int32_t *slots, int32_t B,
-                                  int32_t L, hipStream_t st);
+                                  int32_t L, hipStream_t st, const int32_t *rope_pos = nullptr,
+                                  const float *rope_cs = nullptr, int32_t rope_max_pos = 0);
 hipError_t launch_gather(const PoolGeometry &g, int32_t layer, const int32_t *tables, const int32_t *lens,
                          int32_t B, int32_t max_blocks, int32_t S_out, int32_t left_pad, void *keys,
                          void *values, void *ks, void *kz, void *vs, void *vz, hipStream_t st);

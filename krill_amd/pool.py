@@ -237,6 +237,24 @@ class KVPool:
         L.check(L.lib().krill_quantize_append(self._h, layer, k.data_ptr(), v.data_ptr(), slot_mapping.data_ptr(),
                                               B, Lq, self._stream(stream)))
 
+    def quantize_append_rope(self, layer: int, k, v, slot_mapping, positions, cos_sin, stream=None):
+        """quantize_append with K rotated first (krill_quantize_append_rope):
+        positions int32 [B, L], cos_sin float32 [max_pos, D] (see rope_table)."""
+        torch = _torch()
+        B, H, Lq, D = k.shape
+        if H != self.num_kv_heads or D != self.head_dim:
+            raise ValueError(f"K/V shape {tuple(k.shape)} does not match pool heads/dim")
+        self._check_dev("k", k, self.in_dtype)
+        self._check_dev("v", v, self.in_dtype, k.shape)
+        self._check_dev("slot_mapping", slot_mapping, torch.int32, (B, Lq))
+        self._check_dev("positions", positions, torch.int32, (B, Lq))
+        self._check_dev("cos_sin", cos_sin, torch.float32)
+        if cos_sin.dim() != 2 or cos_sin.shape[1] != D:
+            raise ValueError(f"cos_sin must be [max_pos, {D}]")
+        L.check(L.lib().krill_quantize_append_rope(self._h, layer, k.data_ptr(), v.data_ptr(), H * Lq * D, Lq * D, D,
+                                                   slot_mapping.data_ptr(), positions.data_ptr(), cos_sin.data_ptr(),
+                                                   cos_sin.shape[0], B, Lq, self._stream(stream)))
+
     def quantize_append_strided(self, layer: int, k, v, strides, slot_mapping, B: int, Lq: int, stream=None):
         """k, v: device tensors addressed with element strides (b, h, l), d contiguous."""
         torch = _torch()
@@ -373,6 +391,16 @@ class KVPool:
             lens.data_ptr(), B, mb, max_seq_len, Hq, float(scale), out.data_ptr(), code, ws.data_ptr(),
             ws.numel(), self._stream(stream)))
         return out
+
+
+def rope_table(max_pos: int, head_dim: int, base: float = 10000.0) -> np.ndarray:
+    """float32 [max_pos, head_dim] cos/sin table for krill_quantize_append_rope:
+    row p holds cos(p * base^(-2i/D)) for i < D/2, then the sines, computed
+    in double precision and rounded once (MLX RoPE angles, traditional = false)."""
+    half = head_dim // 2
+    inv = base ** (-2.0 * np.arange(half, dtype=np.float64) / head_dim)
+    ang = np.arange(max_pos, dtype=np.float64)[:, None] * inv[None, :]
+    return np.concatenate([np.cos(ang), np.sin(ang)], axis=1).astype(np.float32)
 
 
 def prefix_key(model_id: str, media_hash, dtype_tag: int, tokens) -> int:

@@ -38,6 +38,12 @@ attention_f64 (a7/a8)       closed forms: one key -> output = that value row;
 stack_left_padded (a5)      closed form of BatchedDecode.swift:119-147 on
                             integer rows (tests/test_oracle.py).
 prefix_key (a10)            FNV-1a 64 published test vectors ("" and "a").
+rope_rows (next row 3)      closed forms: position 0 of a cos/sin table is the
+                            identity bit for bit; a quarter turn (cos 0,
+                            sin 1) maps (x, y) -> (-y, x) exactly; against
+                            the float64 rotation of each (i, i + D/2) pair
+                            within one rounding of the element dtype; two
+                            turns compose to their sum; pair norms kept.
 ==========================  ====================================================
 """
 from __future__ import annotations
@@ -203,6 +209,25 @@ def quantize_mlx(x_bits: np.ndarray, dt: int, group: int = 64):
 def quantize(x_bits: np.ndarray, dt: int, mode: int, group: int = 64):
     """mode 0 = reference rows, mode 1 = affine groups of `group`."""
     return quantize_ref(x_bits, dt) if mode == 0 else quantize_mlx(x_bits, dt, group)
+
+
+def rope_rows(x_bits: np.ndarray, dt: int, positions, cos_sin) -> np.ndarray:
+    """RoPE of rows [..., D] (MLX RoPE, traditional = false, all D dims) as
+    krill_quantize_append_rope applies it to K: pair (i, i + D/2) of the row
+    at position p turns by the table's angle i: x'[i] = x[i] c - x[i+D/2] s,
+    x'[i+D/2] = x[i] s + x[i+D/2] c in float32 (each product and sum rounded
+    once), then rounded to the element dtype.  positions: one per row
+    (shape x.shape[:-1]); cos_sin: float32 [max_pos, D].  Returns dtype bits."""
+    x = bits_to_f32(x_bits, dt)
+    D = x.shape[-1]
+    h = D // 2
+    cs = np.asarray(cos_sin, np.float32)[np.asarray(positions)]
+    c, s = cs[..., :h], cs[..., h:]
+    x1, x2 = x[..., :h], x[..., h:]
+    o1 = (x1 * c).astype(np.float32) - (x2 * s).astype(np.float32)
+    o2 = (x1 * s).astype(np.float32) + (x2 * c).astype(np.float32)
+    o = np.concatenate([o1, o2], axis=-1).astype(np.float32)
+    return f32_to_bf16_bits(o) if dt == DT_BF16 else f32_to_f16_bits(o)
 
 
 def dequant_ref_f16(q, s, z) -> np.ndarray:

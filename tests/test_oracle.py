@@ -305,3 +305,64 @@ def test_common_prefix_length_reference_vectors(oracle):
     assert cpl([1, 2], [1, 2, 3, 4]) == 2
     assert cpl([9, 1], [1, 2]) == 0
     assert cpl([], [1]) == 0
+
+
+# ---------------------------------------------------------------- RoPE rows
+def _rope_table(max_pos, D, base=10000.0):
+    from krill_amd.pool import rope_table
+
+    return rope_table(max_pos, D, base)
+
+
+def _bits(oracle, rng, shape, dt):
+    x = rng.standard_normal(shape).astype(np.float32)
+    return oracle.f32_to_bf16_bits(x) if dt == oracle.DT_BF16 else oracle.f32_to_f16_bits(x)
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+def test_rope_position_zero_is_identity_and_quarter_turn_swaps(oracle, bf16):
+    dt = oracle.DT_BF16 if bf16 else oracle.DT_F16
+    rng = np.random.default_rng(3)
+    D = 64
+    x = _bits(oracle, rng, (5, D), dt)
+    tab = _rope_table(4, D)
+    assert np.array_equal(oracle.rope_rows(x, dt, np.zeros(5, np.int64), tab), x)
+    quarter = np.concatenate([np.zeros((1, D // 2), np.float32), np.ones((1, D // 2), np.float32)], axis=1)
+    y = oracle.rope_rows(x, dt, np.zeros(5, np.int64), quarter)
+    xf, yf = oracle.bits_to_f32(x, dt), oracle.bits_to_f32(y, dt)
+    np.testing.assert_array_equal(yf[:, : D // 2], -xf[:, D // 2:])
+    np.testing.assert_array_equal(yf[:, D // 2:], xf[:, : D // 2])
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+def test_rope_matches_float64_pair_rotation(oracle, bf16):
+    dt = oracle.DT_BF16 if bf16 else oracle.DT_F16
+    rng = np.random.default_rng(4)
+    D, P = 128, 300
+    x = _bits(oracle, rng, (P, D), dt)
+    pos = rng.integers(0, 4096, P)
+    tab = _rope_table(4096, D)
+    got = oracle.bits_to_f32(oracle.rope_rows(x, dt, pos, tab), dt).astype(np.float64)
+    xf = oracle.bits_to_f32(x, dt).astype(np.float64)
+    h = D // 2
+    ang = pos[:, None] * (10000.0 ** (-2.0 * np.arange(h) / D))[None, :]
+    c, s = np.cos(ang), np.sin(ang)
+    want = np.concatenate([xf[:, :h] * c - xf[:, h:] * s, xf[:, :h] * s + xf[:, h:] * c], axis=1)
+    ulp = 2.0 ** -8 if bf16 else 2.0 ** -11
+    # one rounding to the element dtype on top of the float32 steps and the table's rounding
+    tol = ulp * np.abs(want) + 1e-6 * (np.abs(xf).max(axis=1, keepdims=True) + 1)
+    assert np.all(np.abs(got - want) <= tol)
+    n0 = np.hypot(xf[:, :h], xf[:, h:])
+    n1 = np.hypot(got[:, :h], got[:, h:])
+    assert np.all(np.abs(n1 - n0) <= 2 * ulp * n0 + 1e-6)
+
+
+def test_rope_turns_compose(oracle):
+    rng = np.random.default_rng(5)
+    D, dt = 64, oracle.DT_F16
+    x = _bits(oracle, rng, (50, D), dt)
+    tab = _rope_table(64, D)
+    twice = oracle.rope_rows(oracle.rope_rows(x, dt, np.full(50, 17), tab), dt, np.full(50, 23), tab)
+    direct = oracle.rope_rows(x, dt, np.full(50, 40), tab)
+    a, b = oracle.bits_to_f32(twice, dt), oracle.bits_to_f32(direct, dt)
+    assert np.abs(a - b).max() <= 4 * 2.0 ** -11 * np.abs(b).max()
