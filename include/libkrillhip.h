@@ -271,6 +271,21 @@ int32_t krill_decode_append_attention(krill_pool_t pool, int32_t layer, const vo
                                       int32_t max_seq_len, int32_t Hq, float scale, void *dev_out,
                                       int32_t out_dtype, void *dev_ws, size_t ws_bytes,
                                       krill_stream_t stream);
+/* The decode step with RoPE as well: krill_decode_append_attention for
+ * unrotated queries and new K rows, each turned first by its token's
+ * position seq_lens[b] - 1 exactly as krill_quantize_append_rope turns K
+ * (table dev_cos_sin[max_pos][D], max_pos >= max_seq_len): the
+ * applyRoPEPerRow of queries and keys (Attention.swift:13-20), then
+ * update() and SDPA.  The output and the pool bytes equal those of
+ * krill_quantize_append_rope at the reserved slots followed by
+ * krill_decode_attention on the rotated queries. */
+int32_t krill_decode_append_attention_rope(krill_pool_t pool, int32_t layer, const void *dev_q,
+                                           const void *dev_k_new, const void *dev_v_new, int64_t stride_b,
+                                           int64_t stride_h, const int32_t *dev_block_tables,
+                                           const int32_t *dev_seq_lens, int32_t B, int32_t max_blocks,
+                                           int32_t max_seq_len, int32_t Hq, float scale, const float *dev_cos_sin,
+                                           int32_t max_pos, void *dev_out, int32_t out_dtype, void *dev_ws,
+                                           size_t ws_bytes, krill_stream_t stream);
 /* Speculative-verify / chunked-prefill attention: Lq new query rows per
  * sequence, already appended, causal inside the window (row j sees tokens
  * [0, len - Lq + j]; BatchedDecode.swift:299-312, LlamaModel.swift:186-202).

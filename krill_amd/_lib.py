@@ -154,6 +154,8 @@ SIGNATURES = {
                                ctypes.c_size_t, P],
     "krill_decode_append_attention": [P, I32, P, P, P, I64, I64, P, P, I32, I32, I32, I32, ctypes.c_float, P,
                                       I32, P, ctypes.c_size_t, P],
+    "krill_decode_append_attention_rope": [P, I32, P, P, P, I64, I64, P, P, I32, I32, I32, I32, ctypes.c_float, P,
+                                           I32, P, I32, P, ctypes.c_size_t, P],
 }
 _RESTYPE = {"krill_last_error": ctypes.c_char_p}
 

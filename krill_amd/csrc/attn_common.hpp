@@ -48,6 +48,11 @@ struct AttnArgs {
   int32_t out_dtype;
   const uint16_t *k_new, *v_new;  // fused append of the newest token (null: none)
   int64_t kn_sb, kn_sh;           // their element strides (batch, head)
+  // RoPE (null: none): queries and the newest K rows turn by their positions
+  // (query row j of sequence b: lens[b] - Lq + j) with the fp32 table
+  // rope_cs[rope_max_pos][D]
+  const float *rope_cs;
+  int32_t rope_max_pos;
 };
 
 inline AttnArgs make_attn_args(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p) {
@@ -83,6 +88,8 @@ inline AttnArgs make_attn_args(const PoolGeometry &g, int32_t layer, const AttnL
   r.v_new = static_cast<const uint16_t *>(a.v_new);
   r.kn_sb = a.kn_sb;
   r.kn_sh = a.kn_sh;
+  r.rope_cs = a.rope_cs;
+  r.rope_max_pos = a.rope_max_pos;
   return r;
 }
 
@@ -98,6 +105,45 @@ __device__ __forceinline__ int seq_blocks(const AttnArgs &a, int len) {
 
 __device__ __forceinline__ float load_q(const uint16_t *p, int dt) {
   return dt == DT_BF16 ? bf16_bits_to_f32(*p) : f16_bits_to_f32(*p);
+}
+
+// RoPE table row of position `pos` (clamped into the table: positions come
+// from device lengths the host bounds by max_seq_len <= rope_max_pos).
+__device__ __forceinline__ const float *rope_row(const AttnArgs &a, int pos, int D) {
+  pos = pos < 0 ? 0 : (pos >= a.rope_max_pos ? a.rope_max_pos - 1 : pos);
+  return a.rope_cs + (int64_t)pos * D;
+}
+
+// RoPE of one row held as E = D/64 elements per lane (d = lane*E + e, dtype
+// bits): MLX RoPE, traditional = false -- the partner of d is d +- D/2, in
+// lane ^ 32 -- in fp32, each product and sum rounded once, then rounded to
+// the dtype.  All 64 lanes must be active.
+template <int D, int DT>
+__device__ __forceinline__ void rope_row_lanes(uint16_t (&x)[D / 64], const float *crow) {
+  constexpr int E = D / 64;
+  const int lane = threadIdx.x & 63;
+  const bool hi = lane >= 32;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float xv = elem_to_f32<DT>(x[e]);
+    const float o = __shfl_xor(xv, 32, 64);
+    const int i = (lane & 31) * E + e;
+    const float c = crow[i], sn = crow[D / 2 + i];
+    const float r = hi ? o * sn + xv * c : xv * c - o * sn;
+    x[e] = DT == DT_BF16 ? f32_to_bf16_bits(r) : f32_to_f16_bits(r);
+  }
+}
+// The same for a pair of dtype elements per word: lo holds elements (d, d+1),
+// hi their partners (d + D/2, d + D/2 + 1); c2 / s2 the pair's cos / sin.
+template <int DT>
+__device__ __forceinline__ void rope_pair_words(uint32_t &lo, uint32_t &hi, float2 c2, float2 s2) {
+  const float a0 = elem_to_f32<DT>((uint16_t)(lo & 0xffffu)), a1 = elem_to_f32<DT>((uint16_t)(lo >> 16));
+  const float b0 = elem_to_f32<DT>((uint16_t)(hi & 0xffffu)), b1 = elem_to_f32<DT>((uint16_t)(hi >> 16));
+  const float r0 = a0 * c2.x - b0 * s2.x, r1 = a1 * c2.y - b1 * s2.y;
+  const float t0 = a0 * s2.x + b0 * c2.x, t1 = a1 * s2.y + b1 * c2.y;
+  auto bits = [](float f) -> uint32_t { return DT == DT_BF16 ? f32_to_bf16_bits(f) : f32_to_f16_bits(f); };
+  lo = bits(r0) | (bits(r1) << 16);
+  hi = bits(t0) | (bits(t1) << 16);
 }
 
 // Output / partial-result addressing.  Rows are r = j*R + h (query position

@@ -57,7 +57,7 @@ __host__ __device__ constexpr int mfma_stage_bytes(int D, int G) { return (head_
 // compute unit, which costs more than the deeper prefetch gains).
 __host__ __device__ constexpr int mfma_stages(int D) { return 2; }
 
-template <int D, int MODE, int NRT>
+template <int D, int MODE, int NRT, bool ROPE>
 __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
   constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
   constexpr int KS = D / 32;   // 32-d steps of Q.K^T
@@ -153,6 +153,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
 #pragma unroll
   for (int rt = 0; rt < NRT; ++rt) rvalid[rt] = rbase + 16 * rt + n < a.NR;
   uint4 qraw[NRT][KS];
+  int qlen = 0;  // length of the sequence whose queries are loaded (RoPE positions)
   auto load_q = [&](int bq) {
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
@@ -162,8 +163,36 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) qraw[rt][ks] = *reinterpret_cast<const uint4 *>(qp + 32 * ks + 8 * q4);
     }
+    if constexpr (ROPE) qlen = seq_len(bq);
   };
   auto finish_q = [&]() {
+    if constexpr (ROPE) {
+      // lane's row (query position j = r / R, token qlen - Lq + j): the 8
+      // elements of step ks < KS/2 turn with those of step ks + KS/2
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt) {
+        const int r = rvalid[rt] ? rbase + 16 * rt + n : 0;
+        const float *crow = rope_row(a, qlen - a.Lq + r / a.R, D);
+#pragma unroll
+        for (int ks = 0; ks < KS / 2; ++ks) {
+          const int d = 32 * ks + 8 * q4;
+          uint32_t lo[4] = {qraw[rt][ks].x, qraw[rt][ks].y, qraw[rt][ks].z, qraw[rt][ks].w};
+          uint32_t hi[4] = {qraw[rt][ks + KS / 2].x, qraw[rt][ks + KS / 2].y, qraw[rt][ks + KS / 2].z,
+                            qraw[rt][ks + KS / 2].w};
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const float2 c2 = *reinterpret_cast<const float2 *>(crow + d + 2 * w);
+            const float2 s2 = *reinterpret_cast<const float2 *>(crow + D / 2 + d + 2 * w);
+            if (a.q_dtype == DT_BF16)
+              rope_pair_words<DT_BF16>(lo[w], hi[w], c2, s2);
+            else
+              rope_pair_words<DT_F16>(lo[w], hi[w], c2, s2);
+          }
+          qraw[rt][ks] = uint4{lo[0], lo[1], lo[2], lo[3]};
+          qraw[rt][ks + KS / 2] = uint4{hi[0], hi[1], hi[2], hi[3]};
+        }
+      }
+    }
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
 #pragma unroll
@@ -515,8 +544,18 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
 template <int D, int MODE>
 static hipError_t launch_mfma_nrt(const AttnArgs &args, int NRT, dim3 grid, hipStream_t st) {
   switch (NRT) {
-    case 1: k_attn_mfma<D, MODE, 1><<<grid, dim3(64), 0, st>>>(args); break;
-    case 2: k_attn_mfma<D, MODE, 2><<<grid, dim3(64), 0, st>>>(args); break;
+    case 1:
+      if (args.rope_cs)
+        k_attn_mfma<D, MODE, 1, true><<<grid, dim3(64), 0, st>>>(args);
+      else
+        k_attn_mfma<D, MODE, 1, false><<<grid, dim3(64), 0, st>>>(args);
+      break;
+    case 2:
+      if (args.rope_cs)
+        k_attn_mfma<D, MODE, 2, true><<<grid, dim3(64), 0, st>>>(args);
+      else
+        k_attn_mfma<D, MODE, 2, false><<<grid, dim3(64), 0, st>>>(args);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -550,9 +589,9 @@ template <int D, int MODE>
 static int32_t occupancy_mfma(int nrt) {
   int n = 0;
   hipError_t e = nrt == 2 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                                &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, 2>), 64, 0)
+                                &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, 2, false>), 64, 0)
                           : hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                                &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, 1>), 64, 0);
+                                &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, 1, false>), 64, 0);
   if (e != hipSuccess || n <= 0) {
     (void)hipGetLastError();
     n = (160 * 1024) / (mfma_stages(D) * mfma_stage_bytes(D, MODE == MODE_AFFINE ? D / 64 : 1));

@@ -193,7 +193,7 @@ __device__ __forceinline__ void store_newest(const AttnArgs &a, int hk, int phys
   }
 }
 
-template <int D, int NR, int MODE>
+template <int D, int NR, int MODE, bool ROPE>
 __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_valu(AttnArgs a) {
   constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
   constexpr int NP = D / 16;   // 16-byte K pieces per token row
@@ -298,10 +298,13 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   auto prepare = [&](int bs, int f) {
     const int len2 = seq_len(bs);
     if (!((tab_okm >> (f - i0)) & 1)) return;
-    if (a.q_dtype == DT_BF16)
+    if (a.q_dtype == DT_BF16) {
+      if constexpr (ROPE) rope_row_lanes<D, DT_BF16>(rk, rope_row(a, len2 - 1, D));
       prepare_newest<D, MODE, DT_BF16>(rk, rv, newrow, pkm, pvm);
-    else
+    } else {
+      if constexpr (ROPE) rope_row_lanes<D, DT_F16>(rk, rope_row(a, len2 - 1, D));
       prepare_newest<D, MODE, DT_F16>(rk, rv, newrow, pkm, pvm);
+    }
     patch_i = f;
     patch_t = (len2 - 1) & 63;
   };
@@ -342,6 +345,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   uint32_t qv[NR][D / 32];
   float qs[NR][G];
   const bool q_bf16 = a.q_dtype == DT_BF16;
+  int qlen = 0;  // length of the sequence whose queries are loaded (RoPE positions)
   auto load_q = [&](int bq) {  // raw pairs of sequence bq
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
@@ -350,8 +354,28 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) qv[r][c] = qp[16 * c + (lane & 15)];
     }
+    if constexpr (ROPE) qlen = seq_len(bq);
   };
   auto finish_q = [&]() {
+    if constexpr (ROPE) {
+      // row r (query position j = r / R, token qlen - Lq + j): pair words
+      // 16 c + (lane & 15) of the first half turn with their partners
+      // D/64 columns on
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const float *crow = rope_row(a, qlen - a.Lq + r / a.R, D);
+#pragma unroll
+        for (int c = 0; c < D / 64; ++c) {
+          const int d = 2 * (16 * c + (lane & 15));
+          const float2 c2 = *reinterpret_cast<const float2 *>(crow + d);
+          const float2 s2 = *reinterpret_cast<const float2 *>(crow + D / 2 + d);
+          if (q_bf16)
+            rope_pair_words<DT_BF16>(qv[r][c], qv[r][c + D / 64], c2, s2);
+          else
+            rope_pair_words<DT_F16>(qv[r][c], qv[r][c + D / 64], c2, s2);
+        }
+      }
+    }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
 #pragma unroll
@@ -718,7 +742,10 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
 
 template <int D, int MODE, int NR>
 static void launch_one(const AttnArgs &args, int B, dim3 grid, hipStream_t st) {
-  k_attn_valu<D, NR, MODE><<<grid, dim3(64), 0, st>>>(args);
+  if (args.rope_cs)
+    k_attn_valu<D, NR, MODE, true><<<grid, dim3(64), 0, st>>>(args);
+  else
+    k_attn_valu<D, NR, MODE, false><<<grid, dim3(64), 0, st>>>(args);
 }
 
 template <int D, int MODE>
@@ -744,7 +771,7 @@ static int32_t occupancy_nr(int NR) {
   switch (NR) {
 #define KRILL_OCC(N)                                                                                        \
   case N:                                                                                                   \
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(&k_attn_valu<D, N, MODE>), \
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(&k_attn_valu<D, N, MODE, false>), \
                                                      64, 0);                                                \
     if (e != hipSuccess || n <= 0) n = 4 * valu_waves_per_simd<D, N>();                                    \
     break;

@@ -484,6 +484,8 @@ int32_t krill_attention_workspace_size(krill_pool_t pool, int32_t B, int32_t Hq,
 struct NewTokens {  // decode step with the append fused (all null/zero: none)
   const void *k = nullptr, *v = nullptr;
   int64_t sb = 0, sh = 0;
+  const float *rope_cs = nullptr;  // RoPE of the queries and the new K rows (null: none)
+  int32_t rope_max_pos = 0;
 };
 
 static int32_t run_attention(krill_pool_t pool, int32_t layer, const void *dev_q, int32_t Lq,
@@ -528,6 +530,8 @@ static int32_t run_attention(krill_pool_t pool, int32_t layer, const void *dev_q
   a.v_new = nt.v;
   a.kn_sb = nt.sb;
   a.kn_sh = nt.sh;
+  a.rope_cs = nt.rope_cs;
+  a.rope_max_pos = nt.rope_max_pos;
   DeviceGuard dg(pool->device);
   hipStream_t st = pick_stream(pool, stream);
   if (int32_t rc = flush_pending(pool, st)) return rc;
@@ -559,6 +563,29 @@ int32_t krill_decode_append_attention(krill_pool_t pool, int32_t layer, const vo
   nt.v = dev_v_new;
   nt.sb = stride_b;
   nt.sh = stride_h;
+  return run_attention(pool, layer, dev_q, 1, dev_block_tables, dev_seq_lens, B, max_blocks, max_seq_len, Hq, scale,
+                       dev_out, out_dtype, dev_ws, ws_bytes, stream, nt);
+}
+
+int32_t krill_decode_append_attention_rope(krill_pool_t pool, int32_t layer, const void *dev_q,
+                                           const void *dev_k_new, const void *dev_v_new, int64_t stride_b,
+                                           int64_t stride_h, const int32_t *dev_block_tables,
+                                           const int32_t *dev_seq_lens, int32_t B, int32_t max_blocks,
+                                           int32_t max_seq_len, int32_t Hq, float scale, const float *dev_cos_sin,
+                                           int32_t max_pos, void *dev_out, int32_t out_dtype, void *dev_ws,
+                                           size_t ws_bytes, krill_stream_t stream) {
+  krill::clear_error();
+  if (B > 0 && (!dev_k_new || !dev_v_new || !dev_cos_sin)) return fail(KRILL_E_INVAL, "NULL new K/V or table pointer");
+  if (stride_b < 0 || stride_h < 0) return fail(KRILL_E_INVAL, "negative stride");
+  if (max_pos < 1 || max_pos < max_seq_len)
+    return fail(KRILL_E_INVAL, "RoPE table of %d positions does not cover max_seq_len %d", max_pos, max_seq_len);
+  NewTokens nt;
+  nt.k = dev_k_new;
+  nt.v = dev_v_new;
+  nt.sb = stride_b;
+  nt.sh = stride_h;
+  nt.rope_cs = dev_cos_sin;
+  nt.rope_max_pos = max_pos;
   return run_attention(pool, layer, dev_q, 1, dev_block_tables, dev_seq_lens, B, max_blocks, max_seq_len, Hq, scale,
                        dev_out, out_dtype, dev_ws, ws_bytes, stream, nt);
 }

@@ -315,9 +315,13 @@ __global__ __launch_bounds__(256) void k_append_newest(AttnArgs a) {
   const int phys = a.tables[(int64_t)b * a.max_blocks + nb - 1];
   if ((unsigned)phys >= (unsigned)a.lv.num_blocks) return;
   const uint16_t *src = (kv ? a.v_new : a.k_new) + (int64_t)b * a.kn_sb + (int64_t)h * a.kn_sh + lane * E;
+  uint16_t raw[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) raw[e] = src[e];
+  if (a.rope_cs && kv == 0) rope_row_lanes<D, DT>(raw, rope_row(a, len - 1, D));
   float x[E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) x[e] = elem_to_f32<DT>(src[e]);
+  for (int e = 0; e < E; ++e) x[e] = elem_to_f32<DT>(raw[e]);
   uint8_t qb[E];
   float scale, zero;
   quantize_row<D, MODE, DT>(x, qb, scale, zero);

@@ -34,6 +34,9 @@ struct AttnLaunch {
   // len - 1 before it is read; null for attention over the cache as it is
   const void *k_new = nullptr, *v_new = nullptr;
   int64_t kn_sb = 0, kn_sh = 0;
+  // RoPE of the queries and the newest K rows (null: none), table [max_pos][D]
+  const float *rope_cs = nullptr;
+  int32_t rope_max_pos = 0;
 };
 
 // Splits/rows plan shared by the workspace query and the launch.

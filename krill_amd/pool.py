@@ -358,8 +358,21 @@ class KVPool:
                                                    out.data_ptr(), code, ws.data_ptr(), ws.numel(), st))
         return out
 
+    def decode_append_attention_rope(self, layer: int, q, k_new, v_new, tables, lens, max_seq_len: int,
+                                     scale: float, cos_sin, out_dtype=None, ws=None, out=None, stream=None):
+        """decode_append_attention with the queries and new K rows unrotated:
+        both turn by the new token's position lens[b] - 1 (cos_sin: float32
+        [max_pos, D], max_pos >= max_seq_len; see rope_table)."""
+        return self._decode_append(layer, q, k_new, v_new, tables, lens, max_seq_len, scale, out_dtype, ws, out,
+                                   stream, cos_sin)
+
     def decode_append_attention(self, layer: int, q, k_new, v_new, tables, lens, max_seq_len: int, scale: float,
                                 out_dtype=None, ws=None, out=None, stream=None):
+        return self._decode_append(layer, q, k_new, v_new, tables, lens, max_seq_len, scale, out_dtype, ws, out,
+                                   stream, None)
+
+    def _decode_append(self, layer, q, k_new, v_new, tables, lens, max_seq_len, scale, out_dtype, ws, out, stream,
+                       cos_sin):
         """Decode step with the append fused: writes each sequence's newest token
         (k_new, v_new: [B, Hkv, 1, D] or [B, Hkv, D] in in_dtype) at position
         lens[b] - 1, then attends q [B, Hq, 1, D] over the cache.  Same pool bytes
@@ -386,10 +399,19 @@ class KVPool:
         need = self.workspace_size(B, Hq, 1, max_seq_len)
         if ws is None or ws.numel() < need:
             ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
-        L.check(L.lib().krill_decode_append_attention(
-            self._h, layer, q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), H * D, D, tables.data_ptr(),
-            lens.data_ptr(), B, mb, max_seq_len, Hq, float(scale), out.data_ptr(), code, ws.data_ptr(),
-            ws.numel(), self._stream(stream)))
+        if cos_sin is None:
+            L.check(L.lib().krill_decode_append_attention(
+                self._h, layer, q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), H * D, D, tables.data_ptr(),
+                lens.data_ptr(), B, mb, max_seq_len, Hq, float(scale), out.data_ptr(), code, ws.data_ptr(),
+                ws.numel(), self._stream(stream)))
+        else:
+            self._check_dev("cos_sin", cos_sin, torch.float32)
+            if cos_sin.dim() != 2 or cos_sin.shape[1] != D:
+                raise ValueError(f"cos_sin must be [max_pos, {D}]")
+            L.check(L.lib().krill_decode_append_attention_rope(
+                self._h, layer, q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), H * D, D, tables.data_ptr(),
+                lens.data_ptr(), B, mb, max_seq_len, Hq, float(scale), cos_sin.data_ptr(), cos_sin.shape[0],
+                out.data_ptr(), code, ws.data_ptr(), ws.numel(), self._stream(stream)))
         return out
 
 

@@ -7,7 +7,7 @@ and the output against the oracle directly."""
 import numpy as np
 import pytest
 
-from kvutil import Filled, i32, oracle_attention, rand_bits, to_dev
+from kvutil import DT, Filled, i32, oracle_attention, rand_bits, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -137,3 +137,59 @@ def test_fused_step_qwen3_14b_shape_against_oracle():
     err = np.abs(ctx["out"].float().cpu().numpy() - ref).max()
     assert err <= ATOL, f"max abs error {err:.3e}"
     _close(ctx)
+
+
+@pytest.mark.parametrize("D,R,dt", [(128, 5, "bf16"), (64, 4, "f16"), (256, 2, "bf16"), (128, 16, "bf16")])
+def test_fused_rope_step_matches_rope_append_and_rotated_queries(D, R, dt):
+    """krill_decode_append_attention_rope against krill_quantize_append_rope at
+    the reserved slots + decode attention on queries rotated by the oracle
+    (R = 16: more than 8 rows per KV head, the MFMA path)."""
+    from krill_amd.pool import rope_table
+    from oracle import oracle as O
+
+    print(f"\ncase fused_rope D={D} R={R} dt={dt}", flush=True)
+    H, mode, seed = 2, "affine_g64", 40 + D + R
+    prefill = [70, 1, 200, 64, 517]
+    B = len(prefill)
+    blocks = sum((T + 64) // 64 for T in prefill) + 8
+    pools, fills = [], []
+    for _ in range(2):
+        p = _pool(H, D, mode, dt, blocks, 1, seed, 0, 0)
+        fills.append(Filled(p, prefill, np.random.default_rng(seed), dt))
+        pools.append(p)
+    rng = np.random.default_rng(seed + 1)
+    kn = rand_bits(rng, (B, H, 1, D), dt)
+    vn = rand_bits(rng, (B, H, 1, D), dt)
+    q = rand_bits(rng, (B, H * R, 1, D), dt)
+    lens = np.array([T + 1 for T in prefill], np.int32)
+    slots = [np.stack([p.reserve_append(f.seqs[b], 1) for b in range(B)]).astype(np.int32)
+             for p, f in zip(pools, fills)]
+    np.testing.assert_array_equal(slots[0], slots[1])
+    mb = max((T + 63) // 64 for T in lens)
+    tabs = [p.batch_tables(f.seqs, mb)[0] for p, f in zip(pools, fills)]
+    tables, tl = i32(tabs[0]), i32(lens)
+    max_len = int(lens.max())
+    cs = rope_table(max_len + 3, D, 1.0e6)
+    csd = torch.from_numpy(cs).cuda()
+    pos = (lens - 1).astype(np.int32)
+    scale = 1.0 / np.sqrt(D)
+    # two calls: RoPE append of the new rows, attention on oracle-rotated queries
+    pools[0].quantize_append_rope(0, to_dev(kn, dt), to_dev(vn, dt), i32(slots[0]), i32(pos.reshape(B, 1)), csd)
+    q_rot = O.rope_rows(q, DT[dt], np.broadcast_to(pos[:, None, None], (B, H * R, 1)), cs)
+    out_two = pools[0].attention(0, to_dev(q_rot, dt), tables, tl, max_len, scale)
+    out_fused = pools[1].decode_append_attention_rope(0, to_dev(q, dt), to_dev(kn, dt), to_dev(vn, dt), tables, tl,
+                                                      max_len, scale, csd)
+    torch.cuda.synchronize()
+    assert torch.equal(out_two, out_fused), "fused RoPE step differs from RoPE append + attention"
+    snaps = [p.gather(0, tables, tl, max_len) for p in pools]
+    for name in snaps[0]:
+        a, b_ = snaps[0][name].cpu().numpy(), snaps[1][name].cpu().numpy()
+        assert np.array_equal(a.view(np.uint8), b_.view(np.uint8)), f"pool {name} differs"
+    # and the new K bytes are the oracle's quantization of the rotated row
+    kr = O.rope_rows(kn, DT[dt], np.broadcast_to(pos[:, None, None], (B, H, 1)), cs)
+    kq, _, _ = O.quantize(kr, DT[dt], 1)
+    got = snaps[1]["keys"].cpu().numpy()
+    for b in range(B):
+        np.testing.assert_array_equal(got[b, :, lens[b] - 1], kq[b, :, 0])
+    for p in pools:
+        p.close()
