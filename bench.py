@@ -11,7 +11,9 @@ and its small host->device copies:
   each sequence back to its accepted length;
 - shared prefix: decode steps of sequences forked from one refcounted
   prefix (copy-on-write of the shared partial block, LRU eviction of
-  unreferenced prefix entries at 90 % occupancy).
+  unreferenced prefix entries at 90 % occupancy); attention as the
+  shared-prefix cascade (--single-pass: one decode attention over the
+  whole tables).
 
 Default workload: Qwen3-14B-shaped KV (40 layers, 40 query / 8 KV heads,
 head_dim 128), affine int8 in groups of 64 with fp16 scale/bias, batch 32,
@@ -66,6 +68,9 @@ def parse():
     ap.add_argument("--unfused", action="store_true",
                     help="decode step as two calls per layer (quantize-append, then decode attention) instead of "
                          "the fused krill_decode_append_attention")
+    ap.add_argument("--single-pass", action="store_true",
+                    help="shared-prefix workload: one decode attention over the whole tables instead of the "
+                         "prefix/suffix cascade")
     ap.add_argument("--kernel-reps", type=int, default=5, help="repetitions of the attention-only timing loop")
     ap.add_argument("--cpu-baseline", type=int, default=1, help="1: time the CPU baseline sample on rank 0")
     ap.add_argument("--seed", type=int, default=20261203)
@@ -248,16 +253,23 @@ def _time_calls(env, call, reps):
 class StepTables:
     """Pinned host buffers (ring of 3) and device copies of the step's block tables, lengths and slots."""
 
-    def __init__(self, env, B, max_blocks, slots_per_seq):
+    def __init__(self, env, B, max_blocks, slots_per_seq, prefix_blocks=0):
         t = env.torch
-        self.env, self.B, self.mb = env, B, max_blocks
+        self.env, self.B, self.mb, self.pb = env, B, max_blocks, prefix_blocks
+        sw = max(max_blocks - prefix_blocks, 1)
         self.ring = [(t.empty((B, max(slots_per_seq, 1)), dtype=t.int32).pin_memory(),
                       t.empty((B, max_blocks), dtype=t.int32).pin_memory(),
+                      t.empty((B,), dtype=t.int32).pin_memory(),
+                      t.empty((B, sw), dtype=t.int32).pin_memory(),
                       t.empty((B,), dtype=t.int32).pin_memory()) for _ in range(3)]
         self.events = [None] * 3
         self.d_slots = t.empty((B, max(slots_per_seq, 1)), dtype=t.int32, device=env.dev)
         self.d_tables = t.empty((B, max_blocks), dtype=t.int32, device=env.dev)
         self.d_lens = t.empty((B,), dtype=t.int32, device=env.dev)
+        # with a shared prefix of prefix_blocks blocks: each table from that column on, and the length after it
+        self.suffix_width = sw
+        self.d_suffix_tables = t.empty((B, sw), dtype=t.int32, device=env.dev)
+        self.d_suffix_lens = t.empty((B,), dtype=t.int32, device=env.dev)
 
     def host(self, i):
         j = i % 3
@@ -266,11 +278,17 @@ class StepTables:
         return j, self.ring[j][0].numpy(), self.ring[j][1].numpy(), self.ring[j][2].numpy()
 
     def upload(self, j, slots=True):
-        ps, pt, pl = self.ring[j]
+        ps, pt, pl, sfx_t, sfx_l = self.ring[j]
         if slots:
             self.d_slots.copy_(ps, non_blocking=True)
-        self.d_tables.copy_(pt, non_blocking=True)
-        self.d_lens.copy_(pl, non_blocking=True)
+        if self.pb:
+            sfx_t.numpy()[:] = pt.numpy()[:, self.pb:]
+            sfx_l.numpy()[:] = pl.numpy() - 64 * self.pb
+            self.d_suffix_tables.copy_(sfx_t, non_blocking=True)
+            self.d_suffix_lens.copy_(sfx_l, non_blocking=True)
+        else:
+            self.d_tables.copy_(pt, non_blocking=True)
+            self.d_lens.copy_(pl, non_blocking=True)
         ev = self.env.torch.cuda.Event()
         ev.record(self.env.stream)
         self.events[j] = ev
@@ -321,6 +339,39 @@ def _decode_calls(env, seqs, st, max_len_final, Hq):
             fused(layer, mx)
 
     return step_layer, call_only, keep
+
+
+def _cascade_calls(env, seqs, st, max_len_final, Hq, prefix_table):
+    """Per layer: quantize-append of the new token, then the shared-prefix
+    cascade (prefix pass over the P shared blocks for all B sequences, suffix
+    pass, merge)."""
+    KL, lib, h, sp, w = env.KL, env.lib, env.h, env.sp, env.w
+    B, Hkv, D, layers = len(seqs), w["Hkv"], w["D"], w["layers"]
+    Pb = st.pb
+    q_all = env.randn_bf16((layers, B, Hq, 1, D))
+    k_new = env.randn_bf16((layers, B, Hkv, 1, D))
+    v_new = env.randn_bf16((layers, B, Hkv, 1, D))
+    out = env.torch.empty((B, Hq, 1, D), dtype=env.torch.bfloat16, device=env.dev)
+    need = ctypes.c_size_t()
+    KL.check(lib.krill_shared_prefix_workspace_size(h, B, Hq, Pb, max_len_final - 64 * Pb, ctypes.byref(need)))
+    ws = env.torch.empty(max(need.value, 1), dtype=env.torch.uint8, device=env.dev)
+    qp = [q_all[l].data_ptr() for l in range(layers)]
+    kp = [k_new[l].data_ptr() for l in range(layers)]
+    vp = [v_new[l].data_ptr() for l in range(layers)]
+    scale = ctypes.c_float(1.0 / math.sqrt(D))
+    keep = (q_all, k_new, v_new, out, ws, prefix_table)
+
+    def attend(layer, mx):
+        KL.check(lib.krill_decode_attention_shared_prefix(
+            h, layer, qp[layer], prefix_table.data_ptr(), Pb, st.d_suffix_tables.data_ptr(),
+            st.d_suffix_lens.data_ptr(), B, st.suffix_width, mx - 64 * Pb, Hq, scale, out.data_ptr(),
+            KL.DTYPE_BF16, ws.data_ptr(), need.value, sp))
+
+    def step_layer(layer, mx):
+        KL.check(lib.krill_quantize_append(h, layer, kp[layer], vp[layer], st.d_slots.data_ptr(), B, 1, sp))
+        attend(layer, mx)
+
+    return step_layer, attend, keep
 
 
 def run_decode(args, w):
@@ -449,8 +500,17 @@ def run_shared_prefix(args, w):
     lens0 = P + suffix
     max_len_final = int(lens0.max()) + total_steps
     max_blocks = (max_len_final + 63) // 64
-    st = StepTables(env, B, max_blocks, 1)
-    step_layer, call_only, keep = _decode_calls(env, seqs, st, max_len_final, Hq)
+    cascade = not args.single_pass
+    Pb = P // 64
+    st = StepTables(env, B, max_blocks, 1, prefix_blocks=Pb if cascade else 0)
+    if cascade:
+        # the P full prefix blocks: the same first Pb table entries in every fork
+        t0, _ = pool.batch_tables(seqs, max_blocks)
+        assert (t0[:, :Pb] == t0[0, :Pb]).all()
+        prefix_table = env.torch.as_tensor(np.ascontiguousarray(t0[0, :Pb]), device=env.dev)
+        step_layer, call_only, keep = _cascade_calls(env, seqs, st, max_len_final, Hq, prefix_table)
+    else:
+        step_layer, call_only, keep = _decode_calls(env, seqs, st, max_len_final, Hq)
     seqs_np = np.array(seqs, np.int32)
     one = np.empty(1, np.int32)
     cur_len = [int(x) for x in lens0]
@@ -463,7 +523,7 @@ def run_shared_prefix(args, w):
             ps[b, 0] = one[0]
             cur_len[b] += 1
         env.KL.check(env.lib.krill_batch_tables(env.h, env.i32p(seqs_np), B, max_blocks, env.i32p(pt), env.i32p(pl)))
-        st.upload(j, slots=args.unfused)
+        st.upload(j, slots=args.unfused or cascade)
         mx = max(cur_len)
         for layer in range(layers):
             step_layer(layer, mx)
@@ -490,13 +550,16 @@ def run_shared_prefix(args, w):
                     f"unique suffixes U[{w['lo']},{w['hi']}], {args.quant} int8, pool at the 90 % LRU watermark "
                     f"with {stale_entries} unreferenced {stale_tokens}-token prefix entries; step = per layer "
                     "quantize-append 1 token/seq + paged decode attention"
-                    + (" (two calls)" if args.unfused else " (one fused call)"),
+                    + (f" as a cascade (the {Pb} full prefix blocks attended once for all {B} sequences, each "
+                       "suffix on its own, partials merged)" if cascade else
+                       " (two calls)" if args.unfused else " (one fused call)"),
         "layers": layers, "Hq": Hq, "Hkv": Hkv, "head_dim": D, "batch": B, "quant": args.quant,
-        "prefix": P, "suffix_mean": float(np.mean(suffix)), "num_blocks": num_blocks,
+        "prefix": P, "cascade": cascade, "suffix_mean": float(np.mean(suffix)), "num_blocks": num_blocks,
     }
     roofline = {
         "bound": "hbm",
-        "kernel": "fused append + paged decode attention call, one layer; unique bytes (shared prefix once)",
+        "kernel": ("shared-prefix cascade call (prefix pass + suffix pass + merge), one layer" if cascade else
+                   "fused append + paged decode attention call, one layer") + "; unique bytes (shared prefix once)",
         "achieved": round(uniq_launch / (attn_ms * 1e-3) / 1e9, 2),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",

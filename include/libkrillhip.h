@@ -286,6 +286,25 @@ int32_t krill_decode_append_attention_rope(krill_pool_t pool, int32_t layer, con
                                            int32_t max_seq_len, int32_t Hq, float scale, const float *dev_cos_sin,
                                            int32_t max_pos, void *dev_out, int32_t out_dtype, void *dev_ws,
                                            size_t ws_bytes, krill_stream_t stream);
+/* Decode attention for sequences that share a prefix (forked from one
+ * prefix entry: krill_seq_fork / krill_prefix_lookup, PrefixCache.swift
+ * :161-170 with InferenceEngine.swift:1395-1420): sequence b's keys are the
+ * prefix_blocks * 64 tokens of the blocks dev_prefix_table[0..prefix_blocks)
+ * followed by its own dev_suffix_lens[b] tokens in the blocks
+ * dev_suffix_tables[b][..] (its table from column prefix_blocks on).  Same
+ * output as krill_decode_attention over the whole tables (within floating-
+ * point reassociation): the prefix is attended once for all B sequences'
+ * queries (as one sequence whose query positions are the B sequences, on the
+ * MFMA path when B * Hq/Hkv > 8 rows per KV head), each suffix on its own,
+ * and the partial softmaxes merged.  Three launches on `stream`. */
+int32_t krill_shared_prefix_workspace_size(krill_pool_t pool, int32_t B, int32_t Hq, int32_t prefix_blocks,
+                                           int32_t max_suffix_len, size_t *bytes_out);
+int32_t krill_decode_attention_shared_prefix(krill_pool_t pool, int32_t layer, const void *dev_q,
+                                             const int32_t *dev_prefix_table, int32_t prefix_blocks,
+                                             const int32_t *dev_suffix_tables, const int32_t *dev_suffix_lens,
+                                             int32_t B, int32_t max_blocks, int32_t max_suffix_len, int32_t Hq,
+                                             float scale, void *dev_out, int32_t out_dtype, void *dev_ws,
+                                             size_t ws_bytes, krill_stream_t stream);
 /* Speculative-verify / chunked-prefill attention: Lq new query rows per
  * sequence, already appended, causal inside the window (row j sees tokens
  * [0, len - Lq + j]; BatchedDecode.swift:299-312, LlamaModel.swift:186-202).

@@ -53,6 +53,11 @@ struct AttnArgs {
   // rope_cs[rope_max_pos][D]
   const float *rope_cs;
   int32_t rope_max_pos;
+  // element strides of q (batch, head, query position); default: [B][Hq][Lq][D]
+  int64_t q_sb, q_sh, q_sj;
+  int32_t len_const;     // >= 0: every sequence holds this many tokens (lens not read)
+  int32_t causal;        // 1: query row j sees keys [0, len - Lq + j]; 0: every key
+  int32_t partial_only;  // 1: every segment leaves a partial, none writes the output
 };
 
 inline AttnArgs make_attn_args(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p) {
@@ -90,6 +95,18 @@ inline AttnArgs make_attn_args(const PoolGeometry &g, int32_t layer, const AttnL
   r.kn_sh = a.kn_sh;
   r.rope_cs = a.rope_cs;
   r.rope_max_pos = a.rope_max_pos;
+  if (a.q_strided) {
+    r.q_sb = a.q_sb;
+    r.q_sh = a.q_sh;
+    r.q_sj = a.q_sj;
+  } else {
+    r.q_sj = g.D;
+    r.q_sh = (int64_t)a.Lq * g.D;
+    r.q_sb = (int64_t)a.Hq * a.Lq * g.D;
+  }
+  r.len_const = a.len_const;
+  r.causal = a.causal;
+  r.partial_only = a.partial_only;
   return r;
 }
 
@@ -146,6 +163,17 @@ __device__ __forceinline__ void rope_pair_words(uint32_t &lo, uint32_t &hi, floa
   hi = bits(t0) | (bits(t1) << 16);
 }
 
+// Tokens held by sequence b.
+__device__ __forceinline__ int len_of(const AttnArgs &a, int b) { return a.len_const >= 0 ? a.len_const : a.lens[b]; }
+// Query vector (head hq, position j) of sequence b.
+__device__ __forceinline__ const uint16_t *q_row(const AttnArgs &a, int b, int hq, int j) {
+  return a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + (int64_t)j * a.q_sj;
+}
+// Keys [0, lim) seen by query position j of a sequence of length len.
+__device__ __forceinline__ int key_limit(const AttnArgs &a, int len, int j) {
+  return a.causal ? len - a.Lq + j + 1 : len;
+}
+
 // Output / partial-result addressing.  Rows are r = j*R + h (query position
 // j, head h inside the KV group).
 __device__ __forceinline__ int64_t out_row_base(const AttnArgs &a, int b, int hk, int r, int D) {
@@ -175,7 +203,7 @@ __device__ __forceinline__ int wave_allsum_int(int v) {
 // last key its last row sees (causal window); a single group reads them all.
 __device__ __forceinline__ int seq_blocks_rg(const AttnArgs &a, int len, int rg) {
   const int nb = seq_blocks(a, len);
-  if (a.row_groups <= 1) return nb;
+  if (a.row_groups <= 1 || !a.causal) return nb;
   const int rlast = min(a.NR, (rg + 1) * a.rows_per_group) - 1;
   const int lim = len - a.Lq + rlast / a.R + 1;
   const int nv = lim > 0 ? (lim + 63) >> 6 : 0;
@@ -191,7 +219,7 @@ __device__ __forceinline__ int flat_total_and_start(const AttnArgs &a, int b, in
   int carry = 0;
   for (int c0 = 0; c0 < a.B; c0 += 64) {
     const int bb = c0 + lane;
-    const int nbv = bb < a.B ? seq_blocks_rg(a, a.lens[bb], rg) : 0;
+    const int nbv = bb < a.B ? seq_blocks_rg(a, len_of(a, bb), rg) : 0;
     const int incl = wave_incl_scan(nbv) + carry;
     if (b >= c0 && b < c0 + 64) {
       start_out = __builtin_amdgcn_readlane(incl - nbv, b - c0);

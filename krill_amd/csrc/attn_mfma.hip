@@ -78,13 +78,13 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
 
   // ---- this wave's flat blocks [i0, iend) of the (head, row group) order
   const int W = a.waves;
-  int c0 = 0, lenv = lane < a.B ? a.lens[lane] : 0;
+  int c0 = 0, lenv = lane < a.B ? len_of(a, lane) : 0;
   int nbv = seq_blocks_rg(a, lenv, rg);
   int incl = wave_incl_scan(nbv);
   int T = __builtin_amdgcn_readlane(incl, 63);
   for (int cc = 64; cc < a.B; cc += 64) {
     const int bb = cc + lane;
-    T += __builtin_amdgcn_readfirstlane(wave_allsum_int(bb < a.B ? seq_blocks_rg(a, a.lens[bb], rg) : 0));
+    T += __builtin_amdgcn_readfirstlane(wave_allsum_int(bb < a.B ? seq_blocks_rg(a, len_of(a, bb), rg) : 0));
   }
   const int Wt = min(W, T);  // every participating wave holds >= 1 block
   if (wv >= Wt) return;
@@ -96,7 +96,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
     for (c0 = 0; c0 < a.B; c0 += 64) {
       if (c0 > 0) {
         const int bb = c0 + lane;
-        lenv = bb < a.B ? a.lens[bb] : 0;
+        lenv = bb < a.B ? len_of(a, bb) : 0;
         nbv = seq_blocks_rg(a, lenv, rg);
         incl = wave_incl_scan(nbv) + carry;
       }
@@ -111,7 +111,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
     }
   }
   if (b < 0) return;
-  auto seq_len = [&](int bs) -> int { return bs - c0 < 64 ? __builtin_amdgcn_readlane(lenv, bs - c0) : a.lens[bs]; };
+  auto seq_len = [&](int bs) -> int { return bs - c0 < 64 ? __builtin_amdgcn_readlane(lenv, bs - c0) : len_of(a, bs); };
 
   // block-table entries of flat blocks i0 .. iend-1 (<= 64), lane j: block i0 + j
   int tab = 0, iend_eff = iend;
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
     for (int rt = 0; rt < NRT; ++rt) {
       const int r = rvalid[rt] ? rbase + 16 * rt + n : 0;
       const int hq = hk * a.R + r % a.R, j = r / a.R;
-      const uint16_t *qp = a.q + (((int64_t)bq * a.Hq + hq) * a.Lq + j) * D;
+      const uint16_t *qp = q_row(a, bq, hq, j);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) qraw[rt][ks] = *reinterpret_cast<const uint4 *>(qp + 32 * ks + 8 * q4);
     }
@@ -243,9 +243,9 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
       const int r = rbase + 16 * rt + n;
-      lim[rt] = rvalid[rt] ? len - a.Lq + r / a.R + 1 : 0;
+      lim[rt] = rvalid[rt] ? key_limit(a, len, r / a.R) : 0;
     }
-    const int lim_lo = len - a.Lq + rbase / a.R + 1;  // keys seen by the group's first row
+    const int lim_lo = key_limit(a, len, rbase / a.R);  // keys seen by the group's first row
     float m_run[NRT], l_part[NRT], c_part[NRT][G];
     float4_t oacc[NRT][NDT];
 #pragma unroll
@@ -484,7 +484,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
     // ---- end of the segment: lane holds O^T[d = 16*dt + 4*q4 + e][row n].
     // The whole sequence in this wave -> output; otherwise a partial in slot
     // (hk * row_groups + rg) * (waves + B) + wave + b.
-    const bool whole = s >= i0 && e <= iend;
+    const bool whole = !a.partial_only && s >= i0 && e <= iend;
     const int64_t slot = ((int64_t)hk * RG + rg) * (a.waves + a.B) + wv + b;
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {

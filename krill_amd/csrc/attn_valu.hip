@@ -214,13 +214,13 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   // Sequence lengths of the first 64 sequences stay in `lenv` (lane j:
   // sequence c0 + j, c0 = the chunk holding the wave's first sequence).
   const int W = a.waves;
-  int c0 = 0, lenv = lane < a.B ? a.lens[lane] : 0;
+  int c0 = 0, lenv = lane < a.B ? len_of(a, lane) : 0;
   int nbv = seq_blocks(a, lenv);
   int incl = wave_incl_scan(nbv);
   int T = __builtin_amdgcn_readlane(incl, 63);
   for (int cc = 64; cc < a.B; cc += 64) {
     const int bb = cc + lane;
-    T += __builtin_amdgcn_readfirstlane(wave_allsum_int(bb < a.B ? seq_blocks(a, a.lens[bb]) : 0));
+    T += __builtin_amdgcn_readfirstlane(wave_allsum_int(bb < a.B ? seq_blocks(a, len_of(a, bb)) : 0));
   }
   // At most T waves take part, so every participating wave holds at least
   // one block (the merge relies on it: each wave between a sequence's first
@@ -235,7 +235,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     for (c0 = 0; c0 < a.B; c0 += 64) {
       if (c0 > 0) {
         const int bb = c0 + lane;
-        lenv = bb < a.B ? a.lens[bb] : 0;
+        lenv = bb < a.B ? len_of(a, bb) : 0;
         nbv = seq_blocks(a, lenv);
         incl = wave_incl_scan(nbv) + carry;
       }
@@ -250,7 +250,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     }
   }
   if (b < 0) return;
-  auto seq_len = [&](int bs) -> int { return bs - c0 < 64 ? __builtin_amdgcn_readlane(lenv, bs - c0) : a.lens[bs]; };
+  auto seq_len = [&](int bs) -> int { return bs - c0 < 64 ? __builtin_amdgcn_readlane(lenv, bs - c0) : len_of(a, bs); };
 
   // Decode step with the append fused: the wave that reads a sequence's last
   // block writes the sequence's newest token there (position len - 1; not
@@ -350,7 +350,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       const int hq = hk * a.R + r % a.R, j = r / a.R;
-      const uint32_t *qp = reinterpret_cast<const uint32_t *>(a.q + (((int64_t)bq * a.Hq + hq) * a.Lq + j) * D);
+      const uint32_t *qp = reinterpret_cast<const uint32_t *>(q_row(a, bq, hq, j));
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) qv[r][c] = qp[16 * c + (lane & 15)];
     }
@@ -442,7 +442,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
 
     int lim[NR];
 #pragma unroll
-    for (int r = 0; r < NR; ++r) lim[r] = len - a.Lq + r / a.R + 1;
+    for (int r = 0; r < NR; ++r) lim[r] = key_limit(a, len, r / a.R);
 
     float m_run[NR], l_part[NR], c_part[NR][G], acc[NR][DPL];
 #pragma unroll
@@ -703,7 +703,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
 #pragma unroll
       for (int e2 = 0; e2 < DPL; ++e2) acc[r][e2] += cg;
     }
-    if (s >= i0 && e <= iend) {
+    if (!a.partial_only && s >= i0 && e <= iend) {
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
         const float inv = lsum[r] > 0.0f ? 1.0f / lsum[r] : 0.0f;

@@ -590,6 +590,109 @@ int32_t krill_decode_append_attention_rope(krill_pool_t pool, int32_t layer, con
                        dev_out, out_dtype, dev_ws, ws_bytes, stream, nt);
 }
 
+// Plans of the shared-prefix cascade's two passes and the workspace split.
+static int32_t plan_shared_prefix(krill_pool_t pool, int32_t B, int32_t Hq, int32_t prefix_blocks,
+                                  int32_t max_suffix_len, krill::AttnPlan *pp, krill::AttnPlan *sp,
+                                  size_t *suffix_off, size_t *total) {
+  if (B < 0 || prefix_blocks < 1 || max_suffix_len < 0) return fail(KRILL_E_INVAL, "bad B, prefix_blocks or length");
+  if ((int64_t)prefix_blocks * 64 > INT32_MAX / 2) return fail(KRILL_E_RANGE, "prefix of %d blocks", prefix_blocks);
+  int32_t r = krill::plan_attention(pool->geom, 1, Hq, std::max(B, 1), prefix_blocks * 64, pool->opt_split_blocks, 0,
+                                    pp);
+  if (r == 0)
+    r = krill::plan_attention(pool->geom, B, Hq, 1, max_suffix_len, pool->opt_split_blocks, pool->opt_path, sp);
+  if (r == -2) return fail(KRILL_E_UNSUPPORTED, "VALU path handles at most 8 query rows per KV head");
+  if (r != 0) return fail(KRILL_E_INVAL, "Hq %d not a multiple of %d KV heads, or bad B/length", Hq, pool->geom.Hkv);
+  *suffix_off = (pp->ws_bytes + 255) & ~(size_t)255;
+  *total = *suffix_off + sp->ws_bytes;
+  return KRILL_OK;
+}
+
+int32_t krill_shared_prefix_workspace_size(krill_pool_t pool, int32_t B, int32_t Hq, int32_t prefix_blocks,
+                                           int32_t max_suffix_len, size_t *bytes_out) {
+  krill::clear_error();
+  if (int32_t rc = check_pool(pool)) return rc;
+  if (!bytes_out) return fail(KRILL_E_INVAL, "bytes_out is NULL");
+  krill::AttnPlan pp, sp;
+  size_t off = 0, total = 0;
+  if (int32_t rc = plan_shared_prefix(pool, B, Hq, prefix_blocks, max_suffix_len, &pp, &sp, &off, &total)) return rc;
+  *bytes_out = total;
+  return KRILL_OK;
+}
+
+int32_t krill_decode_attention_shared_prefix(krill_pool_t pool, int32_t layer, const void *dev_q,
+                                             const int32_t *dev_prefix_table, int32_t prefix_blocks,
+                                             const int32_t *dev_suffix_tables, const int32_t *dev_suffix_lens,
+                                             int32_t B, int32_t max_blocks, int32_t max_suffix_len, int32_t Hq,
+                                             float scale, void *dev_out, int32_t out_dtype, void *dev_ws,
+                                             size_t ws_bytes, krill_stream_t stream) {
+  krill::clear_error();
+  if (int32_t rc = check_device_pool(pool, layer)) return rc;
+  if (B < 0 || max_blocks < 0 || max_suffix_len < 0) return fail(KRILL_E_INVAL, "negative B, max_blocks or length");
+  if (B == 0) return KRILL_OK;
+  if (!dev_q || !dev_prefix_table || !dev_suffix_tables || !dev_suffix_lens || !dev_out)
+    return fail(KRILL_E_INVAL, "NULL device pointer");
+  if (out_dtype != KRILL_DTYPE_F32 && out_dtype != KRILL_DTYPE_F16 && out_dtype != KRILL_DTYPE_BF16)
+    return fail(KRILL_E_INVAL, "out_dtype %d", out_dtype);
+  if (!std::isfinite(scale)) return fail(KRILL_E_INVAL, "scale is not finite");
+  if ((int64_t)max_blocks * 64 < (int64_t)max_suffix_len)
+    return fail(KRILL_E_RANGE, "max_suffix_len %d exceeds the %d-block table width", max_suffix_len, max_blocks);
+  krill::AttnPlan pp, sp;
+  size_t off = 0, total = 0;
+  if (int32_t rc = plan_shared_prefix(pool, B, Hq, prefix_blocks, max_suffix_len, &pp, &sp, &off, &total)) return rc;
+  if (ws_bytes < total || !dev_ws) return fail(KRILL_E_INVAL, "workspace of %zu bytes < %zu required", ws_bytes, total);
+  const int32_t od = out_dtype == KRILL_DTYPE_F32 ? krill::DT_F32 : out_dtype == KRILL_DTYPE_F16 ? krill::DT_F16
+                                                                                                : krill::DT_BF16;
+  const int64_t D = pool->geom.D;
+  // prefix pass: one sequence (the prefix blocks), the B sequences as its query positions
+  krill::AttnLaunch pa;
+  pa.q = dev_q;
+  pa.tables = dev_prefix_table;
+  pa.lens = dev_suffix_lens;  // not read: len_const
+  pa.B = 1;
+  pa.max_blocks = prefix_blocks;
+  pa.max_seq_len = prefix_blocks * 64;
+  pa.Hq = Hq;
+  pa.Lq = B;
+  pa.scale = scale;
+  pa.out = dev_out;
+  pa.out_dtype = od;
+  pa.ws = dev_ws;
+  pa.ws_bytes = off;
+  pa.split_blocks = pp.split_blocks;
+  pa.path = 0;
+  pa.q_strided = 1;  // q is [B][Hq][1][D]: query position j = sequence j
+  pa.q_sb = 0;
+  pa.q_sh = D;
+  pa.q_sj = (int64_t)Hq * D;
+  pa.len_const = prefix_blocks * 64;
+  pa.causal = 0;
+  pa.partial_only = 1;
+  // suffix pass: each sequence's own blocks
+  krill::AttnLaunch sa;
+  sa.q = dev_q;
+  sa.tables = dev_suffix_tables;
+  sa.lens = dev_suffix_lens;
+  sa.B = B;
+  sa.max_blocks = max_blocks;
+  sa.max_seq_len = max_suffix_len;
+  sa.Hq = Hq;
+  sa.Lq = 1;
+  sa.scale = scale;
+  sa.out = dev_out;
+  sa.out_dtype = od;
+  sa.ws = static_cast<uint8_t *>(dev_ws) + off;
+  sa.ws_bytes = ws_bytes - off;
+  sa.split_blocks = sp.split_blocks;
+  sa.path = pool->opt_path;
+  sa.partial_only = 1;
+  DeviceGuard dg(pool->device);
+  hipStream_t st = pick_stream(pool, stream);
+  if (int32_t rc = flush_pending(pool, st)) return rc;
+  hipError_t e = krill::launch_attention_shared_prefix(pool->geom, layer, pa, pp, sa, sp, st);
+  if (e != hipSuccess) return hip_fail(e, "shared-prefix attention launch");
+  return KRILL_OK;
+}
+
 int32_t krill_verify_attention(krill_pool_t pool, int32_t layer, const void *dev_q, int32_t Lq,
                                const int32_t *dev_block_tables, const int32_t *dev_seq_lens, int32_t B,
                                int32_t max_blocks, int32_t max_seq_len, int32_t Hq, float scale, void *dev_out,

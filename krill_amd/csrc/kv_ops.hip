@@ -593,6 +593,114 @@ __global__ __launch_bounds__(64) void k_attn_merge_flat(AttnArgs a) {
   merge_slots<D>(a, slot0, last - first + 1, rr, a.rows_per_group, obase);
 }
 
+// Shared-prefix cascade: sequence b's keys are the P shared prefix blocks
+// followed by its own suffix blocks.  The prefix pass attends every
+// sequence's query rows to the prefix once (one virtual sequence of length
+// 64 P whose query positions are the B sequences, no causal window), the
+// suffix pass each sequence to its suffix; both leave partials only.  This
+// kernel combines, per (row h, KV head, sequence b), the prefix pass's
+// partials of row b*R + h (one per wave of its split) with the suffix pass's
+// partials of row h -- the same softmax merge as k_attn_merge_flat, over two
+// lists of slots.
+struct MergeSrc {
+  const float *o, *ml;
+  int64_t slot0;
+  int n, rr, RR;
+};
+
+template <int D>
+__device__ __forceinline__ void merge_two(const MergeSrc (&src)[2], void *out, int64_t obase, int out_dtype) {
+  constexpr int E = D / 64;  // d = lane + 64 e
+  __shared__ float w_lds[64];
+  const int lane = threadIdx.x;
+  const int n = src[0].n + src[1].n;
+  auto part = [&](int k, const float **o, const float2 **ml) {
+    const int i = k < src[0].n ? 0 : 1;
+    const int64_t slot = src[i].slot0 + (i ? k - src[0].n : k);
+    const int64_t pi = slot * src[i].RR + src[i].rr;
+    *o = src[i].o + pi * D;
+    *ml = reinterpret_cast<const float2 *>(src[i].ml) + pi;
+  };
+  float M = -INFINITY;
+  for (int k0 = 0; k0 < n; k0 += 64)
+    if (k0 + lane < n) {
+      const float *o;
+      const float2 *ml;
+      part(k0 + lane, &o, &ml);
+      M = fmaxf(M, ml->x);
+    }
+  M = uniform_f32(wave_allmax(M));
+  float acc[E], lpart = 0.0f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] = 0.0f;
+  for (int k0 = 0; k0 < n; k0 += 64) {
+    const int cnt = min(64, n - k0);
+    float w = 0.0f;
+    if (lane < cnt) {
+      const float *o;
+      const float2 *ml;
+      part(k0 + lane, &o, &ml);
+      const float2 v = *ml;
+      w = v.x != -INFINITY ? fast_exp2(v.x - M) : 0.0f;
+      lpart += w * v.y;
+    }
+    w_lds[lane] = w;
+    __syncthreads();
+#pragma unroll 4
+    for (int k = 0; k < cnt; ++k) {
+      const float wk = w_lds[k];
+      const float *o;
+      const float2 *ml;
+      part(k0 + k, &o, &ml);
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] += wk * o[lane + 64 * e];
+    }
+    __syncthreads();
+  }
+  const float Lsum = uniform_f32(wave_allsum(lpart));
+  const float inv = (M == -INFINITY || !(Lsum > 0.0f)) ? 0.0f : 1.0f / Lsum;
+#pragma unroll
+  for (int e = 0; e < E; ++e) store_out(out, obase + lane + 64 * e, acc[e] * inv, out_dtype);
+}
+
+template <int D>
+__global__ __launch_bounds__(64) void k_attn_merge_cascade(AttnArgs ap, AttnArgs as) {
+  const int h = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  MergeSrc src[2];
+  // prefix pass: row b * R + h of the single virtual sequence, split over
+  // min(waves, P) waves (every row group reads all P blocks)
+  {
+    const int rp = b * ap.R + h;
+    const int rg = rp / ap.rows_per_group;
+    const int Tp = seq_blocks(ap, ap.len_const);
+    src[0].o = ap.ws_o;
+    src[0].ml = ap.ws_ml;
+    src[0].rr = rp % ap.rows_per_group;
+    src[0].RR = ap.rows_per_group;
+    src[0].slot0 = ((int64_t)hk * ap.row_groups + rg) * (ap.waves + 1);
+    src[0].n = Tp > 0 ? min(ap.waves, Tp) : 0;
+  }
+  // suffix pass: sequence b's waves, row h
+  {
+    const int rg = h / as.rows_per_group;
+    int s = 0, nb = 0;
+    const int T = flat_total_and_start(as, b, rg, s, nb);
+    src[1].o = as.ws_o;
+    src[1].ml = as.ws_ml;
+    src[1].rr = h % as.rows_per_group;
+    src[1].RR = as.rows_per_group;
+    src[1].n = 0;
+    src[1].slot0 = 0;
+    if (nb > 0) {
+      const int Wt = min(as.waves, T);
+      const int first = flat_wave_of(s, T, Wt), last = flat_wave_of(s + nb - 1, T, Wt);
+      src[1].slot0 = ((int64_t)hk * as.row_groups + rg) * (as.waves + as.B) + first + b;
+      src[1].n = last - first + 1;
+    }
+  }
+  merge_two<D>(src, as.out, out_row_base(as, b, hk, h, D), as.out_dtype);
+}
+
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
@@ -823,6 +931,23 @@ static hipError_t launch_append_newest(const PoolGeometry &g, int32_t layer, con
         k_append_newest<D, MODE_AFFINE, DT_F16><<<grid, block, 0, st>>>(args);
     }
   });
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_shared_prefix(const PoolGeometry &g, int32_t layer, const AttnLaunch &pa,
+                                         const AttnPlan &pp, const AttnLaunch &sa, const AttnPlan &sp,
+                                         hipStream_t st) {
+  if (sa.B == 0) return hipSuccess;
+  if (pa.B != 1 || pa.len_const < 0 || pa.causal || !pa.partial_only || !sa.partial_only || sa.Lq != 1 ||
+      pa.Lq != sa.B)
+    return hipErrorInvalidValue;
+  hipError_t e = pp.use_mfma ? launch_attn_mfma(g, layer, pa, pp, st) : launch_attn_valu(g, layer, pa, pp, st);
+  if (e != hipSuccess) return e;
+  e = sp.use_mfma ? launch_attn_mfma(g, layer, sa, sp, st) : launch_attn_valu(g, layer, sa, sp, st);
+  if (e != hipSuccess) return e;
+  const AttnArgs ap = make_attn_args(g, layer, pa, pp), as = make_attn_args(g, layer, sa, sp);
+  const dim3 grid((unsigned)ap.R, (unsigned)g.Hkv, (unsigned)sa.B);
+  KRILL_DISPATCH_D(g.D, { k_attn_merge_cascade<D><<<grid, dim3(64), 0, st>>>(ap, as); });
   return hipGetLastError();
 }
 

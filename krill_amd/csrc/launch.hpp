@@ -37,6 +37,14 @@ struct AttnLaunch {
   // RoPE of the queries and the newest K rows (null: none), table [max_pos][D]
   const float *rope_cs = nullptr;
   int32_t rope_max_pos = 0;
+  // views used by the shared-prefix cascade: q at element strides (q_strided),
+  // every sequence of length len_const (>= 0; lens unused), no causal window,
+  // partials only (no output, no merge launch)
+  int32_t q_strided = 0;
+  int64_t q_sb = 0, q_sh = 0, q_sj = 0;
+  int32_t len_const = -1;
+  int32_t causal = 1;
+  int32_t partial_only = 0;
 };
 
 // Splits/rows plan shared by the workspace query and the launch.
@@ -75,6 +83,13 @@ hipError_t launch_scatter(const PoolGeometry &g, int32_t layer, const void *keys
 hipError_t launch_copy_blocks(const PoolGeometry &g, const int32_t *src_dst, int32_t n, hipStream_t st);
 hipError_t launch_attention(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
                             hipStream_t st);
+// Shared-prefix cascade: the prefix pass (pa: one virtual sequence of the
+// prefix blocks, the B sequences as its query positions, non-causal, partials
+// only), the suffix pass (sa: decode over each sequence's own blocks,
+// partials only) and the merge of both into sa.out.
+hipError_t launch_attention_shared_prefix(const PoolGeometry &g, int32_t layer, const AttnLaunch &pa,
+                                         const AttnPlan &pp, const AttnLaunch &sa, const AttnPlan &sp,
+                                         hipStream_t st);
 
 // Resident waves per compute unit of the VALU decode kernel for (D, NR,
 // mode), from the runtime's occupancy query on a device pool, else the

@@ -358,6 +358,37 @@ class KVPool:
                                                    out.data_ptr(), code, ws.data_ptr(), ws.numel(), st))
         return out
 
+    def attention_shared_prefix(self, layer: int, q, prefix_table, suffix_tables, suffix_lens, max_suffix_len: int,
+                                scale: float, out_dtype=None, ws=None, out=None, stream=None):
+        """Decode attention of B sequences sharing the blocks prefix_table (int32
+        [P] device) before their own suffix blocks (suffix_tables [B, mb],
+        suffix_lens [B], tokens after the 64 P prefix tokens)."""
+        torch = _torch()
+        B, Hq, Lq, D = q.shape
+        if Lq != 1 or D != self.head_dim:
+            raise ValueError("q must be [B, Hq, 1, head_dim]")
+        self._check_dev("q", q, self.in_dtype)
+        self._check_dev("prefix_table", prefix_table, torch.int32)
+        Bt, mb = self._tables(suffix_tables, suffix_lens)
+        if Bt != B:
+            raise ValueError("q batch does not match the suffix tables")
+        P = int(prefix_table.numel())
+        out_dtype = torch.float32 if out_dtype is None else out_dtype
+        code = _dtype_code(out_dtype)
+        if out is None:
+            out = torch.empty((B, Hq, 1, D), dtype=out_dtype, device=q.device)
+        else:
+            self._check_dev("out", out, out_dtype, (B, Hq, 1, D))
+        need = ctypes.c_size_t()
+        L.check(L.lib().krill_shared_prefix_workspace_size(self._h, B, Hq, P, max_suffix_len, ctypes.byref(need)))
+        if ws is None or ws.numel() < need.value:
+            ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device=q.device)
+        L.check(L.lib().krill_decode_attention_shared_prefix(
+            self._h, layer, q.data_ptr(), prefix_table.data_ptr(), P, suffix_tables.data_ptr(), suffix_lens.data_ptr(),
+            B, mb, max_suffix_len, Hq, float(scale), out.data_ptr(), code, ws.data_ptr(), ws.numel(),
+            self._stream(stream)))
+        return out
+
     def decode_append_attention_rope(self, layer: int, q, k_new, v_new, tables, lens, max_seq_len: int,
                                      scale: float, cos_sin, out_dtype=None, ws=None, out=None, stream=None):
         """decode_append_attention with the queries and new K rows unrotated:

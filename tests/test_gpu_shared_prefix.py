@@ -1,0 +1,136 @@
+"""GPU: decode attention over a shared prefix (krill_decode_attention_shared_prefix).
+
+B sequences are forked from one prefix sequence (the reference's prefix-cache
+hit: every request of a batch starts from the same cached system prompt,
+PrefixCache.swift:161-170) and then each appends its own tokens.  The cascade
+attends the P full prefix blocks once for all B sequences and each suffix on
+its own; its output must match the oracle (2e-3 max-abs, as every attention
+test) and the ordinary decode attention over the whole tables: to float32
+reassociation when both run on the VALU kernel (at most 8 query rows per KV
+head in the prefix pass), to 1e-3 when the prefix pass runs on MFMA (bf16
+operands, the softmax weights rounded per block) and the single pass on VALU."""
+import numpy as np
+import pytest
+
+from kvutil import Filled, i32, oracle_attention, rand_bits, to_dev
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():  # pragma: no cover - CPU container
+    pytest.skip("no HIP device", allow_module_level=True)
+
+import krill_amd  # noqa: E402
+
+ATOL = 2e-3
+
+
+def _single_tol(B, R):
+    return 1e-5 if B * R <= 8 else 1e-3
+
+
+class _Joined(Filled):
+    """Prefix rows followed by each fork's own rows, as the oracle sees them."""
+
+    def __init__(self, pre: Filled, suf: Filled):
+        self.pool, self.dt, self.layers = pre.pool, pre.dt, pre.layers
+        self.seqs = suf.seqs
+        self.lens = [pre.lens[0] + T for T in suf.lens]
+        self.k = {l: [np.concatenate([pre.k[l][0], k], axis=1) for k in suf.k[l]] for l in self.layers}
+        self.v = {l: [np.concatenate([pre.v[l][0], v], axis=1) for v in suf.v[l]] for l in self.layers}
+
+
+def _case(mode, D, H, R, prefix_tokens, extra, dt="bf16", seed=0, split_blocks=0, out_dtype=None, path=0):
+    rng = np.random.default_rng(seed)
+    nb = (prefix_tokens + 63) // 64 + sum((prefix_tokens % 64 + T + 63) // 64 for T in extra) + 8
+    pool = krill_amd.KVPool(1, H, D, nb, mode, dt, free_list_seed=seed)
+    pool.set_option(krill_amd._lib.OPT_SPLIT_BLOCKS, split_blocks)
+    pool.set_option(krill_amd._lib.OPT_ATTN_PATH, path)
+    pre = Filled(pool, [prefix_tokens], rng, dt)
+    forks = [pool.seq_fork(pre.seqs[0], prefix_tokens) for _ in extra]
+    suf = Filled(pool, extra, rng, dt, seqs=forks)
+    joined = _Joined(pre, suf)
+    tables, lens, mb = joined.tables()
+    P = prefix_tokens // 64
+    t = tables.cpu().numpy()
+    assert (t[:, :P] == t[0, :P]).all()  # the forks share the prefix blocks
+    prefix_table = i32(t[0, :P])
+    suffix_tables = i32(np.ascontiguousarray(t[:, P:]) if mb > P else np.zeros((len(extra), 1), np.int32))
+    suffix_lens = lens - 64 * P
+    max_suffix = int(suffix_lens.max().item())
+    B = len(extra)
+    q = rand_bits(rng, (B, H * R, 1, D), dt)
+    scale = 1.0 / np.sqrt(D)
+    qd = to_dev(q, dt)
+    out = pool.attention_shared_prefix(0, qd, prefix_table, suffix_tables, suffix_lens, max_suffix, scale,
+                                       out_dtype)
+    whole = pool.attention(0, qd, tables, lens, max(joined.lens), scale, out_dtype)
+    torch.cuda.synchronize()
+    got, single = out.float().cpu().numpy(), whole.float().cpu().numpy()
+    ref = oracle_attention(pool, joined, 0, q, dt, scale)
+    pool.close()
+    return got, single, ref
+
+
+@pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
+@pytest.mark.parametrize("D,R,extra", [
+    (128, 5, [0, 1, 70, 300]),       # 20 prefix rows per KV head: MFMA prefix pass
+    (128, 2, [0, 5]),                # 4 rows: VALU prefix pass
+    (64, 4, [3, 64, 65, 0, 130]),    # 20 rows, D 64
+    (256, 2, [1, 2, 3, 4, 5, 6, 7, 8, 9, 10]),  # 20 rows in two 16-row groups (D 256)
+])
+def test_shared_prefix_matches_oracle_and_single_pass(mode, D, R, extra):
+    print(f"\ncase shared_prefix mode={mode} D={D} R={R} B={len(extra)}", flush=True)
+    for prefix_tokens in (200, 128):  # a shared partial block in every suffix, or none
+        got, single, ref = _case(mode, D, 2, R, prefix_tokens, extra, seed=D + R + prefix_tokens)
+        err = np.abs(got - ref).max()
+        assert err <= ATOL, f"prefix {prefix_tokens}: max abs error {err:.3e}"
+        dev = np.abs(got - single).max()
+        assert dev <= _single_tol(len(extra), R), f"prefix {prefix_tokens}: cascade vs single pass {dev:.3e}"
+
+
+@pytest.mark.parametrize("split_blocks", [1, 3])
+def test_shared_prefix_split_partials(split_blocks):
+    # one block per wave: the 1500-token prefix's 23 blocks over 23 waves
+    print(f"\ncase shared_prefix_split sb={split_blocks}", flush=True)
+    got, single, ref = _case("affine_g64", 128, 2, 5, 1500, [10, 0, 900], seed=7, split_blocks=split_blocks)
+    assert np.abs(got - ref).max() <= ATOL
+    assert np.abs(got - single).max() <= _single_tol(3, 5)
+
+
+def test_shared_prefix_qwen3_14b_shape():
+    """Hq 40, Hkv 8, D 128, affine g64: 8 sequences behind a 4096-token prefix."""
+    print("\ncase shared_prefix_qwen3_14b", flush=True)
+    rng = np.random.default_rng(11)
+    extra = [int(x) for x in rng.integers(1, 200, 8)]
+    got, single, ref = _case("affine_g64", 128, 8, 5, 4096, extra, seed=12)
+    assert np.abs(got - ref).max() <= ATOL
+    assert np.abs(got - single).max() <= _single_tol(8, 5)
+
+
+@pytest.mark.parametrize("out_dtype", ["bf16", "f16"])
+def test_shared_prefix_low_precision_output(out_dtype):
+    print(f"\ncase shared_prefix_out {out_dtype}", flush=True)
+    td = torch.bfloat16 if out_dtype == "bf16" else torch.float16
+    got, _, ref = _case("affine_g64", 128, 2, 5, 300, [7, 100], seed=9, out_dtype=td)
+    ulp = 2.0 ** -8 if out_dtype == "bf16" else 2.0 ** -11
+    err = np.abs(got - ref) - ulp * np.maximum(np.abs(ref), 1e-30)
+    assert err.max() <= ATOL
+
+
+def test_shared_prefix_rejects_empty_prefix_and_small_workspace():
+    print("\ncase shared_prefix_errors", flush=True)
+    pool = krill_amd.KVPool(1, 2, 128, 16, "affine_g64", "bf16", free_list_seed=1)
+    q = torch.zeros((2, 4, 1, 128), dtype=torch.bfloat16, device="cuda")
+    tabs = i32(np.zeros((2, 2), np.int32))
+    lens = i32([1, 1])
+    with pytest.raises(krill_amd._lib.KrillError, match="prefix_blocks"):
+        pool.attention_shared_prefix(0, q, i32(np.zeros(0, np.int32)), tabs, lens, 1, 0.1)
+    ws = torch.empty(16, dtype=torch.uint8, device="cuda")
+    out = torch.empty((2, 4, 1, 128), dtype=torch.float32, device="cuda")
+    L = krill_amd._lib
+    rc = L.lib().krill_decode_attention_shared_prefix(
+        pool._h, 0, q.data_ptr(), tabs.data_ptr(), 1, tabs.data_ptr(), lens.data_ptr(), 2, 2, 1, 4, 0.1,
+        out.data_ptr(), L.DTYPE_F32, ws.data_ptr(), ws.numel(), None)
+    assert rc == L.KRILL_E_INVAL and "workspace" in L.last_error()
+    pool.close()
