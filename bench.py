@@ -209,6 +209,7 @@ def _record(args, w, env, value, ms_step, config, roofline, extra, cpu=None):
         "config": config,
     }
     rec.update(extra)
+    rec["host_ms_per_step"] = round(getattr(env, "host_loop_ms", 0.0), 4)
     rec["roofline"] = roofline
     rec["cpu_baseline"] = cpu
     rec["pool"] = {k: stats[k] for k in ("cow_copies", "blocks_used", "blocks_shared", "evicted_entries",
@@ -228,6 +229,7 @@ def _timed(env, step, warmup, steps):
     for i in range(steps):
         step(warmup + i)
     t_end.record(env.stream)
+    env.host_loop_ms = (time.perf_counter() - wall0) * 1e3 / steps  # host side of a step (calls, table builds)
     t.cuda.synchronize()
     return t_start.elapsed_time(t_end) / steps, time.perf_counter() - wall0
 
@@ -342,9 +344,10 @@ def _decode_calls(env, seqs, st, max_len_final, Hq):
 
 
 def _cascade_calls(env, seqs, st, max_len_final, Hq, prefix_table):
-    """Per layer: quantize-append of the new token, then the shared-prefix
-    cascade (prefix pass over the P shared blocks for all B sequences, suffix
-    pass, merge)."""
+    """Per layer the shared-prefix cascade (prefix pass over the P shared
+    blocks for all B sequences, suffix pass, merge) with the new token's
+    append fused into the suffix pass (--unfused: quantize-append, then the
+    cascade)."""
     KL, lib, h, sp, w = env.KL, env.lib, env.h, env.sp, env.w
     B, Hkv, D, layers = len(seqs), w["Hkv"], w["D"], w["layers"]
     Pb = st.pb
@@ -367,11 +370,20 @@ def _cascade_calls(env, seqs, st, max_len_final, Hq, prefix_table):
             st.d_suffix_lens.data_ptr(), B, st.suffix_width, mx - 64 * Pb, Hq, scale, out.data_ptr(),
             KL.DTYPE_BF16, ws.data_ptr(), need.value, sp))
 
-    def step_layer(layer, mx):
-        KL.check(lib.krill_quantize_append(h, layer, kp[layer], vp[layer], st.d_slots.data_ptr(), B, 1, sp))
-        attend(layer, mx)
+    def fused(layer, mx):
+        KL.check(lib.krill_decode_append_attention_shared_prefix(
+            h, layer, qp[layer], kp[layer], vp[layer], Hkv * D, D, prefix_table.data_ptr(), Pb,
+            st.d_suffix_tables.data_ptr(), st.d_suffix_lens.data_ptr(), B, st.suffix_width, mx - 64 * Pb, Hq, scale,
+            out.data_ptr(), KL.DTYPE_BF16, ws.data_ptr(), need.value, sp))
 
-    return step_layer, attend, keep
+    def step_layer(layer, mx):
+        if env.args.unfused:
+            KL.check(lib.krill_quantize_append(h, layer, kp[layer], vp[layer], st.d_slots.data_ptr(), B, 1, sp))
+            attend(layer, mx)
+        else:
+            fused(layer, mx)
+
+    return step_layer, (attend if env.args.unfused else fused), keep
 
 
 def run_decode(args, w):
@@ -523,7 +535,7 @@ def run_shared_prefix(args, w):
             ps[b, 0] = one[0]
             cur_len[b] += 1
         env.KL.check(env.lib.krill_batch_tables(env.h, env.i32p(seqs_np), B, max_blocks, env.i32p(pt), env.i32p(pl)))
-        st.upload(j, slots=args.unfused or cascade)
+        st.upload(j, slots=args.unfused)
         mx = max(cur_len)
         for layer in range(layers):
             step_layer(layer, mx)
@@ -551,15 +563,19 @@ def run_shared_prefix(args, w):
                     f"with {stale_entries} unreferenced {stale_tokens}-token prefix entries; step = per layer "
                     "quantize-append 1 token/seq + paged decode attention"
                     + (f" as a cascade (the {Pb} full prefix blocks attended once for all {B} sequences, each "
-                       "suffix on its own, partials merged)" if cascade else
-                       " (two calls)" if args.unfused else " (one fused call)"),
+                       "suffix on its own, partials merged)" if cascade else "")
+                    + (" (two calls)" if args.unfused else " (one fused call)"),
         "layers": layers, "Hq": Hq, "Hkv": Hkv, "head_dim": D, "batch": B, "quant": args.quant,
         "prefix": P, "cascade": cascade, "suffix_mean": float(np.mean(suffix)), "num_blocks": num_blocks,
     }
+    if cascade:
+        call_name = "shared-prefix cascade call (prefix pass + suffix pass + merge" + (
+            ")" if args.unfused else ", append fused)")
+    else:
+        call_name = "paged decode attention call" if args.unfused else "fused append + paged decode attention call"
     roofline = {
         "bound": "hbm",
-        "kernel": ("shared-prefix cascade call (prefix pass + suffix pass + merge), one layer" if cascade else
-                   "fused append + paged decode attention call, one layer") + "; unique bytes (shared prefix once)",
+        "kernel": call_name + ", one layer; unique bytes (shared prefix once)",
         "achieved": round(uniq_launch / (attn_ms * 1e-3) / 1e9, 2),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",

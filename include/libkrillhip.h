@@ -305,6 +305,21 @@ int32_t krill_decode_attention_shared_prefix(krill_pool_t pool, int32_t layer, c
                                              int32_t B, int32_t max_blocks, int32_t max_suffix_len, int32_t Hq,
                                              float scale, void *dev_out, int32_t out_dtype, void *dev_ws,
                                              size_t ws_bytes, krill_stream_t stream);
+/* The same with the step's append fused, as krill_decode_append_attention
+ * does for the single-pass decode: sequence b's new token (rows at
+ * dev_k_new / dev_v_new + b * stride_b + h * stride_h) is quantized into its
+ * suffix at position dev_suffix_lens[b] - 1 (slot reserved beforehand) and
+ * attended over in the same launches; byte for byte the same cache and
+ * output as krill_quantize_append followed by
+ * krill_decode_attention_shared_prefix. */
+int32_t krill_decode_append_attention_shared_prefix(krill_pool_t pool, int32_t layer, const void *dev_q,
+                                                    const void *dev_k_new, const void *dev_v_new, int64_t stride_b,
+                                                    int64_t stride_h, const int32_t *dev_prefix_table,
+                                                    int32_t prefix_blocks, const int32_t *dev_suffix_tables,
+                                                    const int32_t *dev_suffix_lens, int32_t B, int32_t max_blocks,
+                                                    int32_t max_suffix_len, int32_t Hq, float scale, void *dev_out,
+                                                    int32_t out_dtype, void *dev_ws, size_t ws_bytes,
+                                                    krill_stream_t stream);
 /* Speculative-verify / chunked-prefill attention: Lq new query rows per
  * sequence, already appended, causal inside the window (row j sees tokens
  * [0, len - Lq + j]; BatchedDecode.swift:299-312, LlamaModel.swift:186-202).

@@ -619,13 +619,12 @@ int32_t krill_shared_prefix_workspace_size(krill_pool_t pool, int32_t B, int32_t
   return KRILL_OK;
 }
 
-int32_t krill_decode_attention_shared_prefix(krill_pool_t pool, int32_t layer, const void *dev_q,
-                                             const int32_t *dev_prefix_table, int32_t prefix_blocks,
-                                             const int32_t *dev_suffix_tables, const int32_t *dev_suffix_lens,
-                                             int32_t B, int32_t max_blocks, int32_t max_suffix_len, int32_t Hq,
-                                             float scale, void *dev_out, int32_t out_dtype, void *dev_ws,
-                                             size_t ws_bytes, krill_stream_t stream) {
-  krill::clear_error();
+static int32_t run_shared_prefix(krill_pool_t pool, int32_t layer, const void *dev_q,
+                                 const int32_t *dev_prefix_table, int32_t prefix_blocks,
+                                 const int32_t *dev_suffix_tables, const int32_t *dev_suffix_lens, int32_t B,
+                                 int32_t max_blocks, int32_t max_suffix_len, int32_t Hq, float scale, void *dev_out,
+                                 int32_t out_dtype, void *dev_ws, size_t ws_bytes, krill_stream_t stream,
+                                 const NewTokens &nt) {
   if (int32_t rc = check_device_pool(pool, layer)) return rc;
   if (B < 0 || max_blocks < 0 || max_suffix_len < 0) return fail(KRILL_E_INVAL, "negative B, max_blocks or length");
   if (B == 0) return KRILL_OK;
@@ -685,12 +684,48 @@ int32_t krill_decode_attention_shared_prefix(krill_pool_t pool, int32_t layer, c
   sa.split_blocks = sp.split_blocks;
   sa.path = pool->opt_path;
   sa.partial_only = 1;
+  sa.k_new = nt.k;  // the newest token sits in the suffix blocks
+  sa.v_new = nt.v;
+  sa.kn_sb = nt.sb;
+  sa.kn_sh = nt.sh;
   DeviceGuard dg(pool->device);
   hipStream_t st = pick_stream(pool, stream);
   if (int32_t rc = flush_pending(pool, st)) return rc;
   hipError_t e = krill::launch_attention_shared_prefix(pool->geom, layer, pa, pp, sa, sp, st);
   if (e != hipSuccess) return hip_fail(e, "shared-prefix attention launch");
   return KRILL_OK;
+}
+
+int32_t krill_decode_attention_shared_prefix(krill_pool_t pool, int32_t layer, const void *dev_q,
+                                             const int32_t *dev_prefix_table, int32_t prefix_blocks,
+                                             const int32_t *dev_suffix_tables, const int32_t *dev_suffix_lens,
+                                             int32_t B, int32_t max_blocks, int32_t max_suffix_len, int32_t Hq,
+                                             float scale, void *dev_out, int32_t out_dtype, void *dev_ws,
+                                             size_t ws_bytes, krill_stream_t stream) {
+  krill::clear_error();
+  return run_shared_prefix(pool, layer, dev_q, dev_prefix_table, prefix_blocks, dev_suffix_tables, dev_suffix_lens, B,
+                           max_blocks, max_suffix_len, Hq, scale, dev_out, out_dtype, dev_ws, ws_bytes, stream,
+                           NewTokens());
+}
+
+int32_t krill_decode_append_attention_shared_prefix(krill_pool_t pool, int32_t layer, const void *dev_q,
+                                                    const void *dev_k_new, const void *dev_v_new, int64_t stride_b,
+                                                    int64_t stride_h, const int32_t *dev_prefix_table,
+                                                    int32_t prefix_blocks, const int32_t *dev_suffix_tables,
+                                                    const int32_t *dev_suffix_lens, int32_t B, int32_t max_blocks,
+                                                    int32_t max_suffix_len, int32_t Hq, float scale, void *dev_out,
+                                                    int32_t out_dtype, void *dev_ws, size_t ws_bytes,
+                                                    krill_stream_t stream) {
+  krill::clear_error();
+  if (B > 0 && (!dev_k_new || !dev_v_new)) return fail(KRILL_E_INVAL, "NULL new K/V pointer");
+  if (stride_b < 0 || stride_h < 0) return fail(KRILL_E_INVAL, "negative new-row stride");
+  NewTokens nt;
+  nt.k = dev_k_new;
+  nt.v = dev_v_new;
+  nt.sb = stride_b;
+  nt.sh = stride_h;
+  return run_shared_prefix(pool, layer, dev_q, dev_prefix_table, prefix_blocks, dev_suffix_tables, dev_suffix_lens, B,
+                           max_blocks, max_suffix_len, Hq, scale, dev_out, out_dtype, dev_ws, ws_bytes, stream, nt);
 }
 
 int32_t krill_verify_attention(krill_pool_t pool, int32_t layer, const void *dev_q, int32_t Lq,

@@ -943,6 +943,10 @@ hipError_t launch_attention_shared_prefix(const PoolGeometry &g, int32_t layer, 
     return hipErrorInvalidValue;
   hipError_t e = pp.use_mfma ? launch_attn_mfma(g, layer, pa, pp, st) : launch_attn_valu(g, layer, pa, pp, st);
   if (e != hipSuccess) return e;
+  if (sa.k_new && sp.use_mfma) {  // the newest tokens (in the suffix blocks) before the MFMA suffix pass
+    e = launch_append_newest(g, layer, sa, sp, st);
+    if (e != hipSuccess) return e;
+  }
   e = sp.use_mfma ? launch_attn_mfma(g, layer, sa, sp, st) : launch_attn_valu(g, layer, sa, sp, st);
   if (e != hipSuccess) return e;
   const AttnArgs ap = make_attn_args(g, layer, pa, pp), as = make_attn_args(g, layer, sa, sp);

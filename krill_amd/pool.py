@@ -359,10 +359,13 @@ class KVPool:
         return out
 
     def attention_shared_prefix(self, layer: int, q, prefix_table, suffix_tables, suffix_lens, max_suffix_len: int,
-                                scale: float, out_dtype=None, ws=None, out=None, stream=None):
+                                scale: float, out_dtype=None, ws=None, out=None, stream=None, k_new=None,
+                                v_new=None):
         """Decode attention of B sequences sharing the blocks prefix_table (int32
         [P] device) before their own suffix blocks (suffix_tables [B, mb],
-        suffix_lens [B], tokens after the 64 P prefix tokens)."""
+        suffix_lens [B], tokens after the 64 P prefix tokens).  With k_new /
+        v_new ([B, Hkv, 1, D]) the step's new token is appended in the same
+        launches at suffix position suffix_lens[b] - 1."""
         torch = _torch()
         B, Hq, Lq, D = q.shape
         if Lq != 1 or D != self.head_dim:
@@ -383,10 +386,19 @@ class KVPool:
         L.check(L.lib().krill_shared_prefix_workspace_size(self._h, B, Hq, P, max_suffix_len, ctypes.byref(need)))
         if ws is None or ws.numel() < need.value:
             ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device=q.device)
-        L.check(L.lib().krill_decode_attention_shared_prefix(
-            self._h, layer, q.data_ptr(), prefix_table.data_ptr(), P, suffix_tables.data_ptr(), suffix_lens.data_ptr(),
-            B, mb, max_suffix_len, Hq, float(scale), out.data_ptr(), code, ws.data_ptr(), ws.numel(),
-            self._stream(stream)))
+        if k_new is None:
+            L.check(L.lib().krill_decode_attention_shared_prefix(
+                self._h, layer, q.data_ptr(), prefix_table.data_ptr(), P, suffix_tables.data_ptr(),
+                suffix_lens.data_ptr(), B, mb, max_suffix_len, Hq, float(scale), out.data_ptr(), code, ws.data_ptr(),
+                ws.numel(), self._stream(stream)))
+            return out
+        H = self.num_kv_heads
+        self._check_dev("k_new", k_new, self.in_dtype, (B, H, 1, D))
+        self._check_dev("v_new", v_new, self.in_dtype, (B, H, 1, D))
+        L.check(L.lib().krill_decode_append_attention_shared_prefix(
+            self._h, layer, q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), H * D, D, prefix_table.data_ptr(), P,
+            suffix_tables.data_ptr(), suffix_lens.data_ptr(), B, mb, max_suffix_len, Hq, float(scale),
+            out.data_ptr(), code, ws.data_ptr(), ws.numel(), self._stream(stream)))
         return out
 
     def decode_append_attention_rope(self, layer: int, q, k_new, v_new, tables, lens, max_seq_len: int,

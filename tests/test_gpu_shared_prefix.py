@@ -40,16 +40,28 @@ class _Joined(Filled):
         self.v = {l: [np.concatenate([pre.v[l][0], v], axis=1) for v in suf.v[l]] for l in self.layers}
 
 
-def _case(mode, D, H, R, prefix_tokens, extra, dt="bf16", seed=0, split_blocks=0, out_dtype=None, path=0):
+def _forked(mode, D, H, prefix_tokens, extra, dt, seed, split_blocks=0, path=0):
+    """A pool holding one prefix sequence and len(extra) forks of it, fork b
+    with extra[b] tokens of its own."""
     rng = np.random.default_rng(seed)
-    nb = (prefix_tokens + 63) // 64 + sum((prefix_tokens % 64 + T + 63) // 64 for T in extra) + 8
+    nb = (prefix_tokens + 63) // 64 + sum((prefix_tokens % 64 + T + 64) // 64 for T in extra) + 8
     pool = krill_amd.KVPool(1, H, D, nb, mode, dt, free_list_seed=seed)
     pool.set_option(krill_amd._lib.OPT_SPLIT_BLOCKS, split_blocks)
     pool.set_option(krill_amd._lib.OPT_ATTN_PATH, path)
     pre = Filled(pool, [prefix_tokens], rng, dt)
     forks = [pool.seq_fork(pre.seqs[0], prefix_tokens) for _ in extra]
     suf = Filled(pool, extra, rng, dt, seqs=forks)
-    joined = _Joined(pre, suf)
+    return pool, rng, _Joined(pre, suf)
+
+
+def _split_tables(pool, seqs, P, mb):
+    t, n = pool.batch_tables(seqs, mb)
+    assert (t[:, :P] == t[0, :P]).all()  # the forks share the prefix blocks
+    return i32(t[0, :P]), i32(np.ascontiguousarray(t[:, P:])), i32(n - 64 * P), int(n.max()) - 64 * P
+
+
+def _case(mode, D, H, R, prefix_tokens, extra, dt="bf16", seed=0, split_blocks=0, out_dtype=None, path=0):
+    pool, rng, joined = _forked(mode, D, H, prefix_tokens, extra, dt, seed, split_blocks, path)
     tables, lens, mb = joined.tables()
     P = prefix_tokens // 64
     t = tables.cpu().numpy()
@@ -134,3 +146,36 @@ def test_shared_prefix_rejects_empty_prefix_and_small_workspace():
         out.data_ptr(), L.DTYPE_F32, ws.data_ptr(), ws.numel(), None)
     assert rc == L.KRILL_E_INVAL and "workspace" in L.last_error()
     pool.close()
+
+
+@pytest.mark.parametrize("path", [0, 2])
+def test_shared_prefix_fused_append_bit_identical(path):
+    """The append fused into the cascade (VALU suffix pass, or the MFMA one
+    after its own append launch) leaves the same cache bytes and output as
+    quantize-append followed by the cascade."""
+    print(f"\ncase shared_prefix_fused_append path={path}", flush=True)
+    D, H, R, prefix_tokens, extra = 128, 2, 5, 200, [0, 3, 64, 130]
+    P, B = prefix_tokens // 64, len(extra)
+    mb = (prefix_tokens + max(extra) + 1 + 63) // 64
+    outs, snaps = [], []
+    for fused in (False, True):
+        pool, _, joined = _forked("affine_g64", D, H, prefix_tokens, extra, "bf16", seed=31, path=path)
+        rng = np.random.default_rng(99)
+        kn, vn = (to_dev(rand_bits(rng, (B, H, 1, D), "bf16"), "bf16") for _ in range(2))
+        q = to_dev(rand_bits(rng, (B, H * R, 1, D), "bf16"), "bf16")
+        slots = np.stack([pool.reserve_append(s, 1) for s in joined.seqs]).astype(np.int32)
+        ptab, stab, slen, smax = _split_tables(pool, joined.seqs, P, mb)
+        if fused:
+            out = pool.attention_shared_prefix(0, q, ptab, stab, slen, smax, 0.1, k_new=kn, v_new=vn)
+        else:
+            pool.quantize_append(0, kn, vn, i32(slots))
+            out = pool.attention_shared_prefix(0, q, ptab, stab, slen, smax, 0.1)
+        t, n = pool.batch_tables(joined.seqs, mb)
+        snap = pool.gather(0, i32(t), i32(n), int(n.max()))
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+        snaps.append({k: v.cpu().numpy() for k, v in snap.items()})
+        pool.close()
+    assert torch.equal(outs[0], outs[1])
+    for k in snaps[0]:
+        assert np.array_equal(snaps[0][k].view(np.uint8), snaps[1][k].view(np.uint8)), k
