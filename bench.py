@@ -26,6 +26,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import gc
 import json
 import math
 import os
@@ -52,6 +53,10 @@ WORKLOADS = {
                                          hi=1024, prefix=4096 + 24),
     "llama-3-8b-verify-b16": dict(kind="verify", layers=32, Hq=32, Hkv=8, D=128, B=16, lo=1024, hi=8192,
                                   draft=8),
+    # the default decode workload with one request leaving and one joining (prompt U[512, 8192],
+    # its K/V appended into a fresh sequence) at every step, no epoch restack
+    "qwen3-14b-b32-continuous": dict(kind="continuous", layers=40, Hq=40, Hkv=8, D=128, B=32, lo=512, hi=8192,
+                                     churn=1),
 }
 
 
@@ -187,7 +192,8 @@ def main():
         torch.cuda.synchronize()
         del x, y
     w = WORKLOADS[args.workload]
-    rec = {"decode": run_decode, "verify": run_verify, "shared_prefix": run_shared_prefix}[w["kind"]](args, w)
+    rec = {"decode": run_decode, "verify": run_verify, "shared_prefix": run_shared_prefix,
+           "continuous": run_continuous}[w["kind"]](args, w)
     print(json.dumps(rec))
 
 
@@ -222,6 +228,18 @@ def _timed(env, step, warmup, steps):
     for i in range(warmup):
         step(i)
     t.cuda.synchronize()
+    # no collector pass inside the timed steps: a full pass over the interpreter's
+    # objects stalls the host for tens of ms, which a native batcher never does
+    gc.collect()
+    gc.disable()
+    try:
+        return _timed_steps(env, step, warmup, steps)
+    finally:
+        gc.enable()
+
+
+def _timed_steps(env, step, warmup, steps):
+    t = env.torch
     t_start = t.cuda.Event(enable_timing=True)
     t_end = t.cuda.Event(enable_timing=True)
     wall0 = time.perf_counter()
@@ -470,6 +488,148 @@ def run_decode(args, w):
              "step_bytes": int(step_bytes), "wall_s_timed": round(wall, 4)}
     rec = _record(args, w, env, gbs_step, ms_step, config, roofline, extra, cpu)
     del keep
+    env.pool.close()
+    return rec
+
+
+def run_continuous(args, w):
+    """Continuous batching without epochs: at every step `churn` rows leave
+    (their blocks freed) and as many requests join, each with its prompt's
+    K/V (prefilled by the caller's model) appended into a fresh sequence; then
+    one fused decode step of all B rows.  The running rows are never copied.
+    The reference batcher instead restacks every row's cache left-padded when
+    the active set changes and scatters it back after the epoch; both copies
+    are timed on the same pool after the steps for comparison."""
+    t = None
+    layers, Hq, Hkv, D, B, churn = w["layers"], w["Hq"], w["Hkv"], w["D"], w["B"], w["churn"]
+    rng = np.random.default_rng(args.seed)
+    lens0 = rng.integers(w["lo"], w["hi"] + 1, size=B).astype(np.int64)
+    total_steps = args.warmup + args.steps + 1
+    new_lens = rng.integers(w["lo"], w["hi"] + 1, size=total_steps * churn).astype(np.int64)
+    leave = rng.integers(0, B, size=total_steps * churn)
+    max_len_final = w["hi"] + total_steps
+    max_blocks = (max_len_final + 63) // 64
+    num_blocks = B * (max_blocks + 1) + 64
+    env = Env(args, w, num_blocks)
+    t = env.torch
+    seqs = [env.pool.seq_create() for _ in range(B)]
+    env.fill(seqs, [int(x) for x in lens0])
+    st = StepTables(env, B, max_blocks, 1)
+    step_layer, call_only, keep = _decode_calls(env, seqs, st, max_len_final, Hq)
+    # prompt K/V of the joining requests (the same random rows for every one; the bytes are what count)
+    Tp = w["hi"]
+    kp = env.randn_bf16((1, Hkv, Tp, D))
+    vp = env.randn_bf16((1, Hkv, Tp, D))
+    strides = (Hkv * Tp * D, Tp * D, D)
+    ring = [t.empty((churn, Tp), dtype=t.int32).pin_memory() for _ in range(3)]
+    d_new = t.empty((churn, Tp), dtype=t.int32, device=env.dev)
+    cur_len = [int(x) for x in lens0]
+    one = np.empty(1, np.int32)
+    joined_tokens = [0]
+
+    def step(i):
+        j, ps, pt, pl = st.host(i)
+        ns = ring[j].numpy()
+        news = []
+        for c in range(churn):
+            r = int(leave[i * churn + c])
+            env.KL.check(env.lib.krill_seq_free(env.h, seqs[r]))
+            sid = ctypes.c_int32()
+            env.KL.check(env.lib.krill_seq_create(env.h, ctypes.byref(sid)))
+            T = int(new_lens[i * churn + c])
+            env.KL.check(env.lib.krill_seq_reserve_append(env.h, sid.value, T, env.i32p(ns[c])))
+            seqs[r] = sid.value
+            cur_len[r] = T
+            news.append(T)
+            joined_tokens[0] += T
+        d_new.copy_(ring[j], non_blocking=True)
+        for b in range(B):
+            env.KL.check(env.lib.krill_seq_reserve_append(env.h, seqs[b], 1, env.i32p(one)))
+            ps[b, 0] = one[0]
+            cur_len[b] += 1
+        seqs_np = np.array(seqs, np.int32)
+        env.KL.check(env.lib.krill_batch_tables(env.h, env.i32p(seqs_np), B, max_blocks, env.i32p(pt), env.i32p(pl)))
+        st.upload(j, slots=args.unfused)
+        mx = max(cur_len)
+        for layer in range(layers):
+            for c, T in enumerate(news):  # the joining requests' prompts, then the batch's decode
+                env.KL.check(env.lib.krill_quantize_append_strided(
+                    env.h, layer, kp.data_ptr(), vp.data_ptr(), *strides, d_new[c].data_ptr(), 1, T, env.sp))
+            step_layer(layer, mx)
+
+    for i in range(args.warmup):
+        step(i)
+    t.cuda.synchronize()
+    lens_start = list(cur_len)
+    j0 = joined_tokens[0]
+    ms_step, wall = _timed(env, lambda i: step(args.warmup + i), 0, args.steps)
+    per_tok = env.per_tok
+    joined = (joined_tokens[0] - j0) / args.steps  # prompt tokens appended per step
+    # decode bytes: each row's cache at the step (rows replaced mid-run counted at their new length)
+    avg_ctx = sum((a + b_) / 2.0 for a, b_ in zip(lens_start, cur_len))
+    qo_layer = B * Hq * D * 2 * 2
+    step_bytes = layers * (avg_ctx * per_tok + qo_layer + joined * (2 * Hkv * D * 2 + per_tok)
+                           + B * (2 * Hkv * D * 2 + per_tok))
+    gbs_step = step_bytes / (ms_step * 1e-3) / 1e9
+    mx = max(cur_len)
+    attn_ms = _time_calls(env, lambda layer: call_only(layer, mx), args.kernel_reps)
+    launch_bytes = sum(cur_len) * per_tok + qo_layer + B * (2 * Hkv * D * 2 + per_tok)
+
+    # the reference's epoch copies on this batch: stack every row left-padded, scatter it back
+    tabs, lns = env.pool.batch_tables(seqs, max_blocks)
+    S = int(lns.max())
+    d_tabs = t.from_numpy(np.ascontiguousarray(tabs)).to(env.dev)
+    d_lns = t.from_numpy(np.ascontiguousarray(lns)).to(env.dev)
+    tok = np.arange(S)
+    slot_map = np.where(tok[None, :] < lns[:, None],
+                        np.take_along_axis(tabs, np.minimum(tok[None, :] // 64, max_blocks - 1).repeat(B, 0), 1) * 64
+                        + tok[None, :] % 64, -1).astype(np.int32)
+    d_slots = t.from_numpy(slot_map).to(env.dev)
+    d_start = t.from_numpy((S - lns).astype(np.int32)).to(env.dev)
+    snap = env.pool.gather(0, d_tabs, d_lns, S, left_pad=True, stream=env.stream)
+    t.cuda.synchronize()
+    e = [t.cuda.Event(enable_timing=True) for _ in range(3)]
+    reps = 3
+    e[0].record(env.stream)
+    for _ in range(reps):
+        env.pool.gather(0, d_tabs, d_lns, S, left_pad=True, stream=env.stream)
+    e[1].record(env.stream)
+    for _ in range(reps):
+        env.pool.scatter(0, snap, d_start, d_slots, stream=env.stream)
+    e[2].record(env.stream)
+    t.cuda.synchronize()
+    gather_ms, scatter_ms = e[0].elapsed_time(e[1]) / reps, e[1].elapsed_time(e[2]) / reps
+    stack_bytes = 2 * int(lns.sum()) * per_tok  # read + write of every row's cache
+
+    config = {
+        "workload": f"{args.workload}: {layers} layers, Hq {Hq}, Hkv {Hkv}, D {D}, B {B}, context "
+                    f"U[{w['lo']},{w['hi']}], {churn} request(s) leaving and joining per step (prompt "
+                    f"U[{w['lo']},{w['hi']}] tokens of K/V appended into a fresh sequence), {args.quant} int8; "
+                    "step = the joining prompts' appends + per layer one fused append + decode attention call "
+                    "over all rows (no restack)",
+        "layers": layers, "Hq": Hq, "Hkv": Hkv, "head_dim": D, "batch": B, "quant": args.quant, "churn": churn,
+        "num_blocks": num_blocks,
+    }
+    roofline = {
+        "bound": "hbm",
+        "kernel": "fused append + paged decode attention call (k_attn_valu + k_attn_merge_flat), one layer",
+        "achieved": round(launch_bytes / (attn_ms * 1e-3) / 1e9, 2),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(launch_bytes / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "bytes_per_launch": int(launch_bytes),
+        "avg_launch_ms": round(attn_ms, 5),
+    }
+    extra = {"tokens_per_s": round(B / (ms_step * 1e-3), 1), "hbm_frac_step": round(gbs_step / HBM_PEAK_GBS, 4),
+             "prompt_tokens_joined_per_step": joined, "wall_s_timed": round(wall, 4),
+             "epoch_restack": {"gather_left_padded_ms_per_layer": round(gather_ms, 4),
+                               "scatter_back_ms_per_layer": round(scatter_ms, 4),
+                               "ms_per_change_all_layers": round((gather_ms + scatter_ms) * layers, 3),
+                               "gbs": round(stack_bytes / ((gather_ms + scatter_ms) * 1e-3) / 1e9, 1),
+                               "rows_tokens": int(lns.sum())}}
+    rec = _record(args, w, env, gbs_step, ms_step, config, roofline, extra)
+    del keep, snap
     env.pool.close()
     return rec
 

@@ -203,8 +203,9 @@ class KVPool:
     # ---------------------------------------------------------- kernels
     @staticmethod
     def _stream(stream=None):
+        """hipStream_t for a torch stream, a raw handle (int) or None (torch's current stream)."""
         if stream is not None:
-            return ctypes.c_void_p(stream)
+            return ctypes.c_void_p(getattr(stream, "cuda_stream", stream))
         torch = _torch()
         if torch.cuda.is_available():
             return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
