@@ -348,38 +348,97 @@ __device__ __forceinline__ bool resolve_token(const int32_t *tables, const int32
   return true;
 }
 
+// One workgroup per (token block, head, sequence): the block's K chunks go
+// out as 16-byte pieces (token t, d 16c..16c+15: contiguous in the pool's
+// chunk-major K and in the output row), V goes through LDS (the pool holds it
+// transposed), metadata as (scale, zero) words.  Rows that no token of the
+// block lands on are left to the zero workgroups (blockIdx.x >= nbx), which
+// clear every output row outside the sequence's token range.  A block whose
+// table entry is out of range (or beyond max_blocks) gives zero rows, as a
+// row gather would.
 template <int D, int G>
 __global__ __launch_bounds__(256) void k_gather(LayerView lv, const int32_t *__restrict__ tables,
-                                                const int32_t *__restrict__ lens, int32_t B, int32_t H,
-                                                int32_t max_blocks, int32_t S_out, int32_t left_pad,
-                                                uint8_t *keys, uint8_t *values, uint16_t *ks, uint16_t *kz,
-                                                uint16_t *vs, uint16_t *vz) {
-  constexpr int E = D / 64;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= (int64_t)B * H * S_out) return;
-  const int s = (int)(row % S_out);
-  const int h = (int)((row / S_out) % H);
-  const int b = (int)(row / ((int64_t)S_out * H));
-  int blk = 0, t = 0;
-  const bool valid = resolve_token(tables, lens, b, max_blocks, lv.num_blocks, S_out, left_pad, s, &blk, &t);
-  const uint8_t *reg = head_region(lv, blk, h);
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int d = lane * E + e;
-    keys[row * D + d] = valid ? reg[k_byte(t, d)] : (uint8_t)0;
-    values[row * D + d] = valid ? reg[v_byte(D, t, d)] : (uint8_t)0;
+                                                const int32_t *__restrict__ lens, int32_t H, int32_t max_blocks,
+                                                int32_t S_out, int32_t left_pad, int32_t nbx, uint8_t *keys,
+                                                uint8_t *values, uint16_t *ks, uint16_t *kz, uint16_t *vs,
+                                                uint16_t *vz) {
+  constexpr int CH = D / 16;  // 16-byte pieces per row
+  constexpr int VB = 64 * D;  // V bytes of one (block, head)
+  __shared__ __attribute__((aligned(16))) uint8_t vl[VB];
+  const int x = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int len = lens[b];
+  const int off = left_pad ? S_out - len : 0;  // output row of token ti: ti + off
+  const int t_lo = max(0, -off), t_hi = min(len, S_out - off);
+  const int64_t row0 = ((int64_t)b * H + h) * S_out;  // first output row of (b, h)
+  const uint4 zero4 = {0u, 0u, 0u, 0u};
+  if (x >= nbx) {  // zero rows: output rows with no token
+    const int s0 = (x - nbx) * 64;
+    for (int p = tid; p < 64 * CH; p += 256) {
+      const int s = s0 + p / CH, c = p % CH;
+      const int ti = s - off;
+      if (s < S_out && (ti < t_lo || ti >= t_hi)) {
+        *reinterpret_cast<uint4 *>(keys + (row0 + s) * D + 16 * c) = zero4;
+        *reinterpret_cast<uint4 *>(values + (row0 + s) * D + 16 * c) = zero4;
+      }
+    }
+    for (int p = tid; p < 64 * G; p += 256) {
+      const int s = s0 + p / G, g = p % G;
+      const int ti = s - off;
+      if (s < S_out && (ti < t_lo || ti >= t_hi)) {
+        const int64_t m = (row0 + s) * G + g;
+        ks[m] = kz[m] = vs[m] = vz[m] = 0;
+      }
+    }
+    return;
   }
-  if (lane < G) {
+  if (t_hi <= t_lo) return;
+  const int j = (t_lo >> 6) + x;  // token block of this workgroup
+  const int ta = max(64 * j, t_lo), tb = min(64 * j + 64, t_hi);
+  if (ta >= tb) return;
+  const int blk = j < max_blocks ? tables[(int64_t)b * max_blocks + j] : -1;
+  const bool valid = (unsigned)blk < (unsigned)lv.num_blocks;  // uniform over the workgroup
+  const uint8_t *reg = valid ? head_region(lv, blk, h) : nullptr;
+  if (valid) {  // V region into LDS, 16 bytes per thread and step
+    for (int p = tid; p < VB / 16; p += 256)
+      *reinterpret_cast<uint4 *>(vl + 16 * p) = *reinterpret_cast<const uint4 *>(reg + v_offset(D) + 16 * p);
+  }
+  __syncthreads();
+  for (int p = tid; p < 64 * CH; p += 256) {
+    const int t = p / CH, c = p % CH;
+    const int ti = 64 * j + t;
+    if (ti < ta || ti >= tb) continue;
+    const int64_t o = (row0 + ti + off) * D + 16 * c;
+    uint4 kq = zero4, vq = zero4;
+    if (valid) {
+      kq = *reinterpret_cast<const uint4 *>(reg + k_byte(t, 16 * c));
+      uint32_t w[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t acc = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc |= (uint32_t)vl[v_byte(D, t, 16 * c + 4 * q + e) - v_offset(D)] << (8 * e);
+        w[q] = acc;
+      }
+      vq = uint4{w[0], w[1], w[2], w[3]};
+    }
+    *reinterpret_cast<uint4 *>(keys + o) = kq;
+    *reinterpret_cast<uint4 *>(values + o) = vq;
+  }
+  for (int p = tid; p < 64 * G; p += 256) {
+    const int t = p / G, g = p % G;
+    const int ti = 64 * j + t;
+    if (ti < ta || ti >= tb) continue;
     uint32_t km = 0, vm = 0;
     if (valid) {
-      km = *reinterpret_cast<const uint32_t *>(reg + km_offset(D) + ((t * G + lane) << 2));
-      vm = *reinterpret_cast<const uint32_t *>(reg + vm_offset(D, G) + ((t * G + lane) << 2));
+      km = *reinterpret_cast<const uint32_t *>(reg + km_offset(D) + ((t * G + g) << 2));
+      vm = *reinterpret_cast<const uint32_t *>(reg + vm_offset(D, G) + ((t * G + g) << 2));
     }
-    ks[row * G + lane] = (uint16_t)(km & 0xffffu);
-    kz[row * G + lane] = (uint16_t)(km >> 16);
-    vs[row * G + lane] = (uint16_t)(vm & 0xffffu);
-    vz[row * G + lane] = (uint16_t)(vm >> 16);
+    const int64_t m = (row0 + ti + off) * G + g;
+    ks[m] = (uint16_t)(km & 0xffffu);
+    kz[m] = (uint16_t)(km >> 16);
+    vs[m] = (uint16_t)(vm & 0xffffu);
+    vz[m] = (uint16_t)(vm >> 16);
   }
 }
 
@@ -780,18 +839,23 @@ hipError_t launch_quantize_append(const PoolGeometry &g, int32_t layer, const vo
 hipError_t launch_gather(const PoolGeometry &g, int32_t layer, const int32_t *tables, const int32_t *lens,
                          int32_t B, int32_t max_blocks, int32_t S_out, int32_t left_pad, void *keys,
                          void *values, void *ks, void *kz, void *vs, void *vz, hipStream_t st) {
-  const int64_t waves = (int64_t)B * g.Hkv * S_out;
-  if (waves == 0) return hipSuccess;
+  if ((int64_t)B * g.Hkv * S_out == 0) return hipSuccess;
+  if (B > 65535 || g.Hkv > 65535) return hipErrorInvalidValue;
   const LayerView lv = layer_view(g, layer);
-  const dim3 grid(wave_blocks(waves)), block(256);
+  // data workgroups: the <= S_out tokens that land in the output span at most
+  // ceil(S_out / 64) + 1 blocks; then one zero workgroup per 64 output rows
+  const int32_t tiles = (S_out + 63) / 64, nbx = tiles + 1;
+  const dim3 grid((unsigned)(nbx + tiles), (unsigned)g.Hkv, (unsigned)B), block(256);
   auto *k8 = static_cast<uint8_t *>(keys), *v8 = static_cast<uint8_t *>(values);
   auto *a = static_cast<uint16_t *>(ks), *bz = static_cast<uint16_t *>(kz), *c = static_cast<uint16_t *>(vs),
        *d = static_cast<uint16_t *>(vz);
   KRILL_DISPATCH_D(g.D, {
     if (g.G == 1)
-      k_gather<D, 1><<<grid, block, 0, st>>>(lv, tables, lens, B, g.Hkv, max_blocks, S_out, left_pad, k8, v8, a, bz, c, d);
+      k_gather<D, 1><<<grid, block, 0, st>>>(lv, tables, lens, g.Hkv, max_blocks, S_out, left_pad, nbx, k8, v8, a,
+                                             bz, c, d);
     else
-      k_gather<D, D / 64><<<grid, block, 0, st>>>(lv, tables, lens, B, g.Hkv, max_blocks, S_out, left_pad, k8, v8, a, bz, c, d);
+      k_gather<D, D / 64><<<grid, block, 0, st>>>(lv, tables, lens, g.Hkv, max_blocks, S_out, left_pad, nbx, k8, v8,
+                                                  a, bz, c, d);
   });
   return hipGetLastError();
 }
