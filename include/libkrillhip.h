@@ -61,6 +61,10 @@ extern "C" {
                                     (1..64, consecutive blocks of the batch's concatenated block lists),
                                     per split of one sequence on the MFMA path; 0 = automatic */
 #define KRILL_OPT_ATTN_PATH 2    /* 0 auto (VALU <= 8 query rows per KV head, else MFMA), 1 VALU, 2 MFMA */
+#define KRILL_OPT_WINDOW 3       /* sliding window in tokens (0 none, else >= 2): before each append a
+                                    sequence keeps its last window - 1 tokens and its blocks that hold none
+                                    of them go back to the pool (RotatingKVCache.trimForAppend,
+                                    RotatingKVCache.swift:70-75); for the pool of the sliding layers */
 
 typedef struct krill_pool *krill_pool_t;
 typedef void *krill_stream_t; /* hipStream_t */
@@ -320,6 +324,27 @@ int32_t krill_decode_append_attention_shared_prefix(krill_pool_t pool, int32_t l
                                                     int32_t max_suffix_len, int32_t Hq, float scale, void *dev_out,
                                                     int32_t out_dtype, void *dev_ws, size_t ws_bytes,
                                                     krill_stream_t stream);
+/* First retained token of each sequence (0 unless the pool's window dropped
+ * tokens): RotatingKVCache's totalSeen - retainedLength
+ * (RotatingKVCache.swift:57-66); the sequence's length stays the total
+ * appended (sequenceLength).  Host arrays. */
+int32_t krill_batch_starts(krill_pool_t pool, const int32_t *seqs, int32_t B, int32_t *starts_out);
+/* Sliding-window attention (RotatingKVCache.update + the sliding mask of
+ * createSlidingWindowCausalMask, LlamaModel.swift:216-230): query row j of
+ * sequence b (position p = lens[b] - Lq + j) sees keys k with
+ * max(starts[b], p - window + 1) <= k <= p.  Tables are the pool's (block
+ * entries below the window are -1 and never read) with the starts of
+ * krill_batch_starts (dev_starts NULL: 0, for a pool that keeps every
+ * block).  Reads only the blocks from the one holding each sequence's first
+ * visible key.  Lq = 1 is decode (the retained window, no mask, as the
+ * reference), Lq > 1 a chunked prefill; VALU / MFMA as the other calls. */
+int32_t krill_window_workspace_size(krill_pool_t pool, int32_t B, int32_t Hq, int32_t Lq, int32_t max_blocks,
+                                    int32_t max_seq_len, int32_t window, size_t *bytes_out);
+int32_t krill_attention_windowed(krill_pool_t pool, int32_t layer, const void *dev_q, int32_t Lq,
+                                 const int32_t *dev_block_tables, const int32_t *dev_seq_lens,
+                                 const int32_t *dev_starts, int32_t window, int32_t B, int32_t max_blocks,
+                                 int32_t max_seq_len, int32_t Hq, float scale, void *dev_out, int32_t out_dtype,
+                                 void *dev_ws, size_t ws_bytes, krill_stream_t stream);
 /* Speculative-verify / chunked-prefill attention: Lq new query rows per
  * sequence, already appended, causal inside the window (row j sees tokens
  * [0, len - Lq + j]; BatchedDecode.swift:299-312, LlamaModel.swift:186-202).

@@ -32,6 +32,7 @@ POOL_HOST_ONLY = 1
 
 OPT_SPLIT_BLOCKS = 1
 OPT_ATTN_PATH = 2
+OPT_WINDOW = 3
 
 _CODE_NAMES = {
     KRILL_E_INVAL: "KRILL_E_INVAL",
@@ -135,6 +136,7 @@ SIGNATURES = {
     "krill_seq_reserve_append": [P, I32, I32, PI32],
     "krill_seq_block_table": [P, I32, PI32, I32, PI32],
     "krill_batch_tables": [P, PI32, I32, I32, PI32, PI32],
+    "krill_batch_starts": [P, PI32, I32, PI32],
     "krill_prefix_store": [P, I32, STR, STR, PI64, I32, PI32],
     "krill_prefix_lookup": [P, STR, STR, PI64, I32, PI32, PI32],
     "krill_prefix_lookup_longest": [P, STR, STR, PI64, I32, PI32, PI32],
@@ -154,6 +156,9 @@ SIGNATURES = {
                                ctypes.c_size_t, P],
     "krill_decode_append_attention": [P, I32, P, P, P, I64, I64, P, P, I32, I32, I32, I32, ctypes.c_float, P,
                                       I32, P, ctypes.c_size_t, P],
+    "krill_window_workspace_size": [P, I32, I32, I32, I32, I32, I32, ctypes.POINTER(ctypes.c_size_t)],
+    "krill_attention_windowed": [P, I32, P, I32, P, P, P, I32, I32, I32, I32, I32, ctypes.c_float, P, I32, P,
+                                 ctypes.c_size_t, P],
     "krill_shared_prefix_workspace_size": [P, I32, I32, I32, I32, ctypes.POINTER(ctypes.c_size_t)],
     "krill_decode_attention_shared_prefix": [P, I32, P, P, I32, P, P, I32, I32, I32, I32, ctypes.c_float, P, I32,
                                              P, ctypes.c_size_t, P],

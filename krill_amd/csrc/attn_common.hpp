@@ -58,6 +58,10 @@ struct AttnArgs {
   int32_t len_const;     // >= 0: every sequence holds this many tokens (lens not read)
   int32_t causal;        // 1: query row j sees keys [0, len - Lq + j]; 0: every key
   int32_t partial_only;  // 1: every segment leaves a partial, none writes the output
+  // sliding window (win_start null: none): query row j of sequence b sees
+  // keys [max(win_start[b], len - Lq + j - window + 1), len - Lq + j]
+  const int32_t *win_start;
+  int32_t window;
 };
 
 inline AttnArgs make_attn_args(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p) {
@@ -107,6 +111,8 @@ inline AttnArgs make_attn_args(const PoolGeometry &g, int32_t layer, const AttnL
   r.len_const = a.len_const;
   r.causal = a.causal;
   r.partial_only = a.partial_only;
+  r.win_start = a.win_start;
+  r.window = a.window;
   return r;
 }
 

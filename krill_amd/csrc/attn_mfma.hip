@@ -57,8 +57,11 @@ __host__ __device__ constexpr int mfma_stage_bytes(int D, int G) { return (head_
 // compute unit, which costs more than the deeper prefetch gains).
 __host__ __device__ constexpr int mfma_stages(int D) { return 2; }
 
-template <int D, int MODE, int NRT, bool ROPE>
+// VAR: 0 plain; 1 RoPE of the queries; 2 sliding window (keys below
+// max(win_start[b], position - window + 1) masked).
+template <int D, int MODE, int NRT, int VAR>
 __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
+  constexpr bool ROPE = VAR == 1, WIN = VAR == 2;
   constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
   constexpr int KS = D / 32;   // 32-d steps of Q.K^T
   constexpr int NDT = D / 16;  // 16-d tiles of P.V
@@ -246,6 +249,17 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
       lim[rt] = rvalid[rt] ? key_limit(a, len, r / a.R) : 0;
     }
     const int lim_lo = key_limit(a, len, rbase / a.R);  // keys seen by the group's first row
+    int lo[NRT], wst = 0, lo_hi = 0;  // sliding window: per-row first key, first retained key, group's largest
+    if constexpr (WIN) {
+      wst = a.win_start[b];
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt) {
+        const int r = rbase + 16 * rt + n;
+        lo[rt] = max(wst, len - a.Lq + r / a.R - a.window + 1);
+      }
+      const int rlast = min(a.NR, rbase + RR) - 1;
+      lo_hi = max(wst, len - a.Lq + rlast / a.R - a.window + 1);
+    }
     float m_run[NRT], l_part[NRT], c_part[NRT][G];
     float4_t oacc[NRT][NDT];
 #pragma unroll
@@ -268,7 +282,8 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
       const int tbase = (i - s) << 6;
       // some row of this group does not see every token of the block (causal
       // edge or the sequence's last block): only then are scores masked
-      const bool edge = tbase + 64 > lim_lo;
+      bool edge = tbase + 64 > lim_lo;
+      if constexpr (WIN) edge = edge || tbase < lo_hi;  // or below some row's window
 
       // ---- S^T = K . Q^T, four 16-token tiles.  Affine mode feeds the bytes
       // as exact fp16 1024 + u and folds the offset into the zero point:
@@ -355,7 +370,8 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
           for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              if (tbase + 16 * tt + 4 * q4 + e >= lim[rt]) sc[tt][rt][e] = -INFINITY;
+              if (tbase + 16 * tt + 4 * q4 + e >= lim[rt] || (WIN && tbase + 16 * tt + 4 * q4 + e < lo[rt]))
+                sc[tt][rt][e] = -INFINITY;
       }
 
       // ---- online softmax with a lazily raised running max (row n of each
@@ -424,7 +440,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
           if (edge) {  // metadata past the sequence's end is not data
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              if (tbase + tokh + e >= len)
+              if (tbase + tokh + e >= len || (WIN && tbase + tokh + e < wst))
 #pragma unroll
                 for (int g = 0; g < G; ++g) vm[e * G + g] = 0u;
           }
@@ -546,15 +562,19 @@ static hipError_t launch_mfma_nrt(const AttnArgs &args, int NRT, dim3 grid, hipS
   switch (NRT) {
     case 1:
       if (args.rope_cs)
-        k_attn_mfma<D, MODE, 1, true><<<grid, dim3(64), 0, st>>>(args);
+        k_attn_mfma<D, MODE, 1, 1><<<grid, dim3(64), 0, st>>>(args);
+      else if (args.win_start)
+        k_attn_mfma<D, MODE, 1, 2><<<grid, dim3(64), 0, st>>>(args);
       else
-        k_attn_mfma<D, MODE, 1, false><<<grid, dim3(64), 0, st>>>(args);
+        k_attn_mfma<D, MODE, 1, 0><<<grid, dim3(64), 0, st>>>(args);
       break;
     case 2:
       if (args.rope_cs)
-        k_attn_mfma<D, MODE, 2, true><<<grid, dim3(64), 0, st>>>(args);
+        k_attn_mfma<D, MODE, 2, 1><<<grid, dim3(64), 0, st>>>(args);
+      else if (args.win_start)
+        k_attn_mfma<D, MODE, 2, 2><<<grid, dim3(64), 0, st>>>(args);
       else
-        k_attn_mfma<D, MODE, 2, false><<<grid, dim3(64), 0, st>>>(args);
+        k_attn_mfma<D, MODE, 2, 0><<<grid, dim3(64), 0, st>>>(args);
       break;
     default: return hipErrorInvalidValue;
   }
@@ -589,9 +609,9 @@ template <int D, int MODE>
 static int32_t occupancy_mfma(int nrt) {
   int n = 0;
   hipError_t e = nrt == 2 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                                &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, 2, false>), 64, 0)
+                                &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, 2, 0>), 64, 0)
                           : hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                                &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, 1, false>), 64, 0);
+                                &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, 1, 0>), 64, 0);
   if (e != hipSuccess || n <= 0) {
     (void)hipGetLastError();
     n = (160 * 1024) / (mfma_stages(D) * mfma_stage_bytes(D, MODE == MODE_AFFINE ? D / 64 : 1));

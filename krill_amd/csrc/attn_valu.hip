@@ -193,8 +193,11 @@ __device__ __forceinline__ void store_newest(const AttnArgs &a, int hk, int phys
   }
 }
 
-template <int D, int NR, int MODE, bool ROPE>
+// VAR: 0 plain; 1 RoPE of the queries (and the fused new K row); 2 sliding
+// window (keys below max(win_start[b], position - window + 1) masked).
+template <int D, int NR, int MODE, int VAR>
 __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_valu(AttnArgs a) {
+  constexpr bool ROPE = VAR == 1, WIN = VAR == 2;
   constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
   constexpr int NP = D / 16;   // 16-byte K pieces per token row
   constexpr int PPG = NP / G;  // pieces per scale group
@@ -443,6 +446,12 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     int lim[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) lim[r] = key_limit(a, len, r / a.R);
+    int lo[NR], wst = 0;  // sliding window: first key each row sees, first retained key
+    if constexpr (WIN) {
+      wst = a.win_start[b];
+#pragma unroll
+      for (int r = 0; r < NR; ++r) lo[r] = max(wst, len - a.Lq + r / a.R - a.window + 1);
+    }
 
     float m_run[NR], l_part[NR], c_part[NR][G], acc[NR][DPL];
 #pragma unroll
@@ -549,7 +558,9 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       } else {
         v = accg[r][0];
       }
-      s[r] = (tbase + lane < lim[r]) ? v * a.scale_log2 : -INFINITY;
+      bool seen = tbase + lane < lim[r];
+      if constexpr (WIN) seen = seen && tbase + lane >= lo[r];
+      s[r] = seen ? v * a.scale_log2 : -INFINITY;
     }
 
     // ---- online softmax with a lazily raised running max
@@ -582,7 +593,8 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     }
 
     // ---- weights to LDS in V storage order
-    const bool valid = tbase + lane < len;
+    bool valid = tbase + lane < len;
+    if constexpr (WIN) valid = valid && tbase + lane >= wst;  // rows below the window are not data
     if constexpr (MODE == MODE_AFFINE) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -743,9 +755,11 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
 template <int D, int MODE, int NR>
 static void launch_one(const AttnArgs &args, int B, dim3 grid, hipStream_t st) {
   if (args.rope_cs)
-    k_attn_valu<D, NR, MODE, true><<<grid, dim3(64), 0, st>>>(args);
+    k_attn_valu<D, NR, MODE, 1><<<grid, dim3(64), 0, st>>>(args);
+  else if (args.win_start)
+    k_attn_valu<D, NR, MODE, 2><<<grid, dim3(64), 0, st>>>(args);
   else
-    k_attn_valu<D, NR, MODE, false><<<grid, dim3(64), 0, st>>>(args);
+    k_attn_valu<D, NR, MODE, 0><<<grid, dim3(64), 0, st>>>(args);
 }
 
 template <int D, int MODE>
@@ -771,7 +785,7 @@ static int32_t occupancy_nr(int NR) {
   switch (NR) {
 #define KRILL_OCC(N)                                                                                        \
   case N:                                                                                                   \
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(&k_attn_valu<D, N, MODE, false>), \
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(&k_attn_valu<D, N, MODE, 0>), \
                                                      64, 0);                                                \
     if (e != hipSuccess || n <= 0) n = 4 * valu_waves_per_simd<D, N>();                                    \
     break;

@@ -82,14 +82,15 @@ void BlockManager::release_block(int32_t b) {
 }
 
 void BlockManager::release_seq_blocks(Seq &s, size_t keep) {
-  for (size_t i = keep; i < s.blocks.size(); ++i) release_block(s.blocks[i]);
+  for (size_t i = keep; i < s.blocks.size(); ++i)
+    if (s.blocks[i] != kDropped) release_block(s.blocks[i]);
   s.blocks.resize(keep);
 }
 
 bool BlockManager::entry_frees_blocks(const Entry &e) const {
   const Seq &s = seqs_[static_cast<size_t>(e.seq)];
   for (int32_t b : s.blocks)
-    if (refcnt_[static_cast<size_t>(b)] == 1) return true;
+    if (b != kDropped && refcnt_[static_cast<size_t>(b)] == 1) return true;
   return false;
 }
 
@@ -162,12 +163,17 @@ int32_t BlockManager::seq_fork(int32_t src, int32_t n_tokens, int32_t *out) {
   int32_t id = new_seq_id();
   Seq &s = seqs_[static_cast<size_t>(id)];
   const Seq &p = seqs_[static_cast<size_t>(src)];
+  if (n_tokens < p.start)
+    return fail(KRILL_E_RANGE, "fork of %d tokens below the sliding window (first retained token %d)", n_tokens,
+                p.start);
   s = Seq{};
   s.alive = true;
   s.len = n_tokens;
+  s.start = p.start;
   size_t nb = static_cast<size_t>((n_tokens + cfg_.block_tokens - 1) / cfg_.block_tokens);
   s.blocks.assign(p.blocks.begin(), p.blocks.begin() + static_cast<std::ptrdiff_t>(nb));
-  for (int32_t b : s.blocks) ++refcnt_[static_cast<size_t>(b)];
+  for (int32_t b : s.blocks)
+    if (b != kDropped) ++refcnt_[static_cast<size_t>(b)];
   ++live_seqs_;
   *out = id;
   return KRILL_OK;
@@ -191,6 +197,7 @@ int32_t BlockManager::seq_reset(int32_t seq) {
   Seq &s = seqs_[static_cast<size_t>(seq)];
   release_seq_blocks(s, 0);
   s.len = 0;
+  s.start = 0;
   return KRILL_OK;
 }
 
@@ -206,7 +213,8 @@ int32_t BlockManager::seq_memory_bytes(int32_t seq, int64_t *out) {
   std::lock_guard<std::mutex> g(mu_);
   if (int32_t rc = check_seq(seq, false)) return rc;
   if (!out) return fail(KRILL_E_INVAL, "bytes_out is NULL");
-  *out = memory_bytes(seqs_[static_cast<size_t>(seq)].len);
+  const Seq &s = seqs_[static_cast<size_t>(seq)];
+  *out = memory_bytes(s.len - s.start);  // retained tokens
   return KRILL_OK;
 }
 
@@ -216,6 +224,9 @@ int32_t BlockManager::seq_truncate(int32_t seq, int32_t n) {
   Seq &s = seqs_[static_cast<size_t>(seq)];
   // QuantizedKVCache.truncate: no-op unless 0 <= n < length (:137-138).
   if (n >= s.len || n < 0) return KRILL_OK;
+  // RotatingKVCache.canTruncate: only the retained tail can go (RotatingKVCache.swift:123-127)
+  if (n < s.start)
+    return fail(KRILL_E_RANGE, "truncate to %d below the sliding window (first retained token %d)", n, s.start);
   size_t keep = static_cast<size_t>((n + cfg_.block_tokens - 1) / cfg_.block_tokens);
   release_seq_blocks(s, keep);
   s.len = n;
@@ -232,6 +243,19 @@ int32_t BlockManager::reserve_append(int32_t seq, int32_t L, int32_t *slots_out)
   if (static_cast<int64_t>(s.len) + L > INT32_MAX / 2)
     return fail(KRILL_E_RANGE, "sequence would exceed %d tokens", INT32_MAX / 2);
   const int32_t bt = cfg_.block_tokens;
+  // Sliding window: keep window - 1 tokens before the append
+  // (RotatingKVCache.trimForAppend, RotatingKVCache.swift:70-75) and drop
+  // every block that holds none of the retained ones.
+  if (cfg_.window > 0 && s.len - s.start > cfg_.window - 1) {
+    s.start = s.len - (cfg_.window - 1);
+    for (int32_t i = 0; i < s.start / bt; ++i) {
+      int32_t &blk = s.blocks[static_cast<size_t>(i)];
+      if (blk != kDropped) {
+        release_block(blk);
+        blk = kDropped;
+      }
+    }
+  }
 
   std::vector<int32_t> fresh;  // allocated here, released on failure
   int32_t cow_idx = -1, cow_old = -1;
@@ -311,11 +335,34 @@ int32_t BlockManager::batch_tables(const int32_t *seqs, int32_t B, int32_t max_b
   return KRILL_OK;
 }
 
+int32_t BlockManager::batch_starts(const int32_t *seqs, int32_t B, int32_t *starts_out) {
+  std::lock_guard<std::mutex> g(mu_);
+  if (B < 0) return fail(KRILL_E_INVAL, "negative batch");
+  if (B > 0 && (!seqs || !starts_out)) return fail(KRILL_E_INVAL, "NULL batch argument");
+  for (int32_t b = 0; b < B; ++b) {
+    if (int32_t rc = check_seq(seqs[b], false)) return rc;
+    starts_out[b] = seqs_[static_cast<size_t>(seqs[b])].start;
+  }
+  return KRILL_OK;
+}
+
+int32_t BlockManager::set_window(int32_t window) {
+  std::lock_guard<std::mutex> g(mu_);
+  if (window < 0 || window == 1) return fail(KRILL_E_INVAL, "sliding window of %d tokens (0 or >= 2)", window);
+  if (window == 0)
+    for (const Seq &s : seqs_)
+      if (s.alive && s.start > 0) return fail(KRILL_E_STATE, "a sequence already dropped tokens to the window");
+  cfg_.window = window;
+  return KRILL_OK;
+}
+
 int32_t BlockManager::prefix_store(int32_t seq, const char *model_id, const char *media_hash,
                                    const int64_t *tokens, int32_t n, int32_t *stored_out) {
   std::lock_guard<std::mutex> g(mu_);
   if (stored_out) *stored_out = 0;
   if (int32_t rc = check_seq(seq, false)) return rc;
+  if (seqs_[static_cast<size_t>(seq)].start > 0)
+    return fail(KRILL_E_UNSUPPORTED, "prefix entry of a sequence that dropped tokens to the sliding window");
   if (n < 0 || (n > 0 && !tokens)) return fail(KRILL_E_INVAL, "bad token array");
   if (n > seqs_[static_cast<size_t>(seq)].len)
     return fail(KRILL_E_RANGE, "store of %d tokens from a sequence of %d", n,
@@ -341,7 +388,7 @@ int32_t BlockManager::prefix_store(int32_t seq, const char *model_id, const char
   s.len = n;
   size_t nb = static_cast<size_t>((n + cfg_.block_tokens - 1) / cfg_.block_tokens);
   s.blocks.assign(p.blocks.begin(), p.blocks.begin() + static_cast<std::ptrdiff_t>(nb));
-  for (int32_t b : s.blocks) ++refcnt_[static_cast<size_t>(b)];
+  for (int32_t b : s.blocks) ++refcnt_[static_cast<size_t>(b)];  // no dropped block: start == 0
   Entry e{key, model_id ? model_id : "", media_hash ? media_hash : "",
           std::vector<int64_t>(tokens, tokens + n), id};
   entries_.push_back(std::move(e));

@@ -36,6 +36,7 @@ struct BlockManagerConfig {
   int32_t min_prefix_len = 8;     // PrefixCache minPrefixLength default (PrefixCache.swift:101)
   int64_t max_entry_bytes = -1;   // <= 0: no cap
   uint64_t free_list_seed = 0;
+  int32_t window = 0;             // sliding window in tokens (0: none)
 };
 
 struct BlockManagerStats {
@@ -61,6 +62,10 @@ class BlockManager {
   int32_t block_table(int32_t seq, int32_t *out, int32_t cap, int32_t *n_out);
   int32_t batch_tables(const int32_t *seqs, int32_t B, int32_t max_blocks, int32_t *tables_out,
                        int32_t *lens_out);
+  // First retained token of each sequence (0 without a window).
+  int32_t batch_starts(const int32_t *seqs, int32_t B, int32_t *starts_out);
+  // Sliding window of every sequence from the next append on (0: none).
+  int32_t set_window(int32_t window);
 
   int32_t prefix_store(int32_t seq, const char *model_id, const char *media_hash,
                        const int64_t *tokens, int32_t n, int32_t *stored_out);
@@ -81,9 +86,12 @@ class BlockManager {
   int64_t memory_bytes(int64_t n) const;
 
  private:
+  // Table entry of a block dropped from a sliding window.
+  static constexpr int32_t kDropped = -1;
   struct Seq {
-    std::vector<int32_t> blocks;
+    std::vector<int32_t> blocks;  // absolute block index -> block id (kDropped below the window)
     int32_t len = 0;
+    int32_t start = 0;  // first retained token
     bool alive = false;
     bool frozen = false;  // owned by a prefix entry
   };

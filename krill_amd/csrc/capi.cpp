@@ -237,6 +237,9 @@ int32_t krill_pool_set_option(krill_pool_t pool, int32_t option, int64_t value) 
       if (value < 0 || value > 2) return fail(KRILL_E_INVAL, "attention path %lld", static_cast<long long>(value));
       pool->opt_path = static_cast<int32_t>(value);
       return KRILL_OK;
+    case KRILL_OPT_WINDOW:
+      if (value < 0 || value > INT32_MAX / 4) return fail(KRILL_E_INVAL, "window %lld", static_cast<long long>(value));
+      return pool->bm->set_window(static_cast<int32_t>(value));
     default:
       return fail(KRILL_E_INVAL, "unknown option %d", option);
   }
@@ -301,6 +304,12 @@ int32_t krill_batch_tables(krill_pool_t pool, const int32_t *seqs, int32_t B, in
   krill::clear_error();
   if (int32_t rc = check_pool(pool)) return rc;
   return pool->bm->batch_tables(seqs, B, max_blocks, tables_out, lens_out);
+}
+
+int32_t krill_batch_starts(krill_pool_t pool, const int32_t *seqs, int32_t B, int32_t *starts_out) {
+  krill::clear_error();
+  if (int32_t rc = check_pool(pool)) return rc;
+  return pool->bm->batch_starts(seqs, B, starts_out);
 }
 
 // -------------------------------------------------------- prefix entries
@@ -726,6 +735,81 @@ int32_t krill_decode_append_attention_shared_prefix(krill_pool_t pool, int32_t l
   nt.sh = stride_h;
   return run_shared_prefix(pool, layer, dev_q, dev_prefix_table, prefix_blocks, dev_suffix_tables, dev_suffix_lens, B,
                            max_blocks, max_suffix_len, Hq, scale, dev_out, out_dtype, dev_ws, ws_bytes, stream, nt);
+}
+
+// Plan of a sliding-window call (the view's lengths are at most
+// Lq + window + 62) and its workspace: the attention's, then the view.
+static int32_t plan_windowed(krill_pool_t pool, int32_t B, int32_t Hq, int32_t Lq, int32_t max_blocks,
+                             int32_t max_seq_len, int32_t window, krill::AttnPlan *plan, size_t *view_off,
+                             size_t *total) {
+  if (B < 0 || Lq < 1 || max_blocks < 0 || max_seq_len < 0) return fail(KRILL_E_INVAL, "bad B, Lq, width or length");
+  if (window < 2) return fail(KRILL_E_INVAL, "sliding window of %d tokens (>= 2)", window);
+  const int64_t vmax = std::min<int64_t>(max_seq_len, (int64_t)Lq + window + 62);
+  int32_t r = krill::plan_attention(pool->geom, B, Hq, Lq, (int32_t)vmax, pool->opt_split_blocks, pool->opt_path,
+                                    plan);
+  if (r == -2) return fail(KRILL_E_UNSUPPORTED, "VALU path handles at most 8 query rows per KV head");
+  if (r != 0) return fail(KRILL_E_INVAL, "Hq %d not a multiple of %d KV heads, or bad B/Lq/length", Hq, pool->geom.Hkv);
+  *view_off = (plan->ws_bytes + 255) & ~(size_t)255;
+  *total = *view_off + ((size_t)B * (size_t)max_blocks + 2 * (size_t)B) * sizeof(int32_t);
+  return KRILL_OK;
+}
+
+int32_t krill_window_workspace_size(krill_pool_t pool, int32_t B, int32_t Hq, int32_t Lq, int32_t max_blocks,
+                                    int32_t max_seq_len, int32_t window, size_t *bytes_out) {
+  krill::clear_error();
+  if (int32_t rc = check_pool(pool)) return rc;
+  if (!bytes_out) return fail(KRILL_E_INVAL, "bytes_out is NULL");
+  krill::AttnPlan plan;
+  size_t off = 0, total = 0;
+  if (int32_t rc = plan_windowed(pool, B, Hq, Lq, max_blocks, max_seq_len, window, &plan, &off, &total)) return rc;
+  *bytes_out = total;
+  return KRILL_OK;
+}
+
+int32_t krill_attention_windowed(krill_pool_t pool, int32_t layer, const void *dev_q, int32_t Lq,
+                                 const int32_t *dev_block_tables, const int32_t *dev_seq_lens,
+                                 const int32_t *dev_starts, int32_t window, int32_t B, int32_t max_blocks,
+                                 int32_t max_seq_len, int32_t Hq, float scale, void *dev_out, int32_t out_dtype,
+                                 void *dev_ws, size_t ws_bytes, krill_stream_t stream) {
+  krill::clear_error();
+  if (int32_t rc = check_device_pool(pool, layer)) return rc;
+  if (B < 0 || max_blocks < 0 || max_seq_len < 0) return fail(KRILL_E_INVAL, "negative B, max_blocks or length");
+  if (B == 0) return KRILL_OK;
+  if (!dev_q || !dev_block_tables || !dev_seq_lens || !dev_out) return fail(KRILL_E_INVAL, "NULL device pointer");
+  if (out_dtype != KRILL_DTYPE_F32 && out_dtype != KRILL_DTYPE_F16 && out_dtype != KRILL_DTYPE_BF16)
+    return fail(KRILL_E_INVAL, "out_dtype %d", out_dtype);
+  if (!std::isfinite(scale)) return fail(KRILL_E_INVAL, "scale is not finite");
+  if ((int64_t)max_blocks * 64 < (int64_t)max_seq_len)
+    return fail(KRILL_E_RANGE, "max_seq_len %d exceeds the %d-block table width", max_seq_len, max_blocks);
+  if (B > 65535) return fail(KRILL_E_RANGE, "batch of %d sequences (at most 65535)", B);
+  krill::AttnPlan plan;
+  size_t off = 0, total = 0;
+  if (int32_t rc = plan_windowed(pool, B, Hq, Lq, max_blocks, max_seq_len, window, &plan, &off, &total)) return rc;
+  if (ws_bytes < total || !dev_ws) return fail(KRILL_E_INVAL, "workspace of %zu bytes < %zu required", ws_bytes, total);
+  krill::AttnLaunch a;
+  a.q = dev_q;
+  a.tables = dev_block_tables;
+  a.lens = dev_seq_lens;
+  a.B = B;
+  a.max_blocks = max_blocks;
+  a.max_seq_len = (int32_t)std::min<int64_t>(max_seq_len, (int64_t)Lq + window + 62);
+  a.Hq = Hq;
+  a.Lq = Lq;
+  a.scale = scale;
+  a.out = dev_out;
+  a.out_dtype = out_dtype == KRILL_DTYPE_F32 ? krill::DT_F32 : out_dtype == KRILL_DTYPE_F16 ? krill::DT_F16
+                                                                                          : krill::DT_BF16;
+  a.ws = dev_ws;
+  a.ws_bytes = off;
+  a.split_blocks = plan.split_blocks;
+  a.path = pool->opt_path;
+  int32_t *view = reinterpret_cast<int32_t *>(static_cast<uint8_t *>(dev_ws) + off);
+  DeviceGuard dg(pool->device);
+  hipStream_t st = pick_stream(pool, stream);
+  if (int32_t rc = flush_pending(pool, st)) return rc;
+  hipError_t e = krill::launch_attention_windowed(pool->geom, layer, a, plan, dev_starts, window, view, st);
+  if (e != hipSuccess) return hip_fail(e, "windowed attention launch");
+  return KRILL_OK;
 }
 
 int32_t krill_verify_attention(krill_pool_t pool, int32_t layer, const void *dev_q, int32_t Lq,

@@ -168,6 +168,13 @@ class KVPool:
         L.check(L.lib().krill_batch_tables(self._h, _i32p(seqs), B, max_blocks, _i32p(tables), _i32p(lens)))
         return tables[:B, :max_blocks], lens[:B]
 
+    def batch_starts(self, seqs) -> np.ndarray:
+        """First retained token of each sequence (sliding-window pools)."""
+        seqs = np.ascontiguousarray(seqs, np.int32)
+        out = np.zeros(max(seqs.size, 1), np.int32)
+        L.check(L.lib().krill_batch_starts(self._h, _i32p(seqs), seqs.size, _i32p(out)))
+        return out[: seqs.size]
+
     # ---------------------------------------------------------- prefix
     def prefix_store(self, seq: int, tokens, model_id: str = "", media_hash=None) -> bool:
         t = np.ascontiguousarray(tokens, np.int64)
@@ -357,6 +364,35 @@ class KVPool:
             L.check(L.lib().krill_verify_attention(self._h, layer, q.data_ptr(), Lq, tables.data_ptr(),
                                                    lens.data_ptr(), B, mb, max_seq_len, Hq, float(scale),
                                                    out.data_ptr(), code, ws.data_ptr(), ws.numel(), st))
+        return out
+
+    def attention_windowed(self, layer: int, q, tables, lens, starts, window: int, max_seq_len: int, scale: float,
+                           out_dtype=None, ws=None, out=None, stream=None):
+        """Sliding-window attention: row j of sequence b (position p = lens[b] -
+        Lq + j) sees keys [max(starts[b], p - window + 1), p]; starts (int32
+        [B] device, or None for 0) from batch_starts."""
+        torch = _torch()
+        B, Hq, Lq, D = q.shape
+        self._check_dev("q", q, self.in_dtype)
+        Bt, mb = self._tables(tables, lens)
+        if Bt != B or D != self.head_dim:
+            raise ValueError("q batch/head_dim does not match the tables/pool")
+        if starts is not None:
+            self._check_dev("starts", starts, torch.int32, (B,))
+        out_dtype = torch.float32 if out_dtype is None else out_dtype
+        code = _dtype_code(out_dtype)
+        if out is None:
+            out = torch.empty((B, Hq, Lq, D), dtype=out_dtype, device=q.device)
+        else:
+            self._check_dev("out", out, out_dtype, (B, Hq, Lq, D))
+        need = ctypes.c_size_t()
+        L.check(L.lib().krill_window_workspace_size(self._h, B, Hq, Lq, mb, max_seq_len, window, ctypes.byref(need)))
+        if ws is None or ws.numel() < need.value:
+            ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device=q.device)
+        L.check(L.lib().krill_attention_windowed(
+            self._h, layer, q.data_ptr(), Lq, tables.data_ptr(), lens.data_ptr(),
+            starts.data_ptr() if starts is not None else None, window, B, mb, max_seq_len, Hq, float(scale),
+            out.data_ptr(), code, ws.data_ptr(), ws.numel(), self._stream(stream)))
         return out
 
     def attention_shared_prefix(self, layer: int, q, prefix_table, suffix_tables, suffix_lens, max_suffix_len: int,

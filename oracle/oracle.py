@@ -38,6 +38,16 @@ attention_f64 (a7/a8)       closed forms: one key -> output = that value row;
 stack_left_padded (a5)      closed form of BatchedDecode.swift:119-147 on
                             integer rows (tests/test_oracle.py).
 prefix_key (a10)            FNV-1a 64 published test vectors ("" and "a").
+sliding_window_rows         the reference's mask tests
+(next row 4)                (SlidingWindowMaskTests.swift:17-53): the
+                            visible sets of (4, 0, 2), (3, 0, 10) and
+                            (1, 600, 512), key by key.
+attention_window_f64        reduces to attention_f64 on the key slice; against
+                            an independent numpy softmax with a -inf mask.
+rotating_retained_start     the retained rows of RotatingKVCacheTests.swift
+                            :115-161 (window 4: last min(t+1, 4) tokens after
+                            t appends; truncate 10 -> 8 then one append keeps
+                            tokens 6, 7, 8; below token 6 refused).
 rope_rows (next row 3)      closed forms: position 0 of a cos/sin table is the
                             identity bit for bit; a quarter turn (cos 0,
                             sin 1) maps (x, y) -> (-y, x) exactly; against
@@ -266,6 +276,48 @@ def attention_f64(q: np.ndarray, k: np.ndarray, v: np.ndarray, limits, scale: fl
     out = np.empty((NR, D), np.float64)
     lib().oracle_attention_f64(_p(q), _p(k), _p(v), NR, T, D, _p(lim), float(scale), _p(out))
     return out
+
+
+def sliding_window_rows(new_len: int, cache_len: int, window: int):
+    """Visible key range [lo, hi) of each of new_len query rows whose first
+    row sits at absolute position cache_len: causal and q - k < window
+    (createSlidingWindowCausalMask, Sources/KrillCore/LlamaModel.swift:216-230)."""
+    rows = []
+    for i in range(new_len):
+        q = cache_len + i
+        rows.append((max(0, q - window + 1), q + 1))
+    return rows
+
+
+def attention_window_f64(q: np.ndarray, k: np.ndarray, v: np.ndarray, lo, hi, scale: float) -> np.ndarray:
+    """q [NR, D], k/v [T, D]: row r attends keys [lo[r], hi[r]) -- attention_f64
+    over that slice of the keys."""
+    q = np.ascontiguousarray(q, np.float64)
+    out = np.empty(q.shape, np.float64)
+    for r in range(q.shape[0]):
+        a, b = int(lo[r]), int(hi[r])
+        out[r] = attention_f64(q[r: r + 1], k[a:b], v[a:b], [b - a], scale)[0]
+    return out
+
+
+def rotating_retained_start(ops, window: int) -> tuple[int, int]:
+    """(total tokens, first retained token) after ops on a RotatingKVCache
+    (Sources/KrillCache/RotatingKVCache.swift:70-75 trimForAppend before
+    every append of L >= 1 rows, :130-138 truncate within the retained
+    tail): ops = [("append", L) | ("truncate", n)]."""
+    total = start = 0
+    for op, x in ops:
+        if op == "append":
+            if x >= 1:
+                if total - start > window - 1:
+                    start = total - (window - 1)
+                total += x
+        elif op == "truncate":
+            if x < total:
+                if x < start:
+                    raise ValueError("truncate below the retained range")
+                total = x
+    return total, start
 
 
 # --------------------------------------------------------------------------

@@ -420,3 +420,90 @@ def test_concurrent_hammer_keeps_capacity_invariant():
     assert st["live_seqs"] == 0
     p.prefix_clear()
     assert p.stats()["blocks_used"] == 0
+
+
+# ---- sliding window (pool option): RotatingKVCache retention in paged form
+
+def _window_pool(window, blocks=64):
+    p = host_pool(blocks)
+    p.set_option(L.OPT_WINDOW, window)
+    return p
+
+
+def test_window_retains_last_window_tokens_reference_vectors(oracle):
+    # RotatingKVCacheTests.swift:115-131 (window 4, ten single appends)
+    p = _window_pool(4)
+    s = p.seq_create()
+    for t in range(10):
+        p.reserve_append(s, 1)
+        start = int(p.batch_starts([s])[0])
+        assert p.seq_length(s) == t + 1 and (t + 1) - start == min(t + 1, 4)
+        assert (t + 1, start) == oracle.rotating_retained_start([("append", 1)] * (t + 1), 4)
+    p.close()
+
+
+def test_window_truncate_bounds_reference_vectors():
+    # RotatingKVCacheTests.swift:133-161: retained 6..9 after ten appends
+    p = _window_pool(4)
+    s = p.seq_create()
+    for _ in range(10):
+        p.reserve_append(s, 1)
+    assert int(p.batch_starts([s])[0]) == 6
+    with pytest.raises(KrillError) as e:
+        p.seq_truncate(s, 5)  # position 5 was rotated out
+    assert e.value.code == L.KRILL_E_RANGE and p.seq_length(s) == 10
+    p.seq_truncate(s, 8)
+    assert p.seq_length(s) == 8
+    p.reserve_append(s, 1)  # retained 6, 7 and the new token
+    assert p.seq_length(s) == 9 and int(p.batch_starts([s])[0]) == 6
+    p.close()
+
+
+def test_window_frees_blocks_and_matches_the_rotating_model(oracle):
+    W = 150
+    p = _window_pool(W, blocks=40)
+    s = p.seq_create()
+    rng = np.random.default_rng(5)
+    ops = []
+    for _ in range(40):
+        if rng.random() < 0.15 and ops:
+            total, start = oracle.rotating_retained_start(ops, W)
+            n = int(rng.integers(start, total + 1))
+            ops.append(("truncate", n))
+            p.seq_truncate(s, n)
+        else:
+            L_ = int(rng.integers(1, 90))
+            ops.append(("append", L_))
+            p.reserve_append(s, L_)
+        total, start = oracle.rotating_retained_start(ops, W)
+        assert p.seq_length(s) == total and int(p.batch_starts([s])[0]) == start
+        table = p.block_table(s)
+        # blocks wholly below the first retained token are dropped (-1), the rest held
+        assert all(b == -1 for b in table[: start // 64]) and all(b >= 0 for b in table[start // 64:])
+        assert p.stats()["blocks_used"] == len(table) - start // 64
+    # 40 appends of up to 89 tokens in a 40-block pool: only the window stays
+    assert p.seq_length(s) > 40 * 64 // 4
+    p.seq_free(s)
+    assert p.stats()["blocks_used"] == 0
+    p.close()
+
+
+def test_window_guards():
+    p = _window_pool(100)
+    with pytest.raises(KrillError):
+        p.set_option(L.OPT_WINDOW, 1)
+    s = p.seq_create()
+    p.reserve_append(s, 300)
+    p.reserve_append(s, 1)  # trims: first retained token 201
+    assert int(p.batch_starts([s])[0]) == 201
+    with pytest.raises(KrillError) as e:
+        p.seq_fork(s, 150)  # below the window
+    assert e.value.code == L.KRILL_E_RANGE
+    f = p.seq_fork(s, 250)
+    assert int(p.batch_starts([f])[0]) == 201
+    with pytest.raises(KrillError) as e:
+        p.prefix_store(s, np.arange(301))  # a prefix entry needs every token
+    assert e.value.code == L.KRILL_E_UNSUPPORTED
+    with pytest.raises(KrillError):
+        p.set_option(L.OPT_WINDOW, 0)  # tokens already dropped
+    p.close()

@@ -1,0 +1,181 @@
+"""GPU: sliding-window layers in paged form (pool option KRILL_OPT_WINDOW +
+krill_attention_windowed).  The reference's gate (RotatingKVCacheTests.swift
+:40-113): the retained window attended without a mask must equal the full
+cache with the sliding mask, at decode (L = 1) and chunked-prefill shapes.
+Here both sides are built: a windowed pool whose blocks below the window go
+back to the pool, and a pool that keeps every block attended with the same
+window rule; both must match the oracle (attention over each row's visible
+keys [max(first retained, p - window + 1), p]) within 2e-3 and each other to
+float32 reassociation.  The first retained token follows RotatingKVCache's
+retention (oracle.rotating_retained_start)."""
+import numpy as np
+import pytest
+
+from kvutil import DT, MODE, i32, rand_bits, to_dev
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():  # pragma: no cover - CPU container
+    pytest.skip("no HIP device", allow_module_level=True)
+
+import krill_amd  # noqa: E402
+
+ATOL = 2e-3
+DTS = "bf16"
+
+
+class Seqs:
+    """B sequences appended through the product path in one pool; the
+    oracle's copy of every token and the ops applied to each sequence."""
+
+    def __init__(self, pool, B, total, rng):
+        H, D = pool.num_kv_heads, pool.head_dim
+        self.pool, self.B = pool, B
+        self.seqs = [pool.seq_create() for _ in range(B)]
+        self.k = [rand_bits(rng, (H, total, D), DTS) for _ in range(B)]
+        self.v = [rand_bits(rng, (H, total, D), DTS) for _ in range(B)]
+        self.ops = [[] for _ in range(B)]
+        self.len = [0] * B
+
+    def append(self, b, L):
+        s, p = self.seqs[b], self.len[b]
+        slots = self.pool.reserve_append(s, L)
+        self.pool.quantize_append(0, to_dev(self.k[b][None, :, p:p + L], DTS), to_dev(self.v[b][None, :, p:p + L], DTS),
+                                  i32(slots[None]))
+        self.len[b] += L
+        self.ops[b].append(("append", L))
+
+    def truncate(self, b, n):
+        self.pool.seq_truncate(self.seqs[b], n)
+        self.len[b] = n
+        self.ops[b].append(("truncate", n))
+
+    def tables(self):
+        mb = max((n + 63) // 64 for n in self.len)
+        t, n = self.pool.batch_tables(self.seqs, mb)
+        return i32(t), i32(n), mb
+
+
+def _oracle_rows(seqs, b, q_bits, window, start, mode):
+    """Expected outputs [Hq, Lq, D] of sequence b's last Lq query rows."""
+    H = seqs.pool.num_kv_heads
+    Hq, Lq, D = q_bits.shape
+    R = Hq // H
+    n = seqs.len[b]
+    kq, ks, kz = O.quantize(seqs.k[b][:, :n], DT[DTS], MODE[mode])
+    vq, vs, vz = O.quantize(seqs.v[b][:, :n], DT[DTS], MODE[mode])
+    kd, vd = O.dequant_f64(kq, ks, kz, MODE[mode]), O.dequant_f64(vq, vs, vz, MODE[mode])
+    qf = O.bits_to_f32(q_bits, DT[DTS]).astype(np.float64)
+    rows = O.sliding_window_rows(Lq, n - Lq, window)
+    lo = [max(start, a) for a, _ in rows]
+    hi = [h for _, h in rows]
+    out = np.zeros((Hq, Lq, D))
+    for hq in range(Hq):
+        out[hq] = O.attention_window_f64(qf[hq], kd[hq // R], vd[hq // R], lo, hi, 1.0 / np.sqrt(D))
+    return out
+
+
+def _check(pools, seqs_list, window, Lq, mode, rng, R, tol_pair=1e-5):
+    """Windowed attention of the last Lq rows of every sequence in each pool
+    (first pool: window option set, blocks below the window dropped; second:
+    every block kept, attended with the first pool's first retained tokens,
+    or with none (None) while no sequence has dropped any)."""
+    B = seqs_list[0].B
+    H, D = pools[0].num_kv_heads, pools[0].head_dim
+    q = rand_bits(rng, (B, H * R, Lq, D), DTS)
+    st = pools[0].batch_starts(seqs_list[0].seqs)
+    outs = []
+    for pool, seqs in zip(pools, seqs_list):
+        t, n, mb = seqs.tables()
+        starts = None if pool is pools[1] and not st.any() else i32(st)
+        out = pool.attention_windowed(0, to_dev(q, DTS), t, n, starts, window, int(max(seqs.len)), 1.0 / np.sqrt(D))
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+    seqs = seqs_list[0]
+    for b in range(B):
+        total, start = O.rotating_retained_start(seqs.ops[b], window)
+        assert total == seqs.len[b] and int(pools[0].batch_starts([seqs.seqs[b]])[0]) == start
+        want = _oracle_rows(seqs, b, q[b], window, start, mode)
+        for o in outs:
+            err = np.abs(o[b] - want).max()
+            assert err <= ATOL, (b, err)
+    dev = np.abs(outs[0] - outs[1]).max()
+    assert dev <= tol_pair, dev
+
+
+def _pools(mode, H, D, blocks, window, seed):
+    a = krill_amd.KVPool(1, H, D, blocks, mode, DTS, free_list_seed=seed)
+    a.set_option(krill_amd._lib.OPT_WINDOW, window)
+    b = krill_amd.KVPool(1, H, D, blocks, mode, DTS, free_list_seed=seed + 1)
+    return a, b
+
+
+@pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
+@pytest.mark.parametrize("D,R", [(128, 4), (64, 2), (256, 2)])
+def test_window_decode_parity(mode, D, R):
+    print(f"\ncase window_decode mode={mode} D={D} R={R}", flush=True)
+    W, H, steps = 100, 2, 24
+    rng = np.random.default_rng(D + R)
+    pools = _pools(mode, H, D, 64, W, seed=D)
+    fills = [[70, 64, 30], [5], [200, 3]]
+    sl = []
+    for pool in pools:
+        ss = Seqs(pool, 3, 420, np.random.default_rng(7))
+        for b, chunks in enumerate(fills):
+            for L in chunks:
+                ss.append(b, L)
+        sl.append(ss)
+    for step in range(steps):
+        for ss in sl:
+            for b in range(3):
+                ss.append(b, 1)
+        if step % 6 == 5 or step == 0:
+            _check(pools, sl, W, 1, mode, rng, R)
+    # the windowed pool holds only the blocks of each window (+ the partly filled last one)
+    used = pools[0].stats()["blocks_used"]
+    assert used <= 3 * ((W + 62) // 64 + 1), used
+    for p in pools:
+        p.close()
+
+
+@pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
+def test_window_chunk_parity(mode):
+    """Chunks straddling the window (RotatingKVCacheTests.swift:77-113 with
+    64-token blocks): the chunk's rows on MFMA when R * L > 8."""
+    print(f"\ncase window_chunks mode={mode}", flush=True)
+    W, H, D, R = 100, 2, 64, 4
+    rng = np.random.default_rng(11)
+    pools = _pools(mode, H, D, 64, W, seed=3)
+    sl = [Seqs(p, 1, 600, np.random.default_rng(9)) for p in pools]
+    for L in [50, 30, 120, 1, 10, 90, 60, 200, 2]:
+        for ss in sl:
+            ss.append(0, L)
+        _check(pools, sl, W, L, mode, rng, R, tol_pair=1e-3)
+    for p in pools:
+        p.close()
+
+
+def test_window_truncate_then_decode():
+    """After a rollback inside the retained tail the first retained token
+    binds (fewer than window keys visible), as in RotatingKVCacheTests
+    .swift:133-161."""
+    print("\ncase window_truncate", flush=True)
+    W, H, D, R = 100, 2, 128, 4
+    rng = np.random.default_rng(13)
+    pools = _pools("affine_g64", H, D, 32, W, seed=5)
+    sl = [Seqs(p, 2, 400, np.random.default_rng(17)) for p in pools]
+    for ss in sl:
+        ss.append(0, 250)
+        ss.append(0, 50)   # trims to the last 99 of 250 first
+        ss.append(1, 120)
+        ss.append(1, 1)
+        ss.truncate(0, 230)
+        ss.append(0, 1)
+        ss.append(1, 1)
+    _, start = O.rotating_retained_start(sl[0].ops[0], W)
+    assert start == 151 and sl[0].len[0] - start < W  # the start binds
+    _check(pools, sl, W, 1, "affine_g64", rng, R)
+    for p in pools:
+        p.close()

@@ -366,3 +366,54 @@ def test_rope_turns_compose(oracle):
     direct = oracle.rope_rows(x, dt, np.full(50, 40), tab)
     a, b = oracle.bits_to_f32(twice, dt), oracle.bits_to_f32(direct, dt)
     assert np.abs(a - b).max() <= 4 * 2.0 ** -11 * np.abs(b).max()
+
+
+# ---- sliding-window layers: pins from the reference's own tests
+
+def _visible(rows, k_total):
+    return [[k for k in range(k_total) if lo <= k < hi] for lo, hi in rows]
+
+
+def test_sliding_window_rows_reference_mask_vectors(oracle):
+    # SlidingWindowMaskTests.swift:17-30: newLen 4, cacheLen 0, window 2
+    assert _visible(oracle.sliding_window_rows(4, 0, 2), 4) == [[0], [0, 1], [1, 2], [2, 3]]
+    # :32-43: total 3 <= window 10 -> the plain causal mask
+    assert _visible(oracle.sliding_window_rows(3, 0, 10), 3) == [[0], [0, 1], [0, 1, 2]]
+    # :45-53: newLen 1, cacheLen 600, window 512: keys 89..600, exactly 512 visible
+    (row,) = _visible(oracle.sliding_window_rows(1, 600, 512), 601)
+    assert row[0] == 89 and row[-1] == 600 and len(row) == 512 and 88 not in row
+
+
+def test_attention_window_against_masked_softmax(oracle):
+    rng = np.random.default_rng(3)
+    T, D = 23, 8
+    q, k, v = rng.standard_normal((5, D)), rng.standard_normal((T, D)), rng.standard_normal((T, D))
+    lo, hi = [0, 4, 9, 17, 22], [3, 12, 20, 23, 23]
+    got = oracle.attention_window_f64(q, k, v, lo, hi, 0.3)
+    s = q @ k.T * 0.3
+    mask = np.array([[lo[r] <= t < hi[r] for t in range(T)] for r in range(5)])
+    s = np.where(mask, s, -np.inf)
+    p = np.exp(s - s.max(axis=1, keepdims=True))
+    want = (p / p.sum(axis=1, keepdims=True)) @ v
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    # a one-key window is that key's value row
+    np.testing.assert_allclose(oracle.attention_window_f64(q[:1], k, v, [7], [8], 1.0)[0], v[7], rtol=0, atol=1e-15)
+
+
+def test_rotating_retained_start_reference_vectors(oracle):
+    # RotatingKVCacheTests.swift:115-131: window 4, ten single appends keep the
+    # last min(t + 1, 4) tokens
+    for t in range(10):
+        total, start = oracle.rotating_retained_start([("append", 1)] * (t + 1), 4)
+        assert total == t + 1 and total - start == min(t + 1, 4)
+    # :133-161: truncate to 8 keeps 6, 7; one more append keeps 6, 7, 8
+    ops = [("append", 1)] * 10
+    assert oracle.rotating_retained_start(ops + [("truncate", 8)], 4) == (8, 6)
+    assert oracle.rotating_retained_start(ops + [("truncate", 8), ("append", 1)], 4) == (9, 6)
+    assert oracle.rotating_retained_start(ops + [("truncate", 6)], 4) == (6, 6)
+    with pytest.raises(ValueError):
+        oracle.rotating_retained_start(ops + [("truncate", 5)], 4)
+    # chunked appends (RotatingKVCacheTests.swift:77-113): retained before each
+    # append is min(retained, window - 1)
+    total, start = oracle.rotating_retained_start([("append", L) for L in (5, 3, 12, 1, 9, 6)], 8)
+    assert (total, total - start) == (36, 7 + 6)
