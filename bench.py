@@ -57,6 +57,9 @@ WORKLOADS = {
     # its K/V appended into a fresh sequence) at every step, no epoch restack
     "qwen3-14b-b32-continuous": dict(kind="continuous", layers=40, Hq=40, Hkv=8, D=128, B=32, lo=512, hi=8192,
                                      churn=1),
+    # the sliding-window layers of a Gemma-3-12B-shaped model (window 1024), contexts as the headline
+    "gemma3-12b-sliding-b32": dict(kind="window", layers=40, Hq=16, Hkv=8, D=256, B=32, lo=512, hi=8192,
+                                   window=1024),
 }
 
 
@@ -193,7 +196,7 @@ def main():
         del x, y
     w = WORKLOADS[args.workload]
     rec = {"decode": run_decode, "verify": run_verify, "shared_prefix": run_shared_prefix,
-           "continuous": run_continuous}[w["kind"]](args, w)
+           "continuous": run_continuous, "window": run_window}[w["kind"]](args, w)
     print(json.dumps(rec))
 
 
@@ -630,6 +633,104 @@ def run_continuous(args, w):
                                "rows_tokens": int(lns.sum())}}
     rec = _record(args, w, env, gbs_step, ms_step, config, roofline, extra)
     del keep, snap
+    env.pool.close()
+    return rec
+
+
+def run_window(args, w):
+    """Decode steps of sliding-window layers: a pool with the window option
+    (each append first drops the blocks below the sequence's last window - 1
+    tokens), per layer the new token's quantize-append and windowed decode
+    attention over the retained window."""
+    layers, Hq, Hkv, D, B, W = w["layers"], w["Hq"], w["Hkv"], w["D"], w["B"], w["window"]
+    t = None
+    rng = np.random.default_rng(args.seed)
+    lens0 = rng.integers(w["lo"], w["hi"] + 1, size=B).astype(np.int64)
+    total_steps = args.warmup + args.steps + 1
+    max_len_final = int(lens0.max()) + total_steps
+    max_blocks = (max_len_final + 63) // 64
+    num_blocks = int(sum((int(x) + 63) // 64 for x in lens0)) + B * 4 + 16
+    env = Env(args, w, num_blocks)
+    t = env.torch
+    env.pool.set_option(env.KL.OPT_WINDOW, W)
+    seqs = [env.pool.seq_create() for _ in range(B)]
+    env.fill(seqs, [int(x) for x in lens0])
+    st = StepTables(env, B, max_blocks, 1)
+    starts_ring = [t.empty((B,), dtype=t.int32).pin_memory() for _ in range(3)]
+    d_starts = t.empty((B,), dtype=t.int32, device=env.dev)
+    q_all = env.randn_bf16((layers, B, Hq, 1, D))
+    k_new = env.randn_bf16((layers, B, Hkv, 1, D))
+    v_new = env.randn_bf16((layers, B, Hkv, 1, D))
+    out = t.empty((B, Hq, 1, D), dtype=t.bfloat16, device=env.dev)
+    need = ctypes.c_size_t()
+    env.KL.check(env.lib.krill_window_workspace_size(env.h, B, Hq, 1, max_blocks, max_len_final, W,
+                                                     ctypes.byref(need)))
+    ws = t.empty(max(need.value, 1), dtype=t.uint8, device=env.dev)
+    scale = ctypes.c_float(1.0 / math.sqrt(D))
+    seqs_np = np.array(seqs, np.int32)
+    one = np.empty(1, np.int32)
+    cur_len = [int(x) for x in lens0]
+    KL, lib, h, sp = env.KL, env.lib, env.h, env.sp
+
+    def attend(layer, mx):
+        KL.check(lib.krill_attention_windowed(h, layer, q_all[layer].data_ptr(), 1, st.d_tables.data_ptr(),
+                                              st.d_lens.data_ptr(), d_starts.data_ptr(), W, B, max_blocks, mx, Hq,
+                                              scale, out.data_ptr(), KL.DTYPE_BF16, ws.data_ptr(), need.value, sp))
+
+    def step(i):
+        j, ps, pt, pl = st.host(i)
+        for b in range(B):
+            KL.check(lib.krill_seq_reserve_append(h, seqs[b], 1, env.i32p(one)))
+            ps[b, 0] = one[0]
+            cur_len[b] += 1
+        KL.check(lib.krill_batch_tables(h, env.i32p(seqs_np), B, max_blocks, env.i32p(pt), env.i32p(pl)))
+        KL.check(lib.krill_batch_starts(h, env.i32p(seqs_np), B, env.i32p(starts_ring[j].numpy())))
+        d_starts.copy_(starts_ring[j], non_blocking=True)
+        st.upload(j, slots=True)
+        mx = max(cur_len)
+        for layer in range(layers):
+            KL.check(lib.krill_quantize_append(h, layer, k_new[layer].data_ptr(), v_new[layer].data_ptr(),
+                                               st.d_slots.data_ptr(), B, 1, sp))
+            attend(layer, mx)
+
+    for i in range(args.warmup):
+        step(i)
+    t.cuda.synchronize()
+    ms_step, wall = _timed(env, lambda i: step(args.warmup + i), 0, args.steps)
+    per_tok = env.per_tok
+    vis = sum(min(n, W) for n in cur_len)  # keys each decode row sees
+    qo_layer = B * Hq * D * 2 * 2
+    app_layer = B * (2 * Hkv * D * 2 + per_tok)
+    step_bytes = layers * (vis * per_tok + qo_layer + app_layer)
+    gbs_step = step_bytes / (ms_step * 1e-3) / 1e9
+    mx = max(cur_len)
+    attn_ms = _time_calls(env, lambda layer: attend(layer, mx), args.kernel_reps)
+    launch_bytes = vis * per_tok + qo_layer
+    stats = env.pool.stats()
+    config = {
+        "workload": f"{args.workload}: {layers} sliding-window layers, window {W}, Hq {Hq}, Hkv {Hkv}, D {D}, B {B}, "
+                    f"context U[{w['lo']},{w['hi']}], {args.quant} int8, pool with the window option (blocks below "
+                    "each window freed); step = per layer quantize-append 1 token/seq + windowed decode attention",
+        "layers": layers, "Hq": Hq, "Hkv": Hkv, "head_dim": D, "batch": B, "quant": args.quant, "window": W,
+        "context_mean": float(np.mean(lens0)), "num_blocks": num_blocks,
+    }
+    roofline = {
+        "bound": "hbm",
+        "kernel": "windowed decode attention call (k_window_view + k_attn_valu + k_attn_merge_flat), one layer; "
+                  "bytes of the keys the rows see",
+        "achieved": round(launch_bytes / (attn_ms * 1e-3) / 1e9, 2),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(launch_bytes / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "bytes_per_launch": int(launch_bytes),
+        "avg_launch_ms": round(attn_ms, 5),
+    }
+    extra = {"tokens_per_s": round(B / (ms_step * 1e-3), 1), "hbm_frac_step": round(gbs_step / HBM_PEAK_GBS, 4),
+             "blocks_held_after": stats["blocks_used"],
+             "blocks_full_history": int(sum((n + 63) // 64 for n in cur_len)), "wall_s_timed": round(wall, 4)}
+    rec = _record(args, w, env, gbs_step, ms_step, config, roofline, extra)
+    del q_all, k_new, v_new, out, ws
     env.pool.close()
     return rec
 
