@@ -491,39 +491,97 @@ __global__ __launch_bounds__(256) void k_gather_dequant(LayerView lv, const int3
 // gather; restoreQuantized (QuantizedKVCache.swift:122-129) and the int8
 // scatterBack slice (ContinuousBatcher.swift:743-801).
 // ---------------------------------------------------------------------------
+// One workgroup per (64-row chunk of the source rows, head, sequence).  A
+// chunk whose 64 slots are one whole block in order (a restore into fresh
+// blocks) is written block-wise: K as 16-byte pieces, V rows staged in LDS
+// and written in the pool's transposed order as 16-byte pieces, metadata as
+// words.  Any other chunk goes row by row (one wave per row, byte stores).
+// Slots < 0 and source rows outside [0, S_in) are skipped.
 template <int D, int G>
 __global__ __launch_bounds__(256) void k_scatter(LayerView lv, const uint8_t *__restrict__ keys,
                                                  const uint8_t *__restrict__ values,
                                                  const uint16_t *__restrict__ ks, const uint16_t *__restrict__ kz,
                                                  const uint16_t *__restrict__ vs, const uint16_t *__restrict__ vz,
-                                                 int32_t B, int32_t H, int32_t S_in,
-                                                 const int32_t *__restrict__ src_start,
+                                                 int32_t H, int32_t S_in, const int32_t *__restrict__ src_start,
                                                  const int32_t *__restrict__ slots, int32_t L) {
   constexpr int E = D / 64;
-  const int lane = threadIdx.x & 63;
-  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (w >= (int64_t)B * L * H) return;
-  const int h = (int)(w % H);
-  const int i = (int)((w / H) % L);
-  const int b = (int)(w / ((int64_t)H * L));
-  const int slot = slots[(int64_t)b * L + i];
-  const int st = src_start[b] + i;
-  if (slot < 0 || st < 0 || st >= S_in) return;
-  const int blk = slot >> 6, t = slot & 63;
-  if (blk >= lv.num_blocks) return;
-  const int64_t row = ((int64_t)b * H + h) * S_in + st;
-  uint8_t *reg = head_region(lv, blk, h);
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int d = lane * E + e;
-    reg[k_byte(t, d)] = keys[row * D + d];
-    reg[v_byte(D, t, d)] = values[row * D + d];
+  constexpr int CH = D / 16;  // 16-byte pieces per row
+  constexpr int VB = 64 * D;  // V bytes of one (block, head)
+  __shared__ __attribute__((aligned(16))) uint8_t vrow[VB];  // V rows [token][D]
+  __shared__ int whole_s;
+  const int x = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int i0 = 64 * x;
+  const int sst = src_start[b];
+  if (tid < 64) {  // wave 0, all lanes: is the chunk one whole block in order?
+    const int i = i0 + tid;
+    const int slot = i < L ? slots[(int64_t)b * L + i] : -1;
+    const int base = __shfl(slot, 0, 64);
+    const bool ok = i < L && sst + i >= 0 && sst + i < S_in && base >= 0 && (base & 63) == 0 &&
+                    (base >> 6) < lv.num_blocks && slot == base + tid;
+    const bool all = __all(ok);
+    if (tid == 0) whole_s = all ? 1 : 0;
   }
-  if (lane < G) {
-    const uint32_t km = (uint32_t)ks[row * G + lane] | ((uint32_t)kz[row * G + lane] << 16);
-    const uint32_t vm = (uint32_t)vs[row * G + lane] | ((uint32_t)vz[row * G + lane] << 16);
-    *reinterpret_cast<uint32_t *>(reg + km_offset(D) + ((t * G + lane) << 2)) = km;
-    *reinterpret_cast<uint32_t *>(reg + vm_offset(D, G) + ((t * G + lane) << 2)) = vm;
+  __syncthreads();
+  if (whole_s) {
+    uint8_t *reg = head_region(lv, slots[(int64_t)b * L + i0] >> 6, h);
+    const int64_t row0 = ((int64_t)b * H + h) * S_in + sst + i0;  // snapshot row of the chunk's first token
+    for (int p = tid; p < 64 * CH; p += 256) {
+      const int t = p & 63, c = p >> 6;
+      *reinterpret_cast<uint4 *>(reg + k_byte(t, 16 * c)) =
+          *reinterpret_cast<const uint4 *>(keys + (row0 + t) * D + 16 * c);
+      *reinterpret_cast<uint4 *>(vrow + t * D + 16 * c) =
+          *reinterpret_cast<const uint4 *>(values + (row0 + t) * D + 16 * c);
+    }
+    for (int p = tid; p < 64 * G; p += 256) {
+      const int t = p / G, g = p % G;
+      const int64_t m = (row0 + t) * G + g;
+      *reinterpret_cast<uint32_t *>(reg + km_offset(D) + ((t * G + g) << 2)) =
+          (uint32_t)ks[m] | ((uint32_t)kz[m] << 16);
+      *reinterpret_cast<uint32_t *>(reg + vm_offset(D, G) + ((t * G + g) << 2)) =
+          (uint32_t)vs[m] | ((uint32_t)vz[m] << 16);
+    }
+    __syncthreads();
+    // 16-byte piece q of the V region: token group tg, half hi (positions
+    // 16 hi .. 16 hi + 15), d = (q % 64) * E + (sel >> 1)  (v_pos_byte)
+    for (int q = tid; q < VB / 16; q += 256) {
+      const int tg = q / (2 * D), r = q % (2 * D);
+      const int sel = r >> 6, hi = sel & 1, d = (r & 63) * E + (sel >> 1);
+      uint32_t w[4];
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        uint32_t acc = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int tok = 32 * tg + vtok(16 * hi + 4 * qq + e);
+          acc |= (uint32_t)vrow[tok * D + d] << (8 * e);
+        }
+        w[qq] = acc;
+      }
+      *reinterpret_cast<uint4 *>(reg + v_offset(D) + 16 * q) = uint4{w[0], w[1], w[2], w[3]};
+    }
+    return;
+  }
+  for (int i = i0 + (tid >> 6); i < min(i0 + 64, L); i += 4) {  // row by row, one wave per row
+    const int slot = slots[(int64_t)b * L + i];
+    const int st = sst + i;
+    if (slot < 0 || st < 0 || st >= S_in) continue;
+    const int blk = slot >> 6, t = slot & 63;
+    if (blk >= lv.num_blocks) continue;
+    const int64_t row = ((int64_t)b * H + h) * S_in + st;
+    uint8_t *reg = head_region(lv, blk, h);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int d = lane * E + e;
+      reg[k_byte(t, d)] = keys[row * D + d];
+      reg[v_byte(D, t, d)] = values[row * D + d];
+    }
+    if (lane < G) {
+      const uint32_t km = (uint32_t)ks[row * G + lane] | ((uint32_t)kz[row * G + lane] << 16);
+      const uint32_t vm = (uint32_t)vs[row * G + lane] | ((uint32_t)vz[row * G + lane] << 16);
+      *reinterpret_cast<uint32_t *>(reg + km_offset(D) + ((t * G + lane) << 2)) = km;
+      *reinterpret_cast<uint32_t *>(reg + vm_offset(D, G) + ((t * G + lane) << 2)) = vm;
+    }
   }
 }
 
@@ -881,18 +939,18 @@ hipError_t launch_scatter(const PoolGeometry &g, int32_t layer, const void *keys
                           const void *ks, const void *kz, const void *vs, const void *vz, int32_t B,
                           int32_t S_in, const int32_t *src_start, const int32_t *slots, int32_t L,
                           hipStream_t st) {
-  const int64_t waves = (int64_t)B * L * g.Hkv;
-  if (waves == 0) return hipSuccess;
+  if ((int64_t)B * L * g.Hkv == 0) return hipSuccess;
+  if (B > 65535 || g.Hkv > 65535) return hipErrorInvalidValue;
   const LayerView lv = layer_view(g, layer);
-  const dim3 grid(wave_blocks(waves)), block(256);
+  const dim3 grid((unsigned)((L + 63) / 64), (unsigned)g.Hkv, (unsigned)B), block(256);
   auto *k8 = static_cast<const uint8_t *>(keys), *v8 = static_cast<const uint8_t *>(values);
   auto *a = static_cast<const uint16_t *>(ks), *bz = static_cast<const uint16_t *>(kz),
        *c = static_cast<const uint16_t *>(vs), *d = static_cast<const uint16_t *>(vz);
   KRILL_DISPATCH_D(g.D, {
     if (g.G == 1)
-      k_scatter<D, 1><<<grid, block, 0, st>>>(lv, k8, v8, a, bz, c, d, B, g.Hkv, S_in, src_start, slots, L);
+      k_scatter<D, 1><<<grid, block, 0, st>>>(lv, k8, v8, a, bz, c, d, g.Hkv, S_in, src_start, slots, L);
     else
-      k_scatter<D, D / 64><<<grid, block, 0, st>>>(lv, k8, v8, a, bz, c, d, B, g.Hkv, S_in, src_start, slots, L);
+      k_scatter<D, D / 64><<<grid, block, 0, st>>>(lv, k8, v8, a, bz, c, d, g.Hkv, S_in, src_start, slots, L);
   });
   return hipGetLastError();
 }

@@ -121,6 +121,34 @@ def test_scatter_restores_snapshot_bit_exact(mode):
 
 
 @pytest.mark.parametrize("mode", ["ref_row", "affine_g64"])
+def test_scatter_at_unaligned_offset_and_whole_blocks(mode):
+    """Rows restored behind 10 existing tokens (chunks straddle blocks: the
+    row path) and into a fresh sequence (whole blocks: the block path) leave
+    the same bytes as the source."""
+    print(f"\ncase scatter_offset mode={mode}", flush=True)
+    rng = np.random.default_rng(21)
+    H, D = 2, 128
+    pool = make_pool(H, D, mode, "bf16", blocks=40)
+    f = Filled(pool, [300], rng, "bf16")
+    tables, lens, _ = f.tables()
+    snap = pool.gather(0, tables, lens, 300)
+    head = Filled(pool, [10], rng, "bf16")
+    dst = head.seqs[0]
+    fresh = pool.seq_create()
+    slots = np.stack([pool.reserve_append(dst, 300), pool.reserve_append(fresh, 300)])
+    snap2 = {k: torch.cat([v, v]) for k, v in snap.items()}
+    pool.scatter(0, snap2, i32([0, 0]), i32(slots))
+    t2, n2 = pool.batch_tables([dst, fresh], (310 + 63) // 64)
+    got = pool.gather(0, i32(t2), i32(n2), 310)
+    torch.cuda.synchronize()
+    for k in snap:
+        a = snap[k].cpu().numpy()[0].view(np.uint8)
+        assert np.array_equal(got[k].cpu().numpy()[0, :, 10:310].view(np.uint8), a), k
+        assert np.array_equal(got[k].cpu().numpy()[1, :, :300].view(np.uint8), a), k
+    pool.close()
+
+
+@pytest.mark.parametrize("mode", ["ref_row", "affine_g64"])
 def test_gather_dequant_matches_oracle(mode):
     print(f"\ncase gather_dequant mode={mode}", flush=True)
     rng = np.random.default_rng(9)
