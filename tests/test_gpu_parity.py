@@ -303,3 +303,40 @@ def test_outlier_channels_long_context_shape():
     got, ref = _attn_case("affine_g64", 128, 4, 8, [9000, 20000], seed=20261205, outlier_frac=0.01)
     err = np.abs(got - ref).max()
     assert err <= ATOL, f"max abs error {err:.3e}"
+
+
+def test_long_context_uniform_keys_give_mean_of_values():
+    """Full long-context size (131072 tokens, the 128k MoE shape: Hkv 4, 8
+    query rows per KV head): with every key row equal all scores are equal,
+    so the output is the mean of the dequantized value rows -- a closed form
+    that checks the split over hundreds of waves and the merge at full size."""
+    print("\ncase long_context_uniform_keys", flush=True)
+    H, R, D = 4, 8, 128
+    lens = [131072, 65537]
+    rng = np.random.default_rng(20261205)
+    pool = make_pool(H, D, "affine_g64", "bf16", blocks=sum((T + 63) // 64 for T in lens) + 4)
+    seqs = [pool.seq_create() for _ in lens]
+    krow = rand_bits(rng, (H, 1, D), "bf16")
+    vals = []
+    C = 4096
+    for s, T in zip(seqs, lens):
+        v = rand_bits(rng, (H, T, D), "bf16", outlier_frac=0.01)
+        vals.append(v)
+        for t0 in range(0, T, C):
+            n = min(C, T - t0)
+            slots = pool.reserve_append(s, n)
+            k = np.ascontiguousarray(np.broadcast_to(krow, (H, n, D)))
+            pool.quantize_append(0, to_dev(k[None], "bf16"), to_dev(v[None, :, t0:t0 + n], "bf16"), i32(slots[None]))
+    t, n = pool.batch_tables(seqs, (max(lens) + 63) // 64)
+    q = rand_bits(rng, (len(lens), H * R, 1, D), "bf16")
+    out = pool.attention(0, to_dev(q, "bf16"), i32(t), i32(n), max(lens), 1.0 / np.sqrt(D))
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    mode = MODE["affine_g64"]
+    for b, v in enumerate(vals):
+        vq, vs, vz = O.quantize(v, DT["bf16"], mode)
+        mean = O.dequant_f64(vq, vs, vz, mode).mean(axis=1)  # [H, D]
+        want = np.repeat(mean, R, axis=0)                     # query head hq reads KV head hq // R
+        err = np.abs(got[b, :, 0] - want).max()
+        assert err <= ATOL, (b, err)
+    pool.close()
