@@ -333,20 +333,7 @@ __global__ __launch_bounds__(256) void k_append_newest(AttnArgs a) {
 // left_pad = 1 reproduces stackCachesLeftPaddedQuantized
 // (Sources/KrillEngine/BatchedDecode.swift:96-151): right-aligned rows,
 // u8 0 / fp16 0 padding.  left_pad = 0 is quantizedSnapshot() with a zero tail.
-// One wave per output (b, h, s) row.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ bool resolve_token(const int32_t *tables, const int32_t *lens, int b,
-                                              int max_blocks, int num_blocks, int S_out, int left_pad,
-                                              int s, int *blk_out, int *t_out) {
-  const int len = lens[b];
-  const int ti = left_pad ? s - (S_out - len) : s;
-  if (ti < 0 || ti >= len || (ti >> 6) >= max_blocks) return false;
-  const int blk = tables[(int64_t)b * max_blocks + (ti >> 6)];
-  if ((unsigned)blk >= (unsigned)num_blocks) return false;
-  *blk_out = blk;
-  *t_out = ti & 63;
-  return true;
-}
 
 // One workgroup per (token block, head, sequence): the block's K chunks go
 // out as 16-byte pieces (token t, d 16c..16c+15: contiguous in the pool's
@@ -446,43 +433,92 @@ __global__ __launch_bounds__(256) void k_gather(LayerView lv, const int32_t *__r
 // MODE_REF: f16(f16(f16(q) * s) + z), the two roundings of
 // QuantizedKVCache.dequantize (QuantizedKVCache.swift:200-204).
 // MODE_AFFINE: f16(s*q + b) rounded once.
+// Tiled as k_gather: one workgroup per (token block, head, sequence), 16 K
+// or V bytes (one scale group) -> 16 fp16 per piece, V through LDS; zero
+// workgroups clear the rows without a token.
+template <int D, int G, int MODE>
+__device__ __forceinline__ void dequant16(const uint8_t (&qb)[16], uint32_t meta, uint16_t *dst) {
+  const float sc = f16_bits_to_f32((uint16_t)(meta & 0xffffu)), zr = f16_bits_to_f32((uint16_t)(meta >> 16));
+  uint32_t w[8];
+#pragma unroll
+  for (int e = 0; e < 16; e += 2) {
+    uint16_t o[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const float q = (float)qb[e + u];
+      if constexpr (MODE == MODE_REF)
+        o[u] = f32_to_f16_bits(f16_bits_to_f32(f32_to_f16_bits(q * sc)) + zr);
+      else
+        o[u] = f32_to_f16_bits(sc * q + zr);
+    }
+    w[e / 2] = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+  }
+  reinterpret_cast<uint4 *>(dst)[0] = uint4{w[0], w[1], w[2], w[3]};
+  reinterpret_cast<uint4 *>(dst)[1] = uint4{w[4], w[5], w[6], w[7]};
+}
+
 template <int D, int G, int MODE>
 __global__ __launch_bounds__(256) void k_gather_dequant(LayerView lv, const int32_t *__restrict__ tables,
-                                                        const int32_t *__restrict__ lens, int32_t B,
-                                                        int32_t H, int32_t max_blocks, int32_t S_out,
-                                                        int32_t left_pad, uint16_t *k_out,
-                                                        uint16_t *v_out) {
-  constexpr int E = D / 64;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= (int64_t)B * H * S_out) return;
-  const int s = (int)(row % S_out);
-  const int h = (int)((row / S_out) % H);
-  const int b = (int)(row / ((int64_t)S_out * H));
-  int blk = 0, t = 0;
-  const bool valid = resolve_token(tables, lens, b, max_blocks, lv.num_blocks, S_out, left_pad, s, &blk, &t);
-  const uint8_t *reg = head_region(lv, blk, h);
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int d = lane * E + e;
-    uint16_t ko = 0, vo = 0;
-    if (valid) {
-      const int g = d / (D / G);
-      const uint32_t km = *reinterpret_cast<const uint32_t *>(reg + km_offset(D) + ((t * G + g) << 2));
-      const uint32_t vm = *reinterpret_cast<const uint32_t *>(reg + vm_offset(D, G) + ((t * G + g) << 2));
-      const float kq = (float)reg[k_byte(t, d)], vq = (float)reg[v_byte(D, t, d)];
-      const float kss = f16_bits_to_f32((uint16_t)(km & 0xffffu)), kzz = f16_bits_to_f32((uint16_t)(km >> 16));
-      const float vss = f16_bits_to_f32((uint16_t)(vm & 0xffffu)), vzz = f16_bits_to_f32((uint16_t)(vm >> 16));
-      if constexpr (MODE == MODE_REF) {
-        ko = f32_to_f16_bits(f16_bits_to_f32(f32_to_f16_bits(kq * kss)) + kzz);
-        vo = f32_to_f16_bits(f16_bits_to_f32(f32_to_f16_bits(vq * vss)) + vzz);
-      } else {
-        ko = f32_to_f16_bits(kss * kq + kzz);
-        vo = f32_to_f16_bits(vss * vq + vzz);
+                                                        const int32_t *__restrict__ lens, int32_t H,
+                                                        int32_t max_blocks, int32_t S_out, int32_t left_pad,
+                                                        int32_t nbx, uint16_t *k_out, uint16_t *v_out) {
+  constexpr int CH = D / 16;
+  constexpr int VB = 64 * D;
+  constexpr int DG = D / G;  // dims per scale group (a multiple of 16)
+  __shared__ __attribute__((aligned(16))) uint8_t vl[VB];
+  const int x = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int len = lens[b];
+  const int off = left_pad ? S_out - len : 0;
+  const int t_lo = max(0, -off), t_hi = min(len, S_out - off);
+  const int64_t row0 = ((int64_t)b * H + h) * S_out;
+  const uint4 zero4 = {0u, 0u, 0u, 0u};
+  if (x >= nbx) {
+    const int s0 = (x - nbx) * 64;
+    for (int p = tid; p < 64 * CH; p += 256) {
+      const int s = s0 + p / CH, c = p % CH;
+      const int ti = s - off;
+      if (s < S_out && (ti < t_lo || ti >= t_hi)) {
+        uint4 *kd = reinterpret_cast<uint4 *>(k_out + (row0 + s) * D + 16 * c);
+        uint4 *vd = reinterpret_cast<uint4 *>(v_out + (row0 + s) * D + 16 * c);
+        kd[0] = kd[1] = vd[0] = vd[1] = zero4;
       }
     }
-    k_out[row * D + d] = ko;
-    v_out[row * D + d] = vo;
+    return;
+  }
+  if (t_hi <= t_lo) return;
+  const int j = (t_lo >> 6) + x;
+  const int ta = max(64 * j, t_lo), tb = min(64 * j + 64, t_hi);
+  if (ta >= tb) return;
+  const int blk = j < max_blocks ? tables[(int64_t)b * max_blocks + j] : -1;
+  const bool valid = (unsigned)blk < (unsigned)lv.num_blocks;
+  const uint8_t *reg = valid ? head_region(lv, blk, h) : nullptr;
+  if (valid) {
+    for (int p = tid; p < VB / 16; p += 256)
+      *reinterpret_cast<uint4 *>(vl + 16 * p) = *reinterpret_cast<const uint4 *>(reg + v_offset(D) + 16 * p);
+  }
+  __syncthreads();
+  for (int p = tid; p < 64 * CH; p += 256) {
+    const int t = p / CH, c = p % CH;
+    const int ti = 64 * j + t;
+    if (ti < ta || ti >= tb) continue;
+    uint16_t *kd = k_out + (row0 + ti + off) * D + 16 * c;
+    uint16_t *vd = v_out + (row0 + ti + off) * D + 16 * c;
+    if (!valid) {
+      reinterpret_cast<uint4 *>(kd)[0] = reinterpret_cast<uint4 *>(kd)[1] = zero4;
+      reinterpret_cast<uint4 *>(vd)[0] = reinterpret_cast<uint4 *>(vd)[1] = zero4;
+      continue;
+    }
+    const int g = (16 * c) / DG;
+    const uint32_t km = *reinterpret_cast<const uint32_t *>(reg + km_offset(D) + ((t * G + g) << 2));
+    const uint32_t vm = *reinterpret_cast<const uint32_t *>(reg + vm_offset(D, G) + ((t * G + g) << 2));
+    const uint4 kq4 = *reinterpret_cast<const uint4 *>(reg + k_byte(t, 16 * c));
+    uint8_t kq[16], vq[16];
+    __builtin_memcpy(kq, &kq4, 16);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) vq[e] = vl[v_byte(D, t, 16 * c + e) - v_offset(D)];
+    dequant16<D, G, MODE>(kq, km, kd);
+    dequant16<D, G, MODE>(vq, vm, vd);
   }
 }
 
@@ -921,16 +957,19 @@ hipError_t launch_gather(const PoolGeometry &g, int32_t layer, const int32_t *ta
 hipError_t launch_gather_dequant(const PoolGeometry &g, int32_t layer, const int32_t *tables,
                                  const int32_t *lens, int32_t B, int32_t max_blocks, int32_t S_out,
                                  int32_t left_pad, void *k_out, void *v_out, hipStream_t st) {
-  const int64_t waves = (int64_t)B * g.Hkv * S_out;
-  if (waves == 0) return hipSuccess;
+  if ((int64_t)B * g.Hkv * S_out == 0) return hipSuccess;
+  if (B > 65535 || g.Hkv > 65535) return hipErrorInvalidValue;
   const LayerView lv = layer_view(g, layer);
-  const dim3 grid(wave_blocks(waves)), block(256);
+  const int32_t tiles = (S_out + 63) / 64, nbx = tiles + 1;
+  const dim3 grid((unsigned)(nbx + tiles), (unsigned)g.Hkv, (unsigned)B), block(256);
   auto *ko = static_cast<uint16_t *>(k_out), *vo = static_cast<uint16_t *>(v_out);
   KRILL_DISPATCH_D(g.D, {
     if (g.mode == MODE_REF)
-      k_gather_dequant<D, 1, MODE_REF><<<grid, block, 0, st>>>(lv, tables, lens, B, g.Hkv, max_blocks, S_out, left_pad, ko, vo);
+      k_gather_dequant<D, 1, MODE_REF><<<grid, block, 0, st>>>(lv, tables, lens, g.Hkv, max_blocks, S_out, left_pad,
+                                                              nbx, ko, vo);
     else
-      k_gather_dequant<D, D / 64, MODE_AFFINE><<<grid, block, 0, st>>>(lv, tables, lens, B, g.Hkv, max_blocks, S_out, left_pad, ko, vo);
+      k_gather_dequant<D, D / 64, MODE_AFFINE><<<grid, block, 0, st>>>(lv, tables, lens, g.Hkv, max_blocks, S_out,
+                                                                       left_pad, nbx, ko, vo);
   });
   return hipGetLastError();
 }
