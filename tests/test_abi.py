@@ -101,3 +101,36 @@ def test_batch_tables_and_block_table():
         p.batch_tables([a], 2)
     assert e.value.code == L.KRILL_E_RANGE
     assert np.all(np.isin(p.block_table(a), np.arange(32)))
+
+
+def test_cascade_and_window_entry_points_validate_on_host():
+    p = krill_amd.KVPool(1, 8, 128, 64, host_only=True)
+    lib = L.lib()
+    out = ctypes.c_size_t()
+    # shared-prefix cascade: a prefix of at least one block; sizes grow with the batch
+    assert lib.krill_shared_prefix_workspace_size(p.handle, 4, 40, 0, 100, ctypes.byref(out)) == L.KRILL_E_INVAL
+    assert lib.krill_shared_prefix_workspace_size(p.handle, 4, 40, 64, 100, ctypes.byref(out)) == L.KRILL_OK
+    small = out.value
+    assert lib.krill_shared_prefix_workspace_size(p.handle, 64, 40, 64, 100, ctypes.byref(out)) == L.KRILL_OK
+    assert out.value > small
+    # windowed attention: window >= 2, workspace holds the per-call table view
+    assert lib.krill_window_workspace_size(p.handle, 4, 40, 1, 128, 8192, 1, ctypes.byref(out)) == L.KRILL_E_INVAL
+    assert lib.krill_window_workspace_size(p.handle, 4, 40, 1, 128, 8192, 1024, ctypes.byref(out)) == L.KRILL_OK
+    assert out.value >= 4 * 128 * 4
+    dummy = ctypes.c_void_p(16)
+    rc = lib.krill_attention_windowed(p.handle, 0, dummy, 1, dummy, dummy, None, 1024, 1, 1, 64, 8, 0.1, dummy,
+                                      L.DTYPE_F32, dummy, 1 << 20, None)
+    assert rc == L.KRILL_E_STATE and "host-only" in L.last_error()
+    rc = lib.krill_decode_attention_shared_prefix(p.handle, 0, dummy, dummy, 1, dummy, dummy, 1, 1, 1, 8, 0.1,
+                                                  dummy, L.DTYPE_F32, dummy, 1 << 20, None)
+    assert rc == L.KRILL_E_STATE
+    # batch_starts: bad handles are errors, not crashes
+    seqs = np.array([12345], np.int32)
+    starts = np.zeros(1, np.int32)
+    rc = lib.krill_batch_starts(p.handle, seqs.ctypes.data_as(L.PI32), 1, starts.ctypes.data_as(L.PI32))
+    assert rc == L.KRILL_E_INVAL
+    s = p.seq_create()
+    assert p.batch_starts([s]).tolist() == [0]
+    with pytest.raises(KrillError):
+        p.set_option(L.OPT_WINDOW, -5)
+    p.close()
