@@ -716,7 +716,7 @@ def run_window(args, w):
     }
     roofline = {
         "bound": "hbm",
-        "kernel": "windowed decode attention call (k_window_view + k_attn_valu + k_attn_merge_flat), one layer; "
+        "kernel": "windowed decode attention call (k_attn_valu window variant + k_attn_merge_flat), one layer; "
                   "bytes of the keys the rows see",
         "achieved": round(launch_bytes / (attn_ms * 1e-3) / 1e9, 2),
         "peak": HBM_PEAK_GBS,

@@ -58,8 +58,9 @@ struct AttnArgs {
   int32_t len_const;     // >= 0: every sequence holds this many tokens (lens not read)
   int32_t causal;        // 1: query row j sees keys [0, len - Lq + j]; 0: every key
   int32_t partial_only;  // 1: every segment leaves a partial, none writes the output
-  // sliding window (win_start null: none): query row j of sequence b sees
-  // keys [max(win_start[b], len - Lq + j - window + 1), len - Lq + j]
+  // sliding window (window > 0): query row j of sequence b sees keys
+  // [max(win_start[b], len - Lq + j - window + 1), len - Lq + j]
+  // (win_start null: 0)
   const int32_t *win_start;
   int32_t window;
 };
@@ -171,6 +172,34 @@ __device__ __forceinline__ void rope_pair_words(uint32_t &lo, uint32_t &hi, floa
 
 // Tokens held by sequence b.
 __device__ __forceinline__ int len_of(const AttnArgs &a, int b) { return a.len_const >= 0 ? a.len_const : a.lens[b]; }
+// Sliding window: the kernels see each sequence from the block holding its
+// first visible key, fb = max(start, len - Lq - window + 1, 0) / 64: length
+// len - 64 fb, table entries from column fb, first retained key start - 64 fb.
+__device__ __forceinline__ int win_first_block(const AttnArgs &a, int b, int len) {
+  const int st = a.win_start ? a.win_start[b] : 0;
+  const int lo = max(max(st, len - a.Lq - a.window + 1), 0);
+  return min(lo >> 6, a.max_blocks);
+}
+// Length of sequence b as the kernels see it.
+template <bool WIN>
+__device__ __forceinline__ int seq_len_view(const AttnArgs &a, int b) {
+  const int len = len_of(a, b);
+  if constexpr (WIN) return len - 64 * win_first_block(a, b, len);
+  return len;
+}
+__device__ __forceinline__ int seq_len_any(const AttnArgs &a, int b) {
+  return a.window > 0 ? seq_len_view<true>(a, b) : len_of(a, b);
+}
+// Table column of the first block the kernels see and the first retained key
+// relative to it (window only).
+template <bool WIN>
+__device__ __forceinline__ int table_offset(const AttnArgs &a, int b) {
+  if constexpr (WIN) return win_first_block(a, b, len_of(a, b));
+  return 0;
+}
+__device__ __forceinline__ int win_view_start(const AttnArgs &a, int b) {
+  return (a.win_start ? a.win_start[b] : 0) - 64 * win_first_block(a, b, len_of(a, b));
+}
 // Query vector (head hq, position j) of sequence b.
 __device__ __forceinline__ const uint16_t *q_row(const AttnArgs &a, int b, int hq, int j) {
   return a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + (int64_t)j * a.q_sj;
@@ -225,7 +254,7 @@ __device__ __forceinline__ int flat_total_and_start(const AttnArgs &a, int b, in
   int carry = 0;
   for (int c0 = 0; c0 < a.B; c0 += 64) {
     const int bb = c0 + lane;
-    const int nbv = bb < a.B ? seq_blocks_rg(a, len_of(a, bb), rg) : 0;
+    const int nbv = bb < a.B ? seq_blocks_rg(a, seq_len_any(a, bb), rg) : 0;
     const int incl = wave_incl_scan(nbv) + carry;
     if (b >= c0 && b < c0 + 64) {
       start_out = __builtin_amdgcn_readlane(incl - nbv, b - c0);

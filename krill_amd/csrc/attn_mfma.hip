@@ -81,13 +81,13 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
 
   // ---- this wave's flat blocks [i0, iend) of the (head, row group) order
   const int W = a.waves;
-  int c0 = 0, lenv = lane < a.B ? len_of(a, lane) : 0;
+  int c0 = 0, lenv = lane < a.B ? seq_len_view<WIN>(a, lane) : 0;
   int nbv = seq_blocks_rg(a, lenv, rg);
   int incl = wave_incl_scan(nbv);
   int T = __builtin_amdgcn_readlane(incl, 63);
   for (int cc = 64; cc < a.B; cc += 64) {
     const int bb = cc + lane;
-    T += __builtin_amdgcn_readfirstlane(wave_allsum_int(bb < a.B ? seq_blocks_rg(a, len_of(a, bb), rg) : 0));
+    T += __builtin_amdgcn_readfirstlane(wave_allsum_int(bb < a.B ? seq_blocks_rg(a, seq_len_view<WIN>(a, bb), rg) : 0));
   }
   const int Wt = min(W, T);  // every participating wave holds >= 1 block
   if (wv >= Wt) return;
@@ -99,7 +99,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
     for (c0 = 0; c0 < a.B; c0 += 64) {
       if (c0 > 0) {
         const int bb = c0 + lane;
-        lenv = bb < a.B ? len_of(a, bb) : 0;
+        lenv = bb < a.B ? seq_len_view<WIN>(a, bb) : 0;
         nbv = seq_blocks_rg(a, lenv, rg);
         incl = wave_incl_scan(nbv) + carry;
       }
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
     }
   }
   if (b < 0) return;
-  auto seq_len = [&](int bs) -> int { return bs - c0 < 64 ? __builtin_amdgcn_readlane(lenv, bs - c0) : len_of(a, bs); };
+  auto seq_len = [&](int bs) -> int { return bs - c0 < 64 ? __builtin_amdgcn_readlane(lenv, bs - c0) : seq_len_view<WIN>(a, bs); };
 
   // block-table entries of flat blocks i0 .. iend-1 (<= 64), lane j: block i0 + j
   int tab = 0, iend_eff = iend;
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
     while (bs < a.B && ss < iend) {
       const int nbs = seq_blocks_rg(a, seq_len(bs), rg);
       if (f < iend && f >= ss && f < ss + nbs) {
-        const int phys = a.tables[(int64_t)bs * a.max_blocks + (f - ss)];
+        const int phys = a.tables[(int64_t)bs * a.max_blocks + table_offset<WIN>(a, bs) + (f - ss)];
         tab = (unsigned)phys < (unsigned)a.lv.num_blocks ? phys : 0;
       }
       ss += nbs;
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
     const int lim_lo = key_limit(a, len, rbase / a.R);  // keys seen by the group's first row
     int lo[NRT], wst = 0, lo_hi = 0;  // sliding window: per-row first key, first retained key, group's largest
     if constexpr (WIN) {
-      wst = a.win_start[b];
+      wst = win_view_start(a, b);
 #pragma unroll
       for (int rt = 0; rt < NRT; ++rt) {
         const int r = rbase + 16 * rt + n;
@@ -563,7 +563,7 @@ static hipError_t launch_mfma_nrt(const AttnArgs &args, int NRT, dim3 grid, hipS
     case 1:
       if (args.rope_cs)
         k_attn_mfma<D, MODE, 1, 1><<<grid, dim3(64), 0, st>>>(args);
-      else if (args.win_start)
+      else if (args.window > 0)
         k_attn_mfma<D, MODE, 1, 2><<<grid, dim3(64), 0, st>>>(args);
       else
         k_attn_mfma<D, MODE, 1, 0><<<grid, dim3(64), 0, st>>>(args);
@@ -571,7 +571,7 @@ static hipError_t launch_mfma_nrt(const AttnArgs &args, int NRT, dim3 grid, hipS
     case 2:
       if (args.rope_cs)
         k_attn_mfma<D, MODE, 2, 1><<<grid, dim3(64), 0, st>>>(args);
-      else if (args.win_start)
+      else if (args.window > 0)
         k_attn_mfma<D, MODE, 2, 2><<<grid, dim3(64), 0, st>>>(args);
       else
         k_attn_mfma<D, MODE, 2, 0><<<grid, dim3(64), 0, st>>>(args);

@@ -217,13 +217,13 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   // Sequence lengths of the first 64 sequences stay in `lenv` (lane j:
   // sequence c0 + j, c0 = the chunk holding the wave's first sequence).
   const int W = a.waves;
-  int c0 = 0, lenv = lane < a.B ? len_of(a, lane) : 0;
+  int c0 = 0, lenv = lane < a.B ? seq_len_view<WIN>(a, lane) : 0;
   int nbv = seq_blocks(a, lenv);
   int incl = wave_incl_scan(nbv);
   int T = __builtin_amdgcn_readlane(incl, 63);
   for (int cc = 64; cc < a.B; cc += 64) {
     const int bb = cc + lane;
-    T += __builtin_amdgcn_readfirstlane(wave_allsum_int(bb < a.B ? seq_blocks(a, len_of(a, bb)) : 0));
+    T += __builtin_amdgcn_readfirstlane(wave_allsum_int(bb < a.B ? seq_blocks(a, seq_len_view<WIN>(a, bb)) : 0));
   }
   // At most T waves take part, so every participating wave holds at least
   // one block (the merge relies on it: each wave between a sequence's first
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     for (c0 = 0; c0 < a.B; c0 += 64) {
       if (c0 > 0) {
         const int bb = c0 + lane;
-        lenv = bb < a.B ? len_of(a, bb) : 0;
+        lenv = bb < a.B ? seq_len_view<WIN>(a, bb) : 0;
         nbv = seq_blocks(a, lenv);
         incl = wave_incl_scan(nbv) + carry;
       }
@@ -253,7 +253,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     }
   }
   if (b < 0) return;
-  auto seq_len = [&](int bs) -> int { return bs - c0 < 64 ? __builtin_amdgcn_readlane(lenv, bs - c0) : len_of(a, bs); };
+  auto seq_len = [&](int bs) -> int { return bs - c0 < 64 ? __builtin_amdgcn_readlane(lenv, bs - c0) : seq_len_view<WIN>(a, bs); };
 
   // Decode step with the append fused: the wave that reads a sequence's last
   // block writes the sequence's newest token there (position len - 1; not
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     while (bs < a.B && ss < iend) {
       const int nbs = seq_blocks(a, seq_len(bs));
       if (f < iend && f >= ss && f < ss + nbs) {
-        const int phys = a.tables[(int64_t)bs * a.max_blocks + (f - ss)];
+        const int phys = a.tables[(int64_t)bs * a.max_blocks + table_offset<WIN>(a, bs) + (f - ss)];
         tab_ok = (unsigned)phys < (unsigned)a.lv.num_blocks;
         tab = tab_ok ? phys : 0;
       }
@@ -448,7 +448,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     for (int r = 0; r < NR; ++r) lim[r] = key_limit(a, len, r / a.R);
     int lo[NR], wst = 0;  // sliding window: first key each row sees, first retained key
     if constexpr (WIN) {
-      wst = a.win_start[b];
+      wst = win_view_start(a, b);
 #pragma unroll
       for (int r = 0; r < NR; ++r) lo[r] = max(wst, len - a.Lq + r / a.R - a.window + 1);
     }
@@ -756,7 +756,7 @@ template <int D, int MODE, int NR>
 static void launch_one(const AttnArgs &args, int B, dim3 grid, hipStream_t st) {
   if (args.rope_cs)
     k_attn_valu<D, NR, MODE, 1><<<grid, dim3(64), 0, st>>>(args);
-  else if (args.win_start)
+  else if (args.window > 0)
     k_attn_valu<D, NR, MODE, 2><<<grid, dim3(64), 0, st>>>(args);
   else
     k_attn_valu<D, NR, MODE, 0><<<grid, dim3(64), 0, st>>>(args);

@@ -737,11 +737,10 @@ int32_t krill_decode_append_attention_shared_prefix(krill_pool_t pool, int32_t l
                            max_blocks, max_suffix_len, Hq, scale, dev_out, out_dtype, dev_ws, ws_bytes, stream, nt);
 }
 
-// Plan of a sliding-window call (the view's lengths are at most
-// Lq + window + 62) and its workspace: the attention's, then the view.
+// Plan of a sliding-window call: the lengths the kernels see (from the block
+// holding each sequence's first visible key) are at most Lq + window + 62.
 static int32_t plan_windowed(krill_pool_t pool, int32_t B, int32_t Hq, int32_t Lq, int32_t max_blocks,
-                             int32_t max_seq_len, int32_t window, krill::AttnPlan *plan, size_t *view_off,
-                             size_t *total) {
+                             int32_t max_seq_len, int32_t window, krill::AttnPlan *plan, size_t *total) {
   if (B < 0 || Lq < 1 || max_blocks < 0 || max_seq_len < 0) return fail(KRILL_E_INVAL, "bad B, Lq, width or length");
   if (window < 2) return fail(KRILL_E_INVAL, "sliding window of %d tokens (>= 2)", window);
   const int64_t vmax = std::min<int64_t>(max_seq_len, (int64_t)Lq + window + 62);
@@ -749,8 +748,7 @@ static int32_t plan_windowed(krill_pool_t pool, int32_t B, int32_t Hq, int32_t L
                                     plan);
   if (r == -2) return fail(KRILL_E_UNSUPPORTED, "VALU path handles at most 8 query rows per KV head");
   if (r != 0) return fail(KRILL_E_INVAL, "Hq %d not a multiple of %d KV heads, or bad B/Lq/length", Hq, pool->geom.Hkv);
-  *view_off = (plan->ws_bytes + 255) & ~(size_t)255;
-  *total = *view_off + ((size_t)B * (size_t)max_blocks + 2 * (size_t)B) * sizeof(int32_t);
+  *total = plan->ws_bytes;
   return KRILL_OK;
 }
 
@@ -760,8 +758,8 @@ int32_t krill_window_workspace_size(krill_pool_t pool, int32_t B, int32_t Hq, in
   if (int32_t rc = check_pool(pool)) return rc;
   if (!bytes_out) return fail(KRILL_E_INVAL, "bytes_out is NULL");
   krill::AttnPlan plan;
-  size_t off = 0, total = 0;
-  if (int32_t rc = plan_windowed(pool, B, Hq, Lq, max_blocks, max_seq_len, window, &plan, &off, &total)) return rc;
+  size_t total = 0;
+  if (int32_t rc = plan_windowed(pool, B, Hq, Lq, max_blocks, max_seq_len, window, &plan, &total)) return rc;
   *bytes_out = total;
   return KRILL_OK;
 }
@@ -783,9 +781,10 @@ int32_t krill_attention_windowed(krill_pool_t pool, int32_t layer, const void *d
     return fail(KRILL_E_RANGE, "max_seq_len %d exceeds the %d-block table width", max_seq_len, max_blocks);
   if (B > 65535) return fail(KRILL_E_RANGE, "batch of %d sequences (at most 65535)", B);
   krill::AttnPlan plan;
-  size_t off = 0, total = 0;
-  if (int32_t rc = plan_windowed(pool, B, Hq, Lq, max_blocks, max_seq_len, window, &plan, &off, &total)) return rc;
-  if (ws_bytes < total || !dev_ws) return fail(KRILL_E_INVAL, "workspace of %zu bytes < %zu required", ws_bytes, total);
+  size_t total = 0;
+  if (int32_t rc = plan_windowed(pool, B, Hq, Lq, max_blocks, max_seq_len, window, &plan, &total)) return rc;
+  if (ws_bytes < total || (total > 0 && !dev_ws))
+    return fail(KRILL_E_INVAL, "workspace of %zu bytes < %zu required", ws_bytes, total);
   krill::AttnLaunch a;
   a.q = dev_q;
   a.tables = dev_block_tables;
@@ -800,14 +799,13 @@ int32_t krill_attention_windowed(krill_pool_t pool, int32_t layer, const void *d
   a.out_dtype = out_dtype == KRILL_DTYPE_F32 ? krill::DT_F32 : out_dtype == KRILL_DTYPE_F16 ? krill::DT_F16
                                                                                           : krill::DT_BF16;
   a.ws = dev_ws;
-  a.ws_bytes = off;
+  a.ws_bytes = ws_bytes;
   a.split_blocks = plan.split_blocks;
   a.path = pool->opt_path;
-  int32_t *view = reinterpret_cast<int32_t *>(static_cast<uint8_t *>(dev_ws) + off);
   DeviceGuard dg(pool->device);
   hipStream_t st = pick_stream(pool, stream);
   if (int32_t rc = flush_pending(pool, st)) return rc;
-  hipError_t e = krill::launch_attention_windowed(pool->geom, layer, a, plan, dev_starts, window, view, st);
+  hipError_t e = krill::launch_attention_windowed(pool->geom, layer, a, plan, dev_starts, window, st);
   if (e != hipSuccess) return hip_fail(e, "windowed attention launch");
   return KRILL_OK;
 }

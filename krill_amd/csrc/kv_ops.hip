@@ -1116,41 +1116,12 @@ hipError_t launch_attention_shared_prefix(const PoolGeometry &g, int32_t layer, 
   return hipGetLastError();
 }
 
-// Windowed view of the batch: sequence b's first visible key (over all Lq
-// query rows) lo = max(start[b], len - Lq - window + 1, 0) lies in block
-// fb = lo / 64; the view's table row b holds blocks fb.. of the original,
-// its length len - 64 fb and its first retained key start[b] - 64 fb.
-__global__ __launch_bounds__(256) void k_window_view(const int32_t *__restrict__ tables,
-                                                    const int32_t *__restrict__ lens,
-                                                    const int32_t *__restrict__ starts, int32_t B,
-                                                    int32_t max_blocks, int32_t Lq, int32_t window,
-                                                    int32_t *__restrict__ vtab, int32_t *__restrict__ vlen,
-                                                    int32_t *__restrict__ vstart) {
-  const int b = blockIdx.y;
-  const int len = lens[b];
-  const int st = starts ? starts[b] : 0;
-  const int lo = max(max(st, len - Lq - window + 1), 0);
-  const int fb = min(lo >> 6, max_blocks);
-  for (int i = blockIdx.x * 256 + threadIdx.x; i < max_blocks; i += gridDim.x * 256)
-    vtab[(int64_t)b * max_blocks + i] = i + fb < max_blocks ? tables[(int64_t)b * max_blocks + i + fb] : -1;
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
-    vlen[b] = len - 64 * fb;
-    vstart[b] = st - 64 * fb;
-  }
-}
-
 hipError_t launch_attention_windowed(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
-                                     const int32_t *starts, int32_t window, int32_t *view, hipStream_t st) {
+                                     const int32_t *starts, int32_t window, hipStream_t st) {
   if (a.B == 0) return hipSuccess;
-  if (window < 2 || a.B > 65535 || a.k_new || a.rope_cs || a.len_const >= 0) return hipErrorInvalidValue;
-  int32_t *vtab = view, *vlen = view + (int64_t)a.B * a.max_blocks, *vstart = vlen + a.B;
-  const dim3 grid((unsigned)std::max(1, std::min((a.max_blocks + 255) / 256, 64)), (unsigned)a.B);
-  k_window_view<<<grid, dim3(256), 0, st>>>(a.tables, a.lens, starts, a.B, a.max_blocks, a.Lq, window, vtab, vlen,
-                                            vstart);
+  if (window < 2 || a.k_new || a.rope_cs || a.len_const >= 0) return hipErrorInvalidValue;
   AttnLaunch w = a;
-  w.tables = vtab;
-  w.lens = vlen;
-  w.win_start = vstart;
+  w.win_start = starts;
   w.window = window;
   return launch_attention(g, layer, w, p, st);
 }

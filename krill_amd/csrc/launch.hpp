@@ -45,8 +45,7 @@ struct AttnLaunch {
   int32_t len_const = -1;
   int32_t causal = 1;
   int32_t partial_only = 0;
-  // sliding window: first retained key per sequence (null: no window) and
-  // the window in tokens; tables/lens here are the per-call windowed view
+  // sliding window (window > 0): first retained key per sequence (null: 0)
   const int32_t *win_start = nullptr;
   int32_t window = 0;
 };
@@ -91,14 +90,12 @@ hipError_t launch_attention(const PoolGeometry &g, int32_t layer, const AttnLaun
 // prefix blocks, the B sequences as its query positions, non-causal, partials
 // only), the suffix pass (sa: decode over each sequence's own blocks,
 // partials only) and the merge of both into sa.out.
-// Sliding-window attention: the tables (absolute block index -> block id,
-// entries below the window dropped) are first cut down to each sequence's
-// blocks from the one holding its first visible key, written into `view`
-// (B * max_blocks + 2 * B ints of workspace) with shifted lengths and
-// first retained keys; then the ordinary attention launches on that view
-// with the window mask.
+// Sliding-window attention: the kernels' window variants read each sequence
+// from the block holding its first visible key (tables: the pool's, entries
+// below the window dropped and never read) and mask keys below
+// max(starts[b], position - window + 1).
 hipError_t launch_attention_windowed(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
-                                     const int32_t *starts, int32_t window, int32_t *view, hipStream_t st);
+                                     const int32_t *starts, int32_t window, hipStream_t st);
 hipError_t launch_attention_shared_prefix(const PoolGeometry &g, int32_t layer, const AttnLaunch &pa,
                                          const AttnPlan &pp, const AttnLaunch &sa, const AttnPlan &sp,
                                          hipStream_t st);
