@@ -1010,6 +1010,11 @@ def cpu_baseline(args, w, lens0, per_tok):
         if el > 12.0 or reps >= 500:
             break
     per_layer_s = el / (reps * sample_layers)
+    # the same restatement on one thread: one step of one layer
+    base.set_threads(1)
+    t1 = time.perf_counter()
+    base.step(q, k, v, O.DT_BF16, 1.0 / math.sqrt(D), out, layers_to_run=1)
+    one_s = time.perf_counter() - t1
     base.close()
     ctx = float(np.sum(lens0)) + 1.5 * B
     gbs = ctx * per_tok / per_layer_s / 1e9
@@ -1023,6 +1028,9 @@ def cpu_baseline(args, w, lens0, per_tok):
         "sample": f"{reps} decode steps x {sample_layers} layers of the same batch ({B} seqs, same lengths) "
                   f"through the CPU restatement of the reference step (row quantize, concat, full fp16 dequant, "
                   f"fp32 SDPA); {el:.1f} s; tokens/s extrapolated to {layers} layers",
+        "single_thread": {"value": round(ctx * per_tok / one_s / 1e9, 3), "unit": "GB/s",
+                          "tokens_per_s": round(B / (one_s * layers), 4),
+                          "sample": f"one decode step of one layer on one thread, {one_s:.1f} s"},
     }
 
 

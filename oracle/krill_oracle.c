@@ -419,6 +419,16 @@ static void *grow_copy(void *old, size_t old_bytes, size_t new_bytes) {
 
 int oracle_baseline_threads(void *h) { return ((base_session *)h)->nthreads; }
 
+/* Threads of the following steps (1 = the single-thread figure). */
+void oracle_baseline_set_threads(void *h, int n) {
+#ifdef _OPENMP
+    ((base_session *)h)->nthreads = n > 0 ? n : 1;
+#else
+    (void)n;
+    ((base_session *)h)->nthreads = 1;
+#endif
+}
+
 /* One decode step over all layers.  k_new/v_new: [layers][B][Hkv][D] bf16
  * (or f16 by dt), q: [layers][B][Hq][D] in dt, out: [layers][B][Hq][D] f32. */
 void oracle_baseline_step(void *h, const uint16_t *q, const uint16_t *k_new, const uint16_t *v_new,
@@ -427,7 +437,7 @@ void oracle_baseline_step(void *h, const uint16_t *q, const uint16_t *k_new, con
     int B = s->B, Hkv = s->Hkv, Hq = s->Hq, D = s->D, R = Hq / Hkv;
     if (layers_to_run <= 0 || layers_to_run > s->layers) layers_to_run = s->layers;
     for (int l = 0; l < layers_to_run; ++l) {
-#pragma omp parallel for schedule(dynamic, 1)
+#pragma omp parallel for schedule(dynamic, 1) num_threads(s->nthreads)
         for (int bh = 0; bh < B * Hkv; ++bh) {
             int b = bh / Hkv, hk = bh % Hkv;
             base_row *r = &s->rows[((int64_t)l * B + b) * Hkv + hk];

@@ -115,6 +115,7 @@ def lib():
         L.oracle_baseline_destroy.argtypes = [P]
         L.oracle_baseline_threads.argtypes = [P]
         L.oracle_baseline_threads.restype = i32
+        L.oracle_baseline_set_threads.argtypes = [P, i32]
         L.oracle_baseline_step.argtypes = [P, P, P, P, i32, f32, P, i32]
         _lib = L
     return _lib
@@ -385,6 +386,9 @@ class Baseline:
     @property
     def threads(self) -> int:
         return int(lib().oracle_baseline_threads(self.h))
+
+    def set_threads(self, n: int):
+        lib().oracle_baseline_set_threads(self.h, int(n))
 
     def step(self, q_bits, k_bits, v_bits, dt, scale, out, layers_to_run=0):
         lib().oracle_baseline_step(self.h, _p(q_bits), _p(k_bits), _p(v_bits), dt,
