@@ -53,6 +53,9 @@ WORKLOADS = {
                                          hi=1024, prefix=4096 + 24),
     "llama-3-8b-verify-b16": dict(kind="verify", layers=32, Hq=32, Hkv=8, D=128, B=16, lo=1024, hi=8192,
                                   draft=8),
+    # chunked prefill: 512 new rows per sequence on top of its cache, every row kept
+    "qwen3-14b-prefill-b8-c512": dict(kind="verify", layers=40, Hq=40, Hkv=8, D=128, B=8, lo=2048, hi=6144,
+                                      draft=512, rollback=False),
     # the default decode workload with one request leaving and one joining (prompt U[512, 8192],
     # its K/V appended into a fresh sequence) at every step, no epoch restack
     "qwen3-14b-b32-continuous": dict(kind="continuous", layers=40, Hq=40, Hkv=8, D=128, B=32, lo=512, hi=8192,
@@ -861,6 +864,7 @@ def run_verify(args, w):
     attention of the k rows (MFMA path), then rollback to the accepted length
     (a ~ U[0, k] accepted: keep a + 1 rows on rejection, all k on full accept)."""
     layers, Hq, Hkv, D, B, k = w["layers"], w["Hq"], w["Hkv"], w["D"], w["B"], w["draft"]
+    rollback = w.get("rollback", True)
     rng = np.random.default_rng(args.seed)
     lens0 = rng.integers(w["lo"], w["hi"] + 1, size=B).astype(np.int64)
     total_steps = args.warmup + args.steps + 1
@@ -906,6 +910,9 @@ def run_verify(args, w):
             verify(layer, mx)
         # rollback (SpeculativeDecoder.swift:309-318): keep a + 1 rows on rejection, k on full accept
         for b in range(B):
+            if not rollback:  # chunked prefill keeps every row
+                accepted_total[0] += k
+                continue
             a = int(acc_rng.integers(0, k + 1))
             keep_rows = a + 1 if a < k else k
             cur_len[b] += keep_rows - k
@@ -938,27 +945,36 @@ def run_verify(args, w):
     # causal: row r of sequence b sees len_b - k + r + 1 tokens; QK^T and PV 2 FLOP per MAC each
     flops = sum(4.0 * Hq * D * sum(c - k + r + 1 for r in range(k)) for c in cur_len)
     tflops = flops / (attn_ms * 1e-3) / 1e12
+    what = (f"{k} draft rows/seq (causal inside the window, {Hq // Hkv * k} query rows per KV head -> MFMA "
+            f"path), accepted a ~ U[0,{k}] then rollback" if rollback else
+            f"a {k}-token prefill chunk per sequence (causal inside the chunk, {Hq // Hkv * k} query rows per KV "
+            "head in row groups of 32 -> MFMA path), every row kept")
     config = {
         "workload": f"{args.workload}: {layers} layers, Hq {Hq}, Hkv {Hkv}, D {D}, B {B}, context "
-                    f"U[{w['lo']},{w['hi']}], {k} draft rows/seq (causal inside the window, "
-                    f"{Hq // Hkv * k} query rows per KV head -> MFMA path), accepted a ~ U[0,{k}] then rollback, "
-                    f"{args.quant} int8; step = per layer quantize-append {k} tokens/seq + verify attention",
+                    f"U[{w['lo']},{w['hi']}], {what}, {args.quant} int8; step = per layer quantize-append {k} "
+                    "tokens/seq + causal attention of those rows",
         "layers": layers, "Hq": Hq, "Hkv": Hkv, "head_dim": D, "batch": B, "draft": k, "quant": args.quant,
         "context_mean": float(np.mean(lens0)), "num_blocks": num_blocks,
     }
+    ai = flops / kv_launch
+    hbm = {"achieved": round(kv_launch / (attn_ms * 1e-3) / 1e9, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(kv_launch / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_launch": int(kv_launch)}
+    mfma = {"achieved": round(tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "flops_per_launch": flops,
+            "arith_intensity": round(ai, 1)}
+    compute_bound = ai > MFMA_F16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)  # above the ridge (~312 FLOP/B)
     roofline = {
-        "bound": "hbm",
-        "kernel": "verify attention call (k_attn_mfma + k_attn_merge_flat), one layer",
-        "achieved": round(kv_launch / (attn_ms * 1e-3) / 1e9, 2),
-        "peak": HBM_PEAK_GBS,
-        "unit": "GB/s",
-        "frac": round(kv_launch / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "traffic": measured_traffic(args, "verify_attn"),
+        "bound": "mfma" if compute_bound else "hbm",
+        "kernel": ("chunked-prefill" if not rollback else "verify") + " attention call (k_attn_mfma + "
+                  "k_attn_merge_flat), one layer",
+        "achieved": mfma["achieved"] if compute_bound else hbm["achieved"],
+        "peak": MFMA_F16_PEAK_TFLOPS if compute_bound else HBM_PEAK_GBS,
+        "unit": "TFLOP/s" if compute_bound else "GB/s",
+        "frac": mfma["frac"] if compute_bound else hbm["frac"],
+        "traffic": measured_traffic(args, "verify_attn") if rollback else None,
         "bytes_per_launch": int(kv_launch),
         "avg_launch_ms": round(attn_ms, 5),
-        "mfma": {"achieved": round(tflops, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                 "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "flops_per_launch": flops,
-                 "arith_intensity": round(flops / kv_launch, 1)},
+        "mfma" if not compute_bound else "hbm": mfma if not compute_bound else hbm,
     }
     accepted = accepted_total[0] - acc0
     extra = {"tokens_per_s": round(accepted / args.steps / (ms_step * 1e-3), 1),

@@ -340,3 +340,13 @@ def test_long_context_uniform_keys_give_mean_of_values():
         err = np.abs(got[b, :, 0] - want).max()
         assert err <= ATOL, (b, err)
     pool.close()
+
+
+def test_chunked_prefill_512_rows():
+    """A 512-token prefill chunk on top of a cache (5 query heads per KV
+    head: 2560 rows per KV head in 80 row groups of 32 on the MFMA path),
+    causal inside the chunk."""
+    print("\ncase chunked_prefill_512", flush=True)
+    got, ref = _attn_case("affine_g64", 128, 2, 5, [600, 1100], Lq=512, seed=31)
+    err = np.abs(got - ref).max()
+    assert err <= ATOL, f"max abs error {err:.3e}"
