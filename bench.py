@@ -183,8 +183,8 @@ class Env:
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: every box in this setup has one MI355X; --gpus {args.gpus} is not "
-              "supported (the path would shard by sequence / KV head, see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (the path would shard by "
+              "sequence / KV head across GPUs)", file=sys.stderr)
         sys.exit(2)
     import torch
 
