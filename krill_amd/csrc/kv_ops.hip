@@ -799,14 +799,25 @@ __device__ __forceinline__ void merge_two(const MergeSrc (&src)[2], void *out, i
     }
     w_lds[lane] = w;
     __syncthreads();
-#pragma unroll 4
-    for (int k = 0; k < cnt; ++k) {
-      const float wk = w_lds[k];
-      const float *o;
-      const float2 *ml;
-      part(k0 + k, &o, &ml);
+    // 16 partial rows in flight at a time: their loads all issue before the
+    // sums that use them
+    constexpr int KC = 16;
+    for (int k1 = 0; k1 < cnt; k1 += KC) {
+      float ov[KC][E];
 #pragma unroll
-      for (int e = 0; e < E; ++e) acc[e] += wk * o[lane + 64 * e];
+      for (int j = 0; j < KC; ++j) {
+        const float *o;
+        const float2 *ml;
+        part(k0 + min(k1 + j, cnt - 1), &o, &ml);
+#pragma unroll
+        for (int e = 0; e < E; ++e) ov[j][e] = o[lane + 64 * e];
+      }
+#pragma unroll
+      for (int j = 0; j < KC; ++j) {
+        const float wk = k1 + j < cnt ? w_lds[k1 + j] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[e] += wk * ov[j][e];
+      }
     }
     __syncthreads();
   }
