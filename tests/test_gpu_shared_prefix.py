@@ -179,3 +179,10 @@ def test_shared_prefix_fused_append_bit_identical(path):
     assert torch.equal(outs[0], outs[1])
     for k in snaps[0]:
         assert np.array_equal(snaps[0][k].view(np.uint8), snaps[1][k].view(np.uint8)), k
+
+
+def test_shared_prefix_f16_inputs():
+    print("\ncase shared_prefix_f16", flush=True)
+    got, single, ref = _case("affine_g64", 128, 2, 5, 200, [0, 9, 130], dt="f16", seed=17)
+    assert np.abs(got - ref).max() <= ATOL
+    assert np.abs(got - single).max() <= _single_tol(3, 5)

@@ -30,20 +30,20 @@ class Seqs:
     """B sequences appended through the product path in one pool; the
     oracle's copy of every token and the ops applied to each sequence."""
 
-    def __init__(self, pool, B, total, rng):
+    def __init__(self, pool, B, total, rng, dt=DTS):
         H, D = pool.num_kv_heads, pool.head_dim
-        self.pool, self.B = pool, B
+        self.pool, self.B, self.dt = pool, B, dt
         self.seqs = [pool.seq_create() for _ in range(B)]
-        self.k = [rand_bits(rng, (H, total, D), DTS) for _ in range(B)]
-        self.v = [rand_bits(rng, (H, total, D), DTS) for _ in range(B)]
+        self.k = [rand_bits(rng, (H, total, D), dt) for _ in range(B)]
+        self.v = [rand_bits(rng, (H, total, D), dt) for _ in range(B)]
         self.ops = [[] for _ in range(B)]
         self.len = [0] * B
 
     def append(self, b, L):
         s, p = self.seqs[b], self.len[b]
         slots = self.pool.reserve_append(s, L)
-        self.pool.quantize_append(0, to_dev(self.k[b][None, :, p:p + L], DTS), to_dev(self.v[b][None, :, p:p + L], DTS),
-                                  i32(slots[None]))
+        self.pool.quantize_append(0, to_dev(self.k[b][None, :, p:p + L], self.dt),
+                                  to_dev(self.v[b][None, :, p:p + L], self.dt), i32(slots[None]))
         self.len[b] += L
         self.ops[b].append(("append", L))
 
@@ -64,10 +64,10 @@ def _oracle_rows(seqs, b, q_bits, window, start, mode):
     Hq, Lq, D = q_bits.shape
     R = Hq // H
     n = seqs.len[b]
-    kq, ks, kz = O.quantize(seqs.k[b][:, :n], DT[DTS], MODE[mode])
-    vq, vs, vz = O.quantize(seqs.v[b][:, :n], DT[DTS], MODE[mode])
+    kq, ks, kz = O.quantize(seqs.k[b][:, :n], DT[seqs.dt], MODE[mode])
+    vq, vs, vz = O.quantize(seqs.v[b][:, :n], DT[seqs.dt], MODE[mode])
     kd, vd = O.dequant_f64(kq, ks, kz, MODE[mode]), O.dequant_f64(vq, vs, vz, MODE[mode])
-    qf = O.bits_to_f32(q_bits, DT[DTS]).astype(np.float64)
+    qf = O.bits_to_f32(q_bits, DT[seqs.dt]).astype(np.float64)
     rows = O.sliding_window_rows(Lq, n - Lq, window)
     lo = [max(start, a) for a, _ in rows]
     hi = [h for _, h in rows]
@@ -84,13 +84,14 @@ def _check(pools, seqs_list, window, Lq, mode, rng, R, tol_pair=1e-5):
     or with none (None) while no sequence has dropped any)."""
     B = seqs_list[0].B
     H, D = pools[0].num_kv_heads, pools[0].head_dim
-    q = rand_bits(rng, (B, H * R, Lq, D), DTS)
+    dt = seqs_list[0].dt
+    q = rand_bits(rng, (B, H * R, Lq, D), dt)
     st = pools[0].batch_starts(seqs_list[0].seqs)
     outs = []
     for pool, seqs in zip(pools, seqs_list):
         t, n, mb = seqs.tables()
         starts = None if pool is pools[1] and not st.any() else i32(st)
-        out = pool.attention_windowed(0, to_dev(q, DTS), t, n, starts, window, int(max(seqs.len)), 1.0 / np.sqrt(D))
+        out = pool.attention_windowed(0, to_dev(q, dt), t, n, starts, window, int(max(seqs.len)), 1.0 / np.sqrt(D))
         torch.cuda.synchronize()
         outs.append(out.cpu().numpy())
     seqs = seqs_list[0]
@@ -105,10 +106,10 @@ def _check(pools, seqs_list, window, Lq, mode, rng, R, tol_pair=1e-5):
     assert dev <= tol_pair, dev
 
 
-def _pools(mode, H, D, blocks, window, seed):
-    a = krill_amd.KVPool(1, H, D, blocks, mode, DTS, free_list_seed=seed)
+def _pools(mode, H, D, blocks, window, seed, dt=DTS):
+    a = krill_amd.KVPool(1, H, D, blocks, mode, dt, free_list_seed=seed)
     a.set_option(krill_amd._lib.OPT_WINDOW, window)
-    b = krill_amd.KVPool(1, H, D, blocks, mode, DTS, free_list_seed=seed + 1)
+    b = krill_amd.KVPool(1, H, D, blocks, mode, dt, free_list_seed=seed + 1)
     return a, b
 
 
@@ -177,5 +178,23 @@ def test_window_truncate_then_decode():
     _, start = O.rotating_retained_start(sl[0].ops[0], W)
     assert start == 151 and sl[0].len[0] - start < W  # the start binds
     _check(pools, sl, W, 1, "affine_g64", rng, R)
+    for p in pools:
+        p.close()
+
+
+@pytest.mark.parametrize("Lq", [1, 40])
+def test_window_f16_inputs(Lq):
+    """fp16 K/V/queries (the other input dtype), decode and a chunk on MFMA."""
+    print(f"\ncase window_f16 Lq={Lq}", flush=True)
+    W, H, D, R = 130, 2, 128, 4
+    rng = np.random.default_rng(41 + Lq)
+    pools = _pools("affine_g64", H, D, 48, W, seed=9, dt="f16")
+    sl = [Seqs(p, 2, 700, np.random.default_rng(43), dt="f16") for p in pools]
+    for ss in sl:
+        ss.append(0, 300)
+        ss.append(1, 90)
+        ss.append(0, Lq)
+        ss.append(1, Lq)
+    _check(pools, sl, W, Lq, "affine_g64", rng, R, tol_pair=1e-3)
     for p in pools:
         p.close()
