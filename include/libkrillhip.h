@@ -177,6 +177,13 @@ int32_t krill_prefix_store(krill_pool_t pool, int32_t seq, const char *model_id,
  * Miss: *prefix_len_out = 0, *entry_seq_out = -1. */
 int32_t krill_prefix_lookup(krill_pool_t pool, const char *model_id, const char *media_hash,
                             const int64_t *tokens, int32_t n, int32_t *prefix_len_out, int32_t *entry_seq_out);
+/* One step of that scan at exactly n tokens: the in-memory entry keyed by
+ * tokens[0..n), LRU-touched on a hit (memoryCache[key] + touchEntryLocked,
+ * PrefixCache.swift:294-298).  For callers that interleave their own tier
+ * between the lengths (the disk tier, :300-304).  Miss (or n below
+ * min_prefix_len): *entry_seq_out = -1. */
+int32_t krill_prefix_probe(krill_pool_t pool, const char *model_id, const char *media_hash, const int64_t *tokens,
+                           int32_t n, int32_t *entry_seq_out);
 /* lookupLongestPrefixQuantized (PrefixCache.swift:235-263): entry with the
  * longest common prefix >= min_prefix_len (ties: most recently used). */
 int32_t krill_prefix_lookup_longest(krill_pool_t pool, const char *model_id, const char *media_hash,

@@ -139,6 +139,7 @@ SIGNATURES = {
     "krill_batch_starts": [P, PI32, I32, PI32],
     "krill_prefix_store": [P, I32, STR, STR, PI64, I32, PI32],
     "krill_prefix_lookup": [P, STR, STR, PI64, I32, PI32, PI32],
+    "krill_prefix_probe": [P, STR, STR, PI64, I32, PI32],
     "krill_prefix_lookup_longest": [P, STR, STR, PI64, I32, PI32, PI32],
     "krill_prefix_clear": [P],
     "krill_prefix_count": [P, PI32],

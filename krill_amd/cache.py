@@ -247,18 +247,20 @@ class PrefixCache:
         """(prefix_len, entry_seq) of an exact entry, or (0, None)."""
         if self.disk is None or not self.disk.enabled:
             return self.pool.prefix_lookup(tokens, self.model_id, media_hash)
-        n_max = len(tokens)
+        # scan (PrefixCache.swift:273-308): at each length the memory entry
+        # (one exact probe), then that length's file, then the next length
+        tokens = np.ascontiguousarray(tokens, np.int64)
         step = max(1, self.min_prefix_len // 2)
-        n = n_max
+        n = len(tokens)
         while n >= self.min_prefix_len:
-            got, entry = self.pool.prefix_lookup(tokens[:n], self.model_id, media_hash)
-            if got == n:
-                return got, entry
+            entry = self.pool.prefix_probe(tokens[:n], self.model_id, media_hash)
+            if entry is not None:
+                return n, entry
             layers = self.disk.load(self._key(tokens[:n], media_hash))
             if layers is not None and self._restore(tokens[:n], layers, media_hash):
-                got, entry = self.pool.prefix_lookup(tokens[:n], self.model_id, media_hash)
-                if got == n:
-                    return got, entry
+                entry = self.pool.prefix_probe(tokens[:n], self.model_id, media_hash)
+                if entry is not None:
+                    return n, entry
             n -= step
         return 0, None
 

@@ -73,6 +73,8 @@ int32_t BlockManager::new_seq_id() {
     free_seq_ids_.pop_back();
     return id;
   }
+  // Room for every id to come back, so that returning one never allocates.
+  free_seq_ids_.reserve(seqs_.size() + 1);
   seqs_.emplace_back();
   return static_cast<int32_t>(seqs_.size() - 1);
 }
@@ -94,7 +96,7 @@ bool BlockManager::entry_frees_blocks(const Entry &e) const {
   return false;
 }
 
-void BlockManager::drop_entry(std::list<Entry>::iterator it, bool count_eviction) {
+void BlockManager::drop_entry(std::list<Entry>::iterator it, bool count_eviction, bool keep_key) {
   Seq &s = seqs_[static_cast<size_t>(it->seq)];
   size_t before = free_.size();
   release_seq_blocks(s, 0);
@@ -106,7 +108,7 @@ void BlockManager::drop_entry(std::list<Entry>::iterator it, bool count_eviction
     ++evicted_entries_;
     evicted_blocks_ += static_cast<int64_t>(free_.size() - before);
   }
-  entry_by_key_.erase(it->key);
+  if (!keep_key) entry_by_key_.erase(it->key);
   entries_.erase(it);
 }
 
@@ -158,20 +160,22 @@ int32_t BlockManager::seq_fork(int32_t src, int32_t n_tokens, int32_t *out) {
   if (int32_t rc = check_seq(src, false)) return rc;
   if (!out) return fail(KRILL_E_INVAL, "seq_out is NULL");
   const int32_t src_len = seqs_[static_cast<size_t>(src)].len;
+  const int32_t src_start = seqs_[static_cast<size_t>(src)].start;
   if (n_tokens < 0 || n_tokens > src_len)
     return fail(KRILL_E_RANGE, "fork of %d tokens from a sequence of %d", n_tokens, src_len);
-  int32_t id = new_seq_id();
-  Seq &s = seqs_[static_cast<size_t>(id)];
-  const Seq &p = seqs_[static_cast<size_t>(src)];
-  if (n_tokens < p.start)
+  if (n_tokens < src_start)
     return fail(KRILL_E_RANGE, "fork of %d tokens below the sliding window (first retained token %d)", n_tokens,
-                p.start);
+                src_start);
+  const Seq &p = seqs_[static_cast<size_t>(src)];
+  const size_t nb = static_cast<size_t>((n_tokens + cfg_.block_tokens - 1) / cfg_.block_tokens);
+  std::vector<int32_t> blocks(p.blocks.begin(), p.blocks.begin() + static_cast<std::ptrdiff_t>(nb));
+  const int32_t id = new_seq_id();  // may grow seqs_ (p is not used after it)
+  Seq &s = seqs_[static_cast<size_t>(id)];
   s = Seq{};
   s.alive = true;
   s.len = n_tokens;
-  s.start = p.start;
-  size_t nb = static_cast<size_t>((n_tokens + cfg_.block_tokens - 1) / cfg_.block_tokens);
-  s.blocks.assign(p.blocks.begin(), p.blocks.begin() + static_cast<std::ptrdiff_t>(nb));
+  s.start = src_start;
+  s.blocks = std::move(blocks);
   for (int32_t b : s.blocks)
     if (b != kDropped) ++refcnt_[static_cast<size_t>(b)];
   ++live_seqs_;
@@ -245,19 +249,30 @@ int32_t BlockManager::reserve_append(int32_t seq, int32_t L, int32_t *slots_out)
   const int32_t bt = cfg_.block_tokens;
   // Sliding window: keep window - 1 tokens before the append
   // (RotatingKVCache.trimForAppend, RotatingKVCache.swift:70-75) and drop
-  // every block that holds none of the retained ones.
+  // every block that holds none of the retained ones.  The blocks go back to
+  // the pool before the allocations below (they may be what makes them
+  // succeed); a failed append takes them back.
+  const int32_t old_start = s.start;
+  const size_t need = static_cast<size_t>((s.len + L + bt - 1) / bt);
+  std::vector<std::pair<int32_t, int32_t>> trimmed;  // (table index, block id)
+  std::vector<int32_t> fresh;  // allocated here, released on failure
+  // Host memory first (a failed allocation then changes nothing).
+  trimmed.reserve(s.blocks.size());
+  fresh.reserve(need - std::min(need, s.blocks.size()) + 1);
+  s.blocks.reserve(need);
+  pending_.reserve(pending_.size() + 1);
   if (cfg_.window > 0 && s.len - s.start > cfg_.window - 1) {
     s.start = s.len - (cfg_.window - 1);
     for (int32_t i = 0; i < s.start / bt; ++i) {
       int32_t &blk = s.blocks[static_cast<size_t>(i)];
       if (blk != kDropped) {
+        trimmed.emplace_back(i, blk);
         release_block(blk);
         blk = kDropped;
       }
     }
   }
 
-  std::vector<int32_t> fresh;  // allocated here, released on failure
   int32_t cow_idx = -1, cow_old = -1;
   auto rollback = [&](int32_t rc) {
     for (int32_t b : fresh) release_block(b);
@@ -266,6 +281,19 @@ int32_t BlockManager::reserve_append(int32_t seq, int32_t L, int32_t *slots_out)
       pending_.pop_back();
     }
     s.blocks.resize(static_cast<size_t>((s.len + bt - 1) / bt));
+    // Re-take the trimmed blocks: a block whose last reference the trim
+    // dropped sits on the free stack (nothing was written to it: no kernel
+    // runs for a failed append).
+    for (const auto &tb : trimmed) {
+      const int32_t b = tb.second;
+      if (refcnt_[static_cast<size_t>(b)] == 0) {
+        auto pos = std::find(free_.begin(), free_.end(), b);
+        if (pos != free_.end()) free_.erase(pos);
+      }
+      ++refcnt_[static_cast<size_t>(b)];
+      s.blocks[static_cast<size_t>(tb.first)] = b;
+    }
+    s.start = old_start;
     return rc;
   };
 
@@ -283,7 +311,6 @@ int32_t BlockManager::reserve_append(int32_t seq, int32_t L, int32_t *slots_out)
       cow_old = tail;
     }
   }
-  size_t need = static_cast<size_t>((s.len + L + bt - 1) / bt);
   while (s.blocks.size() < need) {
     int32_t nb;
     if (int32_t rc = alloc_block(&nb)) return rollback(rc);
@@ -371,28 +398,44 @@ int32_t BlockManager::prefix_store(int32_t seq, const char *model_id, const char
   if (n < cfg_.min_prefix_len) return KRILL_OK;
   if (cfg_.max_entry_bytes > 0 && memory_bytes(n) * cfg_.num_layers > cfg_.max_entry_bytes)
     return KRILL_OK;
-  uint64_t key = prefix_key(model_id, media_hash, cfg_.dtype_tag, tokens, n);
-  auto found = entry_by_key_.find(key);
-  if (found != entry_by_key_.end()) drop_entry(found->second, false);
+  if (cfg_.max_entries <= 0) return KRILL_OK;
+  const uint64_t key = prefix_key(model_id, media_hash, cfg_.dtype_tag, tokens, n);
+  // Everything that allocates happens first, so that a failed host
+  // allocation changes nothing: the entry's block list and list node, the
+  // sequence slot, and the entry's key slot (an existing entry with the same
+  // key hands its slot over).
+  const size_t nb = static_cast<size_t>((n + cfg_.block_tokens - 1) / cfg_.block_tokens);
+  const Seq &src = seqs_[static_cast<size_t>(seq)];
+  std::vector<int32_t> blocks(src.blocks.begin(), src.blocks.begin() + static_cast<std::ptrdiff_t>(nb));
+  std::list<Entry> node;
+  node.push_back(Entry{key, model_id ? model_id : "", media_hash ? media_hash : "",
+                       std::vector<int64_t>(tokens, tokens + n), -1});
+  if (free_seq_ids_.empty()) {  // new_seq_id below may grow seqs_
+    free_seq_ids_.reserve(seqs_.size() + 1);
+    seqs_.reserve(seqs_.size() + 1);
+  }
+  auto slot = entry_by_key_.find(key);
+  const bool replace = slot != entry_by_key_.end();
+  if (!replace) slot = entry_by_key_.emplace(key, entries_.end()).first;
+  // The blocks are referenced before any entry is dropped: the source may
+  // itself be an entry (a handle from krill_prefix_lookup) that the key
+  // match or the capacity eviction below removes.
+  for (int32_t b : blocks) ++refcnt_[static_cast<size_t>(b)];  // no dropped block: start == 0
+  if (replace) drop_entry(slot->second, false, true);
   // storeInMemory: evict LRU while at capacity (PrefixCache.swift:540-551).
   while (!entries_.empty() && static_cast<int32_t>(entries_.size()) >= cfg_.max_entries)
     drop_entry(entries_.begin(), true);
-  if (cfg_.max_entries <= 0) return KRILL_OK;
   // Frozen fork holding the first n tokens.
-  int32_t id = new_seq_id();
+  const int32_t id = new_seq_id();
   Seq &s = seqs_[static_cast<size_t>(id)];
-  const Seq &p = seqs_[static_cast<size_t>(seq)];
   s = Seq{};
   s.alive = true;
   s.frozen = true;
   s.len = n;
-  size_t nb = static_cast<size_t>((n + cfg_.block_tokens - 1) / cfg_.block_tokens);
-  s.blocks.assign(p.blocks.begin(), p.blocks.begin() + static_cast<std::ptrdiff_t>(nb));
-  for (int32_t b : s.blocks) ++refcnt_[static_cast<size_t>(b)];  // no dropped block: start == 0
-  Entry e{key, model_id ? model_id : "", media_hash ? media_hash : "",
-          std::vector<int64_t>(tokens, tokens + n), id};
-  entries_.push_back(std::move(e));
-  entry_by_key_[key] = std::prev(entries_.end());
+  s.blocks = std::move(blocks);
+  node.front().seq = id;
+  entries_.splice(entries_.end(), node);
+  slot->second = std::prev(entries_.end());
   if (stored_out) *stored_out = 1;
   return KRILL_OK;
 }
@@ -408,19 +451,36 @@ int32_t BlockManager::prefix_lookup(const char *model_id, const char *media_hash
   if (n < cfg_.min_prefix_len) return KRILL_OK;
   const int32_t step = std::max(1, cfg_.min_prefix_len / 2);
   for (int32_t check = n; check >= cfg_.min_prefix_len; check -= step) {
-    uint64_t key = prefix_key(model_id, media_hash, cfg_.dtype_tag, tokens, check);
-    auto it = entry_by_key_.find(key);
-    if (it == entry_by_key_.end()) continue;
-    const Entry &e = *it->second;
-    // Keys are hashes; an entry only hits when its tokens are the probe's.
-    if (static_cast<int32_t>(e.tokens.size()) != check ||
-        !std::equal(e.tokens.begin(), e.tokens.end(), tokens))
-      continue;
-    entries_.splice(entries_.end(), entries_, it->second);  // touch (MRU)
+    const int32_t seq = probe_locked(model_id, media_hash, tokens, check);
+    if (seq < 0) continue;
     *prefix_len_out = check;
-    *entry_seq_out = e.seq;
+    *entry_seq_out = seq;
     return KRILL_OK;
   }
+  return KRILL_OK;
+}
+
+int32_t BlockManager::probe_locked(const char *model_id, const char *media_hash, const int64_t *tokens,
+                                   int32_t n) {
+  const uint64_t key = prefix_key(model_id, media_hash, cfg_.dtype_tag, tokens, n);
+  auto it = entry_by_key_.find(key);
+  if (it == entry_by_key_.end()) return -1;
+  const Entry &e = *it->second;
+  // Keys are hashes; an entry only hits when its tokens are the probe's.
+  if (static_cast<int32_t>(e.tokens.size()) != n || !std::equal(e.tokens.begin(), e.tokens.end(), tokens))
+    return -1;
+  entries_.splice(entries_.end(), entries_, it->second);  // touch (MRU)
+  return e.seq;
+}
+
+int32_t BlockManager::prefix_probe(const char *model_id, const char *media_hash, const int64_t *tokens, int32_t n,
+                                   int32_t *entry_seq_out) {
+  std::lock_guard<std::mutex> g(mu_);
+  if (!entry_seq_out) return fail(KRILL_E_INVAL, "NULL output");
+  *entry_seq_out = -1;
+  if (n < 0 || (n > 0 && !tokens)) return fail(KRILL_E_INVAL, "bad token array");
+  if (n < cfg_.min_prefix_len) return KRILL_OK;
+  *entry_seq_out = probe_locked(model_id, media_hash, tokens, n);
   return KRILL_OK;
 }
 

@@ -71,6 +71,9 @@ class BlockManager {
                        const int64_t *tokens, int32_t n, int32_t *stored_out);
   int32_t prefix_lookup(const char *model_id, const char *media_hash, const int64_t *tokens,
                         int32_t n, int32_t *prefix_len_out, int32_t *entry_seq_out);
+  // One exact length: the entry keyed by tokens[0..n) (touched on a hit).
+  int32_t prefix_probe(const char *model_id, const char *media_hash, const int64_t *tokens, int32_t n,
+                       int32_t *entry_seq_out);
   int32_t prefix_lookup_longest(const char *model_id, const char *media_hash,
                                 const int64_t *tokens, int32_t n, int32_t *prefix_len_out,
                                 int32_t *entry_seq_out);
@@ -103,12 +106,15 @@ class BlockManager {
   };
 
   int32_t check_seq(int32_t seq, bool mutable_required) const;
+  // Entry sequence keyed by tokens[0..n) with exactly those tokens, touched
+  // (most recently used); -1 when there is none.  Caller holds mu_.
+  int32_t probe_locked(const char *model_id, const char *media_hash, const int64_t *tokens, int32_t n);
   int32_t new_seq_id();
   int32_t alloc_block(int32_t *out);
   void release_block(int32_t b);
   void release_seq_blocks(Seq &s, size_t keep);
   bool entry_frees_blocks(const Entry &e) const;
-  void drop_entry(std::list<Entry>::iterator it, bool count_eviction);
+  void drop_entry(std::list<Entry>::iterator it, bool count_eviction, bool keep_key = false);
   void evict_until_below(int32_t target_used);
 
   BlockManagerConfig cfg_;

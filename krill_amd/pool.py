@@ -195,6 +195,15 @@ class KVPool:
         """Exact-entry scan (PrefixCache.lookupQuantized): (prefix_len, entry_seq)."""
         return self._lookup(L.lib().krill_prefix_lookup, tokens, model_id, media_hash)
 
+    def prefix_probe(self, tokens, model_id: str = "", media_hash=None):
+        """Entry sequence keyed by exactly `tokens`, or None (one step of the
+        exact scan, PrefixCache.swift:294-298; touched on a hit)."""
+        t = np.ascontiguousarray(tokens, np.int64)
+        ent = ctypes.c_int32()
+        tp = _i64p(t) if t.size else None
+        L.check(L.lib().krill_prefix_probe(self._h, _enc(model_id), _enc(media_hash), tp, t.size, ctypes.byref(ent)))
+        return ent.value if ent.value >= 0 else None
+
     def prefix_lookup_longest(self, tokens, model_id: str = "", media_hash=None):
         """Longest common prefix (PrefixCache.lookupLongestPrefixQuantized)."""
         return self._lookup(L.lib().krill_prefix_lookup_longest, tokens, model_id, media_hash)

@@ -507,3 +507,143 @@ def test_window_guards():
     with pytest.raises(KrillError):
         p.set_option(L.OPT_WINDOW, 0)  # tokens already dropped
     p.close()
+
+
+# ---- regressions: entries as store sources, failed appends, the exact probe
+
+def _refcount_invariant(p, seqs):
+    """Every block's refcount equals the number of table entries naming it
+    over the given live sequences and the prefix entries."""
+    rc = p.refcounts()
+    want = np.zeros_like(rc)
+    for s in seqs:
+        for b in p.block_table(s):
+            if b >= 0:
+                want[b] += 1
+    return rc, want
+
+
+def test_store_from_an_entry_with_the_same_key_keeps_its_blocks():
+    p = host_pool(min_prefix_len=8)
+    s = p.seq_create()
+    p.reserve_append(s, 100)
+    toks = list(range(100))
+    assert p.prefix_store(s, toks, "m")
+    _, e = p.prefix_lookup(toks, "m")
+    table = p.block_table(e).copy()
+    # the source is the entry that the key match replaces
+    assert p.prefix_store(e, toks, "m")
+    plen, e2 = p.prefix_lookup(toks, "m")
+    assert plen == 100 and p.prefix_count() == 1
+    assert np.array_equal(p.block_table(e2), table)
+    rc = p.refcounts()
+    assert all(rc[b] == 2 for b in table)   # the live sequence and the new entry
+    p.seq_free(s)
+    assert all(p.refcounts()[b] == 1 for b in table)
+    p.prefix_clear()
+    assert p.stats()["blocks_used"] == 0
+    p.close()
+
+
+def test_store_from_an_entry_that_capacity_eviction_drops():
+    p = host_pool(min_prefix_len=8, max_prefix_entries=1)
+    s = p.seq_create()
+    p.reserve_append(s, 200)
+    toks = list(range(200))
+    assert p.prefix_store(s, toks, "m")
+    _, e = p.prefix_lookup(toks, "m")
+    p.seq_free(s)                       # the entry holds the only references
+    assert p.prefix_store(e, toks[:100], "m")   # at capacity: the source is evicted
+    assert p.prefix_count() == 1
+    plen, e2 = p.prefix_lookup(toks[:100], "m")
+    assert plen == 100 and p.seq_length(e2) == 100
+    assert p.stats()["blocks_used"] == 2          # the 100-token entry's two blocks
+    assert all(p.refcounts()[b] == 1 for b in p.block_table(e2))
+    p.prefix_clear()
+    assert p.stats()["blocks_used"] == 0
+    p.close()
+
+
+def test_failed_append_on_a_window_pool_changes_nothing():
+    p = _window_pool(100, blocks=4)
+    s = p.seq_create()
+    p.reserve_append(s, 200)                 # 4 blocks, nothing trimmed yet
+    other_table = p.block_table(s).copy()
+    q = p.seq_fork(s, 200)                   # shares every block: the trim frees none
+    with pytest.raises(KrillError) as e:
+        p.reserve_append(s, 100)             # would trim to 101 and need a 5th block
+    assert e.value.code == L.KRILL_E_NOMEM
+    assert p.seq_length(s) == 200 and int(p.batch_starts([s])[0]) == 0
+    assert np.array_equal(p.block_table(s), other_table)
+    assert p.stats()["blocks_used"] == 4
+    assert all(p.refcounts()[b] == 2 for b in other_table)
+    p.seq_free(q)
+    p.reserve_append(s, 100)                 # now the trimmed blocks make room
+    assert int(p.batch_starts([s])[0]) == 101 and p.seq_length(s) == 300
+    p.close()
+
+
+def test_failed_append_rolls_back_a_trim_that_freed_blocks():
+    # the trim frees a block (its only reference) and the append still
+    # needs more blocks than the pool then has
+    p = _window_pool(70, blocks=4)
+    s = p.seq_create()
+    p.reserve_append(s, 150)                       # blocks 0..2, tail block 2 partly filled
+    f = p.seq_fork(s, 150)                         # shares all three
+    p.seq_free(f)
+    before = p.block_table(s).copy()
+    used = p.stats()["blocks_used"]
+    with pytest.raises(KrillError):
+        p.reserve_append(s, 300)                   # needs 4 more blocks after the trim frees 1
+    assert np.array_equal(p.block_table(s), before)
+    assert p.stats()["blocks_used"] == used and int(p.batch_starts([s])[0]) == 0
+    assert all(p.refcounts()[b] == 1 for b in before)
+    p.close()
+
+
+def test_fork_below_the_window_leaks_no_sequence_id():
+    p = _window_pool(100)
+    s = p.seq_create()
+    p.reserve_append(s, 300)
+    p.reserve_append(s, 1)
+    spare = p.seq_create()
+    p.seq_free(spare)                     # its id is the next one handed out
+    with pytest.raises(KrillError):
+        p.seq_fork(s, 150)
+    assert p.seq_create() == spare
+    p.close()
+
+
+def test_exact_probe_hits_one_length_and_touches_only_on_a_hit():
+    p = host_pool(min_prefix_len=8, max_prefix_entries=2)
+    s = p.seq_create()
+    p.reserve_append(s, 64)
+    a, b = list(range(40)), list(range(100, 140))
+    assert p.prefix_store(s, a, "m") and p.prefix_store(s, b, "m")
+    assert p.prefix_probe(a[:39], "m") is None        # one length only, no scan
+    assert p.prefix_probe(a, "other") is None
+    assert p.prefix_probe(a[:7], "m") is None         # below minPrefixLength
+    assert p.prefix_probe(a, "m") is not None         # hit: a becomes most recent
+    p.prefix_store(s, list(range(200, 240)), "m")     # evicts the least recent: b
+    assert p.prefix_probe(b, "m") is None and p.prefix_probe(a, "m") is not None
+    p.close()
+
+
+def test_disk_scan_probes_each_length_once(tmp_path):
+    from krill_amd.cache import PrefixCache
+
+    p = host_pool(min_prefix_len=8)
+    cache = PrefixCache(p, "m", cache_dir=tmp_path, min_prefix_len=8)
+    calls = []
+    real = p.prefix_probe
+    p.prefix_probe = lambda t, *a: calls.append(len(t)) or real(t, *a)
+    toks = np.arange(2048)
+    assert cache.lookup_quantized(toks) == (0, None)
+    assert calls == list(range(2048, 7, -4))
+    s = p.seq_create()
+    p.reserve_append(s, 16)
+    assert p.prefix_store(s, toks[:12], "m")
+    calls.clear()
+    assert cache.lookup_quantized(toks[:16])[0] == 12
+    assert calls == [16, 12]
+    p.close()
