@@ -13,9 +13,9 @@
  * algorithm is restated from the source text.
  *
  * Pinning (how each function is checked independently of itself) is listed in
- * the header of oracle/oracle.py.  Functions whose exact bits depend on the
- * third-party mlx library (MLX affine quantize, MLX SDPA rounding) are marked
- * "parity unpinned" there.
+ * the header of oracle/oracle.py.  The exact rounding of MLX's fused SDPA
+ * (third-party mlx) is the one boundary the oracle does not reproduce: the
+ * attention checks are against binary64 within a stated tolerance.
  *
  * Build: gcc -O2 -std=c11 -fPIC -shared -ffp-contract=off -fno-fast-math -fopenmp
  * (-ffp-contract=off: no fused multiply-add may change a rounding step.)
@@ -137,7 +137,8 @@ void oracle_quantize_ref_rows(const uint16_t *x, int dt, int64_t n_rows, int D,
 /*     (casts to fp16 first so scales/biases are fp16),                      */
 /*     Tests/KrillCoreTests/VerifyProfileTests.swift:70.                     */
 /*     The algorithm itself lives in the third-party mlx library (not in     */
-/*     the reference tree): restated from its published affine scheme.      */
+/*     the reference tree): restated from mlx's CPU affine quantize          */
+/*     (mlx/backend/cpu/quantized.cpp, mlx 0.31 via mlx-swift 0.31.4).       */
 /* ------------------------------------------------------------------------ */
 /*
  * Per group of `group` fp16 values w (computed in binary32):

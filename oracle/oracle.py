@@ -23,12 +23,20 @@ quantize_ref (a1)           (1) tiny-input brute force with exact rational
                             row -> scale 0 after fp16 rounding, q = 0, zero =
                             value; the row minimum always maps to q = 0);
                             (4) committed golden vectors (tests/golden/).
-quantize_mlx (a1')          PARITY UNPINNED against mlx (third-party, absent).
-                            Pinned only by invariants: q in [0,255], group
-                            round-trip error <= |scale|/2 + fp16 rounding of
-                            scale/bias, the zero point exactly representable
-                            when q0 != 0, and brute force of the restated
-                            formula with Fractions on tiny groups.
+quantize_mlx (a1')          MLX's CPU affine quantize (third-party mlx 0.31
+                            via mlx-swift 0.31.4, absent here) restated from
+                            its published algorithm and pinned choice by
+                            choice: groups built so that each plausible
+                            alternative changes a byte, with the bytes derived
+                            by hand -- ties round half to even, the scale is
+                            negative and the bias is the max when |max| >=
+                            |min|, constant groups store fp16(-1e-7) and the
+                            constant (0 -> bias 0), q uses the binary32
+                            scale edge/q0 (not its fp16 rounding) and divides
+                            (not a reciprocal multiply); an exact-rational
+                            restatement with explicit binary32 rounding on 240
+                            random groups; invariants (q in [0,255], round
+                            trip within half a step + fp16 rounding).
 dequant_ref (a3)            exhaustive check of the two-rounding formula for
                             every q byte against numpy float16 arithmetic.
 attention_f64 (a7/a8)       closed forms: one key -> output = that value row;
@@ -205,7 +213,7 @@ def quantize_ref(x_bits: np.ndarray, dt: int):
 
 
 def quantize_mlx(x_bits: np.ndarray, dt: int, group: int = 64):
-    """MLX-style affine 8-bit group quantizer (parity unpinned, see header)."""
+    """MLX affine 8-bit group quantizer (mlx's CPU affine quantize; pins in the header)."""
     x = np.ascontiguousarray(x_bits, dtype=np.uint16)
     D = x.shape[-1]
     G = D // group

@@ -205,6 +205,199 @@ def test_affine_matches_restatement_and_invariants(oracle):
     assert np.all(np.abs(deq[:20, 5]) <= q[:20, 5] * ds[:20, 0] + db[:20, 0] + 1e-12)
 
 
+# Pins of the affine rule's individual choices.  MLX's CPU affine quantize
+# (mlx/backend/cpu/quantized.cpp, mlx 0.31 via mlx-swift 0.31.4; not in the
+# reference tree) computes, per group, in binary32: the true min and max;
+# scale = max((max - min) / 255, 1e-7), negated unless |min| > |max|; edge =
+# min or max accordingly; q0 = rint(edge / scale); if q0 != 0 then
+# scale = edge / q0 and bias = edge, else bias = 0; q = clamp(rint((w - bias)
+# / scale), 0, 255); scale and bias stored in the input dtype (fp16 here).
+# _affine_exact restates it with exact rationals and explicit binary32
+# rounding of every operation; each _alt_* changes one choice.  The
+# constructed groups below are ones where each alternative yields a
+# different byte, with the expected bytes derived by hand in the comments.
+
+from fractions import Fraction as _Fr
+
+
+def _round_bin(x, mant_bits, emin):
+    """x rounded to the nearest binary float with `mant_bits` significand
+    bits and minimum normal exponent `emin` (ties to even), exactly."""
+    if x == 0:
+        return _Fr(0)
+    a = abs(x)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if a < _Fr(2) ** e:
+        e -= 1
+    elif a >= _Fr(2) ** (e + 1):
+        e += 1
+    ulp = _Fr(2) ** (max(e, emin) - (mant_bits - 1))
+    m = a / ulp
+    fl = m.numerator // m.denominator
+    r = m - fl
+    if r > _Fr(1, 2) or (r == _Fr(1, 2) and fl % 2 == 1):
+        fl += 1
+    return (fl * ulp) if x > 0 else -(fl * ulp)
+
+
+def _fl32(x):
+    return _round_bin(x, 24, -126)
+
+
+def _fl16(x):
+    return _round_bin(x, 11, -14)
+
+
+def _rint(x):
+    fl = x.numerator // x.denominator
+    r = x - fl
+    return fl + 1 if r > _Fr(1, 2) or (r == _Fr(1, 2) and fl % 2 == 1) else fl
+
+
+def _round_half_away(x):
+    a = abs(x)
+    n = (a + _Fr(1, 2)).numerator // (a + _Fr(1, 2)).denominator
+    return n if x >= 0 else -n
+
+
+_EPS32 = _fl32(_Fr(1, 10**7))
+
+
+def _affine_exact(w, rnd=_rint, scale_for_q=None, recip=False, minmax=False):
+    """One group (exact fp16 values as Fractions) -> (q list, scale, bias) as
+    Fractions before the fp16 storage rounding."""
+    mn, mx = min(w), max(w)
+    s = max(_fl32(_fl32(mx - mn) / 255), _EPS32)
+    if minmax:  # plain min/max affine: bias = min, positive scale
+        bias = mn
+    else:
+        side = abs(mn) > abs(mx)
+        s = s if side else -s
+        edge = mn if side else mx
+        q0 = rnd(_fl32(edge / s))
+        bias = _Fr(0)
+        if q0 != 0:
+            s = _fl32(edge / q0)
+            bias = edge
+    sq = s if scale_for_q is None else scale_for_q(s)
+    q = []
+    for x in w:
+        d = _fl32(x - bias)
+        v = _fl32(d * _fl32(1 / sq)) if recip else _fl32(d / sq)
+        q.append(min(max(rnd(v), 0), 255))
+    return q, s, bias
+
+
+def _alt_half_away(w):
+    return _affine_exact(w, rnd=_round_half_away)
+
+
+def _alt_fp16_scale(w):
+    return _affine_exact(w, scale_for_q=_fl16)
+
+
+def _alt_reciprocal(w):
+    return _affine_exact(w, recip=True)
+
+
+def _alt_minmax(w):
+    return _affine_exact(w, minmax=True)
+
+
+def _group(values, fill):
+    """64 fp16 values: `values` then `fill` repeated (fp16 bits, exact Fractions)."""
+    v = list(values) + [fill] * (64 - len(values))
+    bits = np.array(v, np.float16).view(np.uint16)
+    assert np.all(bits.view(np.float16).astype(np.float64) == np.array(v, np.float64)), "not fp16 values"
+    return bits, [_Fr(float(x)) for x in bits.view(np.float16).astype(np.float64)]
+
+
+def _f16_bits(x):
+    return int(np.float16(float(_fl16(x))).view(np.uint16))
+
+
+def _check_group(oracle, bits, w):
+    q, s, b = oracle.quantize_mlx(bits.reshape(1, 64), 0, 64)
+    eq, es, eb = _affine_exact(w)
+    assert list(q[0]) == eq
+    assert int(s[0, 0]) == _f16_bits(es) and int(b[0, 0]) == _f16_bits(eb)
+    return list(q[0]), int(s[0, 0]), int(b[0, 0])
+
+
+def test_affine_ties_round_half_to_even(oracle):
+    # min 0, max 255: scale0 = 1, |0| > |255| is false so scale = -1, edge =
+    # 255, q0 = -255, scale = 255 / -255 = -1, bias = 255; q = 255 - w.
+    # w = 126.5 -> 128.5 exactly: rint gives 128, half-away 129.
+    bits, w = _group([0.0, 255.0, 126.5, 125.5], 10.0)
+    q, s, b = _check_group(oracle, bits, w)
+    assert (q[0], q[1], q[2], q[3], q[4]) == (255, 0, 128, 130, 245)
+    assert s == 0xBC00 and b == 0x5BF8  # fp16 -1 and 255
+    assert _alt_half_away(w)[0][2] == 129
+
+
+def test_affine_edge_sign_and_zero_point(oracle):
+    # |max| >= |min| (max 8, min -4): scale = -(12/255) -> edge = 8, q0 =
+    # rint(8 / -(12/255)) = -170, scale = 8 / -170 < 0, bias = 8:
+    # q(8) = 0, q(-4) = 255, q(0) = 170 (zero sits on the grid).
+    bits, w = _group([8.0, -4.0, 0.0, 2.0], 1.0)
+    q, s, b = _check_group(oracle, bits, w)
+    assert (q[0], q[1], q[2]) == (0, 255, 170)
+    assert s & 0x8000 and b == 0x4800  # negative scale, bias fp16 8
+    # plain min/max quantization maps the other way round
+    mq = _alt_minmax(w)[0]
+    assert (mq[0], mq[1]) == (255, 0)
+    # |min| > |max| (min -8, max 4): positive scale, edge = -8 = bias
+    bits, w = _group([-8.0, 4.0, 0.0], 1.0)
+    q, s, b = _check_group(oracle, bits, w)
+    assert (q[0], q[1], q[2]) == (0, 255, 170)
+    assert not s & 0x8000 and b == 0xC800  # bias fp16 -8
+
+
+def test_affine_constant_groups(oracle):
+    # all zero: scale = max(0, 1e-7) negated (|0| > |0| is false), edge = 0,
+    # q0 = 0 -> bias = 0; stored scale fp16(-1e-7) = -2 * 2^-24 (0x8002)
+    bits, w = _group([], 0.0)
+    q, s, b = _check_group(oracle, bits, w)
+    assert q == [0] * 64 and s == 0x8002 and b == 0x0000
+    # constant 3: q0 = rint(3 / -1e-7) = -3e7, scale = 3 / -3e7, bias = 3
+    bits, w = _group([], 3.0)
+    q, s, b = _check_group(oracle, bits, w)
+    assert q == [0] * 64 and s == 0x8002 and b == 0x4200
+
+
+def test_affine_quantizes_with_the_binary32_scale_and_divides(oracle):
+    # min -7.62890625, max 4.33984375: edge = min, q0 = -255, scale =
+    # -7.62890625 / -255 (binary32, not an fp16 value).  w = 0.023406982...
+    # gives 164 with that scale and 163 with its fp16 rounding; w =
+    # 3.814453125 gives 244 dividing and 245 multiplying by the reciprocal.
+    bits, w = _group([-7.62890625, 4.33984375, 0.023406982421875, 3.814453125], 0.0)
+    q, s, b = _check_group(oracle, bits, w)
+    assert (q[0], q[1], q[2], q[3]) == (0, 255, 164, 244)
+    assert _alt_fp16_scale(w)[0][2] == 163
+    assert _alt_reciprocal(w)[0][3] == 245
+
+
+def test_affine_matches_the_exact_restatement_on_random_groups(oracle):
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((240, 64)).astype(np.float32) * rng.choice([1e-4, 0.02, 1, 30], (240, 1)).astype(np.float32)
+    x[:10, :] = np.abs(x[:10, :])     # one-signed groups
+    x[10:20, :] = -np.abs(x[10:20, :])
+    bits = oracle.f32_to_f16_bits(x)
+    q, s, b = oracle.quantize_mlx(bits, 0, 64)
+    wf = bits.view(np.float16).astype(np.float64)
+    differs = {"half_away": 0, "fp16_scale": 0, "minmax": 0}
+    for r in range(240):
+        w = [_Fr(float(v)) for v in wf[r]]
+        eq, es, eb = _affine_exact(w)
+        assert list(q[r]) == eq, r
+        assert int(s[r, 0]) == _f16_bits(es) and int(b[r, 0]) == _f16_bits(eb), r
+        differs["fp16_scale"] += _alt_fp16_scale(w)[0] != eq
+        differs["minmax"] += _alt_minmax(w)[0] != eq
+        differs["half_away"] += _alt_half_away(w)[0] != eq
+    # the scale-precision and sign choices show on ordinary data
+    assert differs["fp16_scale"] > 0 and differs["minmax"] > 0, differs
+
+
 def test_affine_bf16_input_is_cast_to_f16_first(oracle):
     rng = np.random.default_rng(6)
     x = rng.standard_normal((10, 64)).astype(np.float32)
