@@ -25,10 +25,12 @@
 // The 16-byte K chunks hold the 8 d of an A operand contiguously; V is stored
 // per d in exactly the token order in which the S^T accumulator hands P to
 // the P.V B operand.  Bytes become fp16 with one v_perm_b32 per pair (1024 + u,
-// the offset folded into the affine zero point for K, subtracted for V);
-// affine scale/bias are applied to the fp32 scores (per group) and folded
-// into the fp16 weights P*s_v.  The softmax max is raised lazily, so the
-// weights stay below 2^8 and most blocks skip the accumulator rescale.
+// affine mode centres the K and V bytes, u - 128, exact, so the fp32 sums
+// stay small, and adds the zero point plus 128 s on the side); affine
+// scale/bias are applied to the fp32 scores (per group) and folded into the
+// weights P*s_v, which enter P.V as a pair of fp16 operands (high and low
+// part) against the exact V bytes.  The softmax max is raised lazily, so
+// the weights stay below 2^8 and most blocks skip the accumulator rescale.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -43,10 +45,11 @@ __device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t 
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ half8_t bytes8_exact(uint2 w) {
-  const half2_t m1024 = half2_t{(_Float16)-1024.0f, (_Float16)-1024.0f};
-  const half2_t a = bytes01_plus1024(w.x) + m1024, b = bytes23_plus1024(w.x) + m1024;
-  const half2_t c = bytes01_plus1024(w.y) + m1024, d = bytes23_plus1024(w.y) + m1024;
+// Eight bytes as exact fp16 u - 128.
+__device__ __forceinline__ half8_t bytes8_centred(uint2 w) {
+  const half2_t m1152 = half2_t{(_Float16)-1152.0f, (_Float16)-1152.0f};
+  const half2_t a = bytes01_plus1024(w.x) + m1152, b = bytes23_plus1024(w.x) + m1152;
+  const half2_t c = bytes01_plus1024(w.y) + m1152, d = bytes23_plus1024(w.y) + m1152;
   return half8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
@@ -286,8 +289,8 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
       if constexpr (WIN) edge = edge || tbase < lo_hi;  // or below some row's window
 
       // ---- S^T = K . Q^T, four 16-token tiles.  Affine mode feeds the bytes
-      // as exact fp16 1024 + u and folds the offset into the zero point:
-      // q.k = s * (q.(1024 + u)) + (z - 1024 s) * sum q (per 64-d group).
+      // as exact fp16 u - 128 and folds the offset into the zero point:
+      // q.k = s * (q.(u - 128)) + (z + 128 s) * sum q (per 64-d group).
       float sc[4][NRT][4];
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
@@ -316,9 +319,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
             half2_t p3 = (bytes23_plus1024(kb.y) + m1024) * ks2 + kz2;
             A = half8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
           } else {
-            const half2_t p0 = bytes01_plus1024(kb.x), p1 = bytes23_plus1024(kb.x);
-            const half2_t p2 = bytes01_plus1024(kb.y), p3 = bytes23_plus1024(kb.y);
-            A = half8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+            A = bytes8_centred(kb);
           }
           const int g = MODE == MODE_AFFINE ? ks / 2 : 0;
 #pragma unroll
@@ -343,7 +344,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
 #pragma unroll
             for (int g = 0; g < G; ++g) {
               kss[g] = f16_bits_to_f32((uint16_t)(km[e * G + g] & 0xffffu));
-              kzz[g] = fmaf(-1024.0f, kss[g], f16_bits_to_f32((uint16_t)(km[e * G + g] >> 16)));
+              kzz[g] = fmaf(128.0f, kss[g], f16_bits_to_f32((uint16_t)(km[e * G + g] >> 16)));
             }
 #pragma unroll
             for (int rt = 0; rt < NRT; ++rt) {
@@ -418,9 +419,9 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
         l_part[rt] += ps;
       }
 
-      // ---- O^T += V^T . P^T over two 32-token groups; weights p * s_v in
-      // fp16 (below 2^8 * s_v), V bytes as exact fp16 u, the zero points summed
-      // on the side
+      // ---- O^T += V^T . P^T over two 32-token groups; weights p * s_v
+      // (below 2^8 * s_v) as fp16 high and low parts, V bytes as exact fp16
+      // u - 128, the zero points (and 128 s_v) summed on the side
 #pragma unroll
       for (int tg = 0; tg < 2; ++tg) {
         // logical k = 8*q4 + i  <->  token 32*tg + (i < 4 ? 4*q4 + i : 16 + 4*q4 + i - 4)
@@ -452,7 +453,13 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
               vzz[4 * h + e][g] = f16_bits_to_f32((uint16_t)(vm[e * G + g] >> 16));
             }
         }
-        half8_t Bw[NRT][G];
+        // Each binary32 weight w = p * s_v (affine) or p (row mode) goes in as
+        // two fp16 operands, w_hi = f16(w) and w_lo = f16(w - w_hi), against
+        // the same exact V operand: one fp16 weight would carry a relative
+        // error of 2^-11 into every product, up to 2^-11 of a group's value
+        // range in the output when a few keys hold the softmax weight; the
+        // pair leaves about 2^-22.
+        half8_t Bh[NRT][G], Bl[NRT][G];
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
 #pragma unroll
@@ -460,8 +467,13 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
             const float p = sc[2 * tg + (k >> 2)][rt][k & 3];
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-              Bw[rt][g][k] = (_Float16)(MODE == MODE_AFFINE ? p * vss[k][g] : p);
-              if constexpr (MODE == MODE_AFFINE) c_part[rt][g] = fmaf(p, vzz[k][g], c_part[rt][g]);
+              const float w = MODE == MODE_AFFINE ? p * vss[k][g] : p;
+              const _Float16 wh = (_Float16)w;
+              Bh[rt][g][k] = wh;
+              Bl[rt][g][k] = (_Float16)(w - (float)wh);
+              // the zero point and the 128 taken off the V bytes: p (z + 128 s)
+              if constexpr (MODE == MODE_AFFINE)
+                c_part[rt][g] = fmaf(p, fmaf(128.0f, vss[k][g], vzz[k][g]), c_part[rt][g]);
             }
           }
         }
@@ -485,11 +497,14 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
             half2_t p3 = (bytes23_plus1024(vb.y) + m1024) * sp[3] + zp[3];
             A = half8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
           } else {
-            A = bytes8_exact(vb);
+            A = bytes8_centred(vb);
           }
           const int g = MODE == MODE_AFFINE ? dt / 4 : 0;
 #pragma unroll
-          for (int rt = 0; rt < NRT; ++rt) oacc[rt][dt] = mfma16x16x32(A, Bw[rt][g], oacc[rt][dt]);
+          for (int rt = 0; rt < NRT; ++rt) {
+            oacc[rt][dt] = mfma16x16x32(A, Bh[rt][g], oacc[rt][dt]);
+            oacc[rt][dt] = mfma16x16x32(A, Bl[rt][g], oacc[rt][dt]);
+          }
         }
       }
       // every LDS read of this stage has returned: refill the rest

@@ -19,19 +19,22 @@
 //    16-byte loads that are contiguous across lanes in the d-chunk-major
 //    layout), turns byte pairs into fp16 (1024 + u) with one v_perm_b32, and
 //    accumulates v_dot2c_f32_f16 whose query operand is broadcast from the
-//    right lane of the row by DPP row_newbcast.  Affine mode uses linearity
-//    per 64-group:
-//      q.k = s * (q.(1024 + u) - 1024 * sum q) + z * sum q,
+//    right lane of the row by DPP row_newbcast.  Affine mode centres the
+//    bytes (u - 128, exact in fp16, so the fp32 sums stay small) and uses
+//    linearity per 64-group:
+//      q.k = s * (q.(u - 128)) + (z + 128 s) * sum q,
 //    so no element is dequantised.  Reference row mode dequantises exactly
 //    (f16(f16(u*s) + z), QuantizedKVCache.swift:200-204) before the dot.
 //  * online softmax in the log2 domain with a lazily raised running max: a
 //    block only pays for a wave reduction when some score exceeds the
 //    running max by more than 8 (a wave vote), so weights stay below 2^8;
-//  * weights w = p * s_v (fp16) go to LDS in V storage order; each lane
+//  * weights w = p * s_v (binary32) go to LDS in V storage order; each lane
 //    then owns D/64 V^T rows (d values), loaded as contiguous 16-byte pieces,
-//    and reduces token pairs with v_dot2c_f32_f16, 8 tokens at a time.  The
-//    V zero points and the 1024 offset collapse into one per-(row, group)
-//    term.
+//    turns 4 bytes at a time into exact binary32 values and accumulates
+//    w * u with fp32 FMAs.  The V zero points collapse into one per-(row,
+//    group) term.  (fp16 weights, as an earlier version used, put an error
+//    of up to 2^-11 of a group's value range into the output whenever a few
+//    keys hold the softmax weight.)
 //  * the next block's K and V are loaded as soon as the current block's
 //    registers are consumed, so loads overlap the other phase's math.
 // A sequence that lies inside one wave's range is written directly;
@@ -204,7 +207,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   constexpr int PPG = NP / G;  // pieces per scale group
   constexpr int DPL = D / 64;  // V^T rows (d values) per lane
 
-  __shared__ __attribute__((aligned(16))) uint16_t w_lds[NR * G * 64];
+  __shared__ __attribute__((aligned(16))) float w_lds[NR * G * 64];
   __shared__ __attribute__((aligned(16))) uint16_t sz_lds[2 * 64];
 
   const int lane = threadIdx.x;
@@ -321,6 +324,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   const int gl = MODE == MODE_AFFINE ? (DPL * lane) / 64 : 0;  // scale group of this lane's V rows
   const int pos = ((lane >> 5) << 5) + vpos(lane & 31);        // this lane's token in V order
   const half2_t m1024 = half2_t{(_Float16)-1024.0f, (_Float16)-1024.0f};
+  const half2_t m1152 = half2_t{(_Float16)-1152.0f, (_Float16)-1152.0f};
 
   uint4 kr[NP];
   uint4 vr[2][2 * DPL];
@@ -516,6 +520,9 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       if constexpr (MODE == MODE_REF) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) kp[i] = (kp[i] + m1024) * ks2 + kz2;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kp[i] = kp[i] + m1152;  // u - 128, exact
       }
       const int g = MODE == MODE_AFFINE ? p / PPG : 0;
       // the last piece of a scale group finishes accg[.][g]
@@ -553,7 +560,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
         for (int g = 0; g < G; ++g) {
           const float kss = f16_bits_to_f32((uint16_t)(km[g] & 0xffffu));
           const float kzz = f16_bits_to_f32((uint16_t)(km[g] >> 16));
-          v += kss * accg[r][g] + (kzz - 1024.0f * kss) * qs[r][g];
+          v += kss * accg[r][g] + (kzz + 128.0f * kss) * qs[r][g];
         }
       } else {
         v = accg[r][0];
@@ -595,6 +602,9 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     // ---- weights to LDS in V storage order
     bool valid = tbase + lane < len;
     if constexpr (WIN) valid = valid && tbase + lane >= wst;  // rows below the window are not data
+    // The weights stay binary32 (p * s_v rounded once): an fp16 weight
+    // would carry a relative error of 2^-11 into p * s_v * u, up to 2^-11 of
+    // the group's value range in the output when a few keys hold the weight.
     if constexpr (MODE == MODE_AFFINE) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -602,14 +612,13 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
         const float vzf = valid ? f16_bits_to_f32((uint16_t)(vm[g] >> 16)) : 0.0f;
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-          const _Float16 wv = (_Float16)(pr[r] * vsf);
-          w_lds[(r * G + g) * 64 + pos] = __builtin_bit_cast(uint16_t, wv);
-          c_part[r][g] += pr[r] * vzf - 1024.0f * (float)wv;
+          w_lds[(r * G + g) * 64 + pos] = pr[r] * vsf;
+          c_part[r][g] = fmaf(pr[r], vzf, c_part[r][g]);
         }
       }
     } else {
 #pragma unroll
-      for (int r = 0; r < NR; ++r) w_lds[r * 64 + pos] = __builtin_bit_cast(uint16_t, (_Float16)pr[r]);
+      for (int r = 0; r < NR; ++r) w_lds[r * 64 + pos] = pr[r];
       sz_lds[pos] = valid ? (uint16_t)(vm[0] & 0xffffu) : (uint16_t)0;
       sz_lds[64 + pos] = valid ? (uint16_t)(vm[0] >> 16) : (uint16_t)0;
     }
@@ -637,53 +646,56 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       }
     }
 
-    // ---- P.V: lane owns V^T rows d = DPL*lane .. +DPL.  Chunks of 8 tokens
-    // (4 pairs): the chunk's V bytes become fp16 pairs once and serve every
-    // row; the weights of one (chunk, row) are one 16-byte LDS read, issued
-    // two steps ahead of their use.
-    const uint32_t *w32 = reinterpret_cast<const uint32_t *>(w_lds);
-    constexpr int NSTEP = 8 * NR;  // (tg, chunk, row) steps
-    auto wread = [&](int k) -> uint4 {
-      const int r = k % NR, c = k / NR;  // c = tg * 4 + chunk
-      return *reinterpret_cast<const uint4 *>(w32 + (r * G + gl) * 32 + 4 * c);
+    // ---- P.V: lane owns V^T rows d = DPL*lane .. +DPL.  Steps of 4 tokens
+    // (one V word per row d): affine mode turns the 4 bytes into exact
+    // binary32 values u (v_cvt_f32_ubyte) and accumulates w * u with fp32
+    // FMAs, the bias term sum p * z coming per (row, group) at the end; row
+    // mode dequantizes as the reference does, f16(f16(u * s) + z), and
+    // accumulates p * v.  The 4 weights of one (step, row) are one 16-byte
+    // LDS read, issued two steps ahead of their use.
+    constexpr int NSTEP = 16 * NR;  // (tg, chunk, half, row) steps
+    auto wread = [&](int k) -> float4 {
+      const int r = k % NR, c = k / NR;  // c = 2 * (tg * 4 + chunk) + half: positions 4c .. 4c + 3
+      return *reinterpret_cast<const float4 *>(w_lds + (r * G + gl) * 64 + 4 * c);
     };
-    uint4 wq0 = wread(0), wq1 = wread(1 < NSTEP ? 1 : 0);
+    float4 wq0 = wread(0), wq1 = wread(1 < NSTEP ? 1 : 0);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const int tg = c >> 2, ch = c & 3;
-      half2_t vp[DPL][4];
+    for (int c = 0; c < 16; ++c) {
+      const int tg = c >> 3, ch = (c >> 1) & 3, hf = c & 1;
+      float vf[DPL][4];
 #pragma unroll
       for (int e = 0; e < DPL; ++e) {
-        // conversion of this chunk waits for the previous chunk's dots
+        // conversion of this step waits for the previous step's FMAs
         if (c > 0) order_after(vr[tg][2 * e + (ch >> 1)], acc[NR - 1][DPL - 1]);
         const uint4 w = vr[tg][2 * e + (ch >> 1)];
-        const uint32_t w0 = (ch & 1) ? w.z : w.x, w1 = (ch & 1) ? w.w : w.y;
-        vp[e][0] = bytes01_plus1024(w0);
-        vp[e][1] = bytes23_plus1024(w0);
-        vp[e][2] = bytes01_plus1024(w1);
-        vp[e][3] = bytes23_plus1024(w1);
-      }
-      if constexpr (MODE == MODE_REF) {
-        const uint4 sp4 = *reinterpret_cast<const uint4 *>(sz_lds + 8 * c);
-        const uint4 zp4 = *reinterpret_cast<const uint4 *>(sz_lds + 64 + 8 * c);
-        const uint32_t sp[4] = {sp4.x, sp4.y, sp4.z, sp4.w}, zp[4] = {zp4.x, zp4.y, zp4.z, zp4.w};
+        const uint32_t wd = (ch & 1) ? (hf ? w.w : w.z) : (hf ? w.y : w.x);
+        if constexpr (MODE == MODE_AFFINE) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int e = 0; e < DPL; ++e) vp[e][i] = (vp[e][i] + m1024) * u32_as_h2(sp[i]) + u32_as_h2(zp[i]);
+          for (int i = 0; i < 4; ++i) vf[e][i] = (float)((wd >> (8 * i)) & 0xffu);
+        } else {
+          const half2_t lo = bytes01_plus1024(wd), hi = bytes23_plus1024(wd);
+          const uint2 sp2 = *reinterpret_cast<const uint2 *>(sz_lds + 4 * c);
+          const uint2 zp2 = *reinterpret_cast<const uint2 *>(sz_lds + 64 + 4 * c);
+          const half2_t v0 = (lo + m1024) * u32_as_h2(sp2.x) + u32_as_h2(zp2.x);
+          const half2_t v1 = (hi + m1024) * u32_as_h2(sp2.y) + u32_as_h2(zp2.y);
+          vf[e][0] = (float)v0.x;
+          vf[e][1] = (float)v0.y;
+          vf[e][2] = (float)v1.x;
+          vf[e][3] = (float)v1.y;
+        }
       }
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
         const int k = c * NR + r;
-        const uint4 wc = wq0;
+        const float4 wc = wq0;
         asm volatile("" ::: "memory");
         wq0 = wq1;
         if (k + 2 < NSTEP) wq1 = wread(k + 2);
-        const uint32_t ww[4] = {wc.x, wc.y, wc.z, wc.w};
+        const float ww[4] = {wc.x, wc.y, wc.z, wc.w};
 #pragma unroll
         for (int e = 0; e < DPL; ++e)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[r][e] = dot2(u32_as_h2(ww[i]), vp[e][i], acc[r][e]);
+          for (int i = 0; i < 4; ++i) acc[r][e] = __builtin_fmaf(ww[i], vf[e][i], acc[r][e]);
       }
     }
     // K and V registers are free.  With three waves per SIMD the next
