@@ -282,6 +282,26 @@ int32_t krill_decode_append_attention(krill_pool_t pool, int32_t layer, const vo
                                       int32_t max_seq_len, int32_t Hq, float scale, void *dev_out,
                                       int32_t out_dtype, void *dev_ws, size_t ws_bytes,
                                       krill_stream_t stream);
+/* krill_decode_append_attention without a workspace argument: the split-K
+ * partials go to a static device array of 32 MiB (KRILL_NOALLOC_SCRATCH_BYTES)
+ * that each GPU holds from library load to process end.  No counterpart in
+ * the reference: this entry point is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, hosts
+ * that forbid allocation); it calls no hipMalloc/hipFree.  Same arguments,
+ * kernels, output and pool bytes as krill_decode_append_attention.  A step
+ * whose workspace (krill_attention_workspace_size, Lq = 1) exceeds the
+ * array fails with KRILL_E_RANGE before any launch.  Every call on one GPU
+ * shares that GPU's array and leaves its partials there (nothing in it
+ * needs to start at zero): calls that overlap on one GPU -- on different
+ * streams, or from several pools or threads -- race, so keep them on one
+ * stream or ordered by events. */
+#define KRILL_NOALLOC_SCRATCH_BYTES (32u << 20)
+int32_t krill_decode_append_attention_noalloc(krill_pool_t pool, int32_t layer, const void *dev_q,
+                                              const void *dev_k_new, const void *dev_v_new, int64_t stride_b,
+                                              int64_t stride_h, const int32_t *dev_block_tables,
+                                              const int32_t *dev_seq_lens, int32_t B, int32_t max_blocks,
+                                              int32_t max_seq_len, int32_t Hq, float scale, void *dev_out,
+                                              int32_t out_dtype, krill_stream_t stream);
 /* The decode step with RoPE as well: krill_decode_append_attention for
  * unrotated queries and new K rows, each turned first by its token's
  * position seq_lens[b] - 1 exactly as krill_quantize_append_rope turns K

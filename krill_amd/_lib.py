@@ -157,6 +157,8 @@ SIGNATURES = {
                                ctypes.c_size_t, P],
     "krill_decode_append_attention": [P, I32, P, P, P, I64, I64, P, P, I32, I32, I32, I32, ctypes.c_float, P,
                                       I32, P, ctypes.c_size_t, P],
+    "krill_decode_append_attention_noalloc": [P, I32, P, P, P, I64, I64, P, P, I32, I32, I32, I32, ctypes.c_float,
+                                              P, I32, P],
     "krill_window_workspace_size": [P, I32, I32, I32, I32, I32, I32, ctypes.POINTER(ctypes.c_size_t)],
     "krill_attention_windowed": [P, I32, P, I32, P, P, P, I32, I32, I32, I32, I32, ctypes.c_float, P, I32, P,
                                  ctypes.c_size_t, P],

@@ -14,6 +14,7 @@
 #include "common.hpp"
 #include "kdev.hpp"
 #include "launch.hpp"
+#include "scratch.hpp"
 
 using krill::fail;
 
@@ -140,6 +141,9 @@ int32_t krill_pool_create(const krill_pool_desc *desc, krill_stream_t stream, kr
       if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
       e = hipDeviceGetAttribute(&g.num_cus, hipDeviceAttributeMultiprocessorCount, p->device);
       if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(multiprocessor count)");
+      // this device's copy of the static scratch (krill_decode_append_attention_noalloc)
+      e = krill::scratch_init(p->device);
+      if (e != hipSuccess) return hip_fail(e, "address of the static scratch");
       void *mem = nullptr;
       e = hipMalloc(&mem, static_cast<size_t>(total));
       if (e != hipSuccess) {
@@ -573,7 +577,7 @@ static int32_t run_attention(krill_pool_t pool, int32_t layer, const void *dev_q
                              const int32_t *dev_block_tables, const int32_t *dev_seq_lens, int32_t B,
                              int32_t max_blocks, int32_t max_seq_len, int32_t Hq, float scale, void *dev_out,
                              int32_t out_dtype, void *dev_ws, size_t ws_bytes, krill_stream_t stream,
-                             const NewTokens &nt = NewTokens()) {
+                             const NewTokens &nt = NewTokens(), bool static_scratch = false) {
   if (int32_t rc = check_device_pool(pool, layer)) return rc;
   if (B < 0 || max_blocks < 0 || max_seq_len < 0) return fail(KRILL_E_INVAL, "negative B, max_blocks or length");
   if (B == 0) return KRILL_OK;
@@ -589,6 +593,11 @@ static int32_t run_attention(krill_pool_t pool, int32_t layer, const void *dev_q
   if (pr == -2) return fail(KRILL_E_UNSUPPORTED, "VALU path handles at most 8 query rows per KV head");
   if (pr != 0) return fail(KRILL_E_INVAL, "Hq %d not a multiple of %d KV heads, or bad B/Lq/length", Hq,
                            pool->geom.Hkv);
+  if (static_scratch && plan.ws_bytes > ws_bytes)
+    return fail(KRILL_E_RANGE,
+                "this step needs %zu bytes of workspace, more than the %zu-byte static scratch "
+                "(krill_decode_append_attention takes a workspace of any size)",
+                plan.ws_bytes, ws_bytes);
   if (ws_bytes < plan.ws_bytes || (plan.ws_bytes > 0 && !dev_ws))
     return fail(KRILL_E_INVAL, "workspace of %zu bytes < %zu required", ws_bytes, plan.ws_bytes);
   krill::AttnLaunch a;
@@ -649,6 +658,31 @@ int32_t krill_decode_append_attention(krill_pool_t pool, int32_t layer, const vo
     nt.sh = stride_h;
     return run_attention(pool, layer, dev_q, 1, dev_block_tables, dev_seq_lens, B, max_blocks, max_seq_len, Hq, scale,
                          dev_out, out_dtype, dev_ws, ws_bytes, stream, nt);
+  });
+}
+
+int32_t krill_decode_append_attention_noalloc(krill_pool_t pool, int32_t layer, const void *dev_q,
+                                              const void *dev_k_new, const void *dev_v_new, int64_t stride_b,
+                                              int64_t stride_h, const int32_t *dev_block_tables,
+                                              const int32_t *dev_seq_lens, int32_t B, int32_t max_blocks,
+                                              int32_t max_seq_len, int32_t Hq, float scale, void *dev_out,
+                                              int32_t out_dtype, krill_stream_t stream) {
+  return krill::guarded([&]() -> int32_t {
+    krill::clear_error();
+    if (int32_t rc = check_device_pool(pool, layer)) return rc;
+    if (B > 0 && (!dev_k_new || !dev_v_new)) return fail(KRILL_E_INVAL, "NULL new K/V pointer");
+    if (stride_b < 0 || stride_h < 0) return fail(KRILL_E_INVAL, "negative stride");
+    // the device address of this GPU's scratch array, resolved when the pool
+    // was created on it (never the array's host-side name)
+    void *scratch = krill::scratch_ptr(pool->device);
+    if (!scratch) return fail(KRILL_E_STATE, "static scratch of device %d not resolved", pool->device);
+    NewTokens nt;
+    nt.k = dev_k_new;
+    nt.v = dev_v_new;
+    nt.sb = stride_b;
+    nt.sh = stride_h;
+    return run_attention(pool, layer, dev_q, 1, dev_block_tables, dev_seq_lens, B, max_blocks, max_seq_len, Hq, scale,
+                         dev_out, out_dtype, scratch, krill::kScratchBytes, stream, nt, true);
   });
 }
 

@@ -20,7 +20,7 @@ RT="$("$CXX" -print-resource-dir)/lib/linux"
 SANS=("$@")
 [ ${#SANS[@]} -eq 0 ] && SANS=(address thread)
 
-for o in kv_ops attn_valu attn_mfma; do
+for o in kv_ops attn_valu attn_mfma scratch; do
   [ -f "$HERE/_build/$o.o" ] || { echo "missing $HERE/_build/$o.o: run make in $HERE first" >&2; exit 2; }
 done
 
@@ -39,7 +39,7 @@ for san in "${SANS[@]}"; do
   "$CXX" -std=c++17 -O1 -g -fPIC -fno-omit-frame-pointer -fsanitize="$san" \
     -c "$HERE/block_manager.cpp" -o "$out/block_manager.o"
   "$CXX" -shared -fPIC --hip-link --offload-arch="$ARCH" -fsanitize="$san" -shared-libsan -o "$out/libkrillhip.so" \
-    "$out/capi.o" "$out/block_manager.o" "$HERE/_build/kv_ops.o" "$HERE/_build/attn_valu.o" "$HERE/_build/attn_mfma.o"
+    "$out/capi.o" "$out/block_manager.o" "$HERE/_build/kv_ops.o" "$HERE/_build/attn_valu.o" "$HERE/_build/attn_mfma.o" "$HERE/_build/scratch.o"
 
   tree="$(mktemp -d)"
   trap 'rm -rf "$tree"' EXIT
