@@ -96,3 +96,22 @@ def oracle_attention(pool, filled: Filled, layer: int, q_bits: np.ndarray, dt: s
             for r in range(R * Lq):
                 out[b, hk * R + (r % R), r // R] = o[r]
     return out
+
+
+def check_snapshot(snap, filled, layer, left_pad=False):
+    """A gathered snapshot equals the oracle's quantization of `filled`, byte
+    for byte, with zero bytes in the padding."""
+    S = snap["keys"].shape[2]
+    got = {k: v.cpu().numpy() for k, v in snap.items()}
+    for b, T in enumerate(filled.lens):
+        kq, ks, kz, vq, vs, vz = filled.expected(layer, b)
+        sl = slice(S - T, S) if left_pad else slice(0, T)
+        pad = slice(0, S - T) if left_pad else slice(T, S)
+        np.testing.assert_array_equal(got["keys"][b, :, sl], kq)
+        np.testing.assert_array_equal(got["values"][b, :, sl], vq)
+        np.testing.assert_array_equal(got["key_scales"][b, :, sl].view(np.uint16), ks)
+        np.testing.assert_array_equal(got["key_zeros"][b, :, sl].view(np.uint16), kz)
+        np.testing.assert_array_equal(got["value_scales"][b, :, sl].view(np.uint16), vs)
+        np.testing.assert_array_equal(got["value_zeros"][b, :, sl].view(np.uint16), vz)
+        for name in got:
+            assert not np.any(got[name][b, :, pad].view(np.uint8)), f"{name} padding not zero"

@@ -5,7 +5,7 @@ work); attention within 2e-3 max-abs of the float64 oracle (fp32 output)."""
 import numpy as np
 import pytest
 
-from kvutil import DT, MODE, Filled, i32, oracle_attention, rand_bits, to_dev
+from kvutil import DT, MODE, Filled, check_snapshot, i32, oracle_attention, rand_bits, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -25,23 +25,6 @@ def make_pool(H, D, mode, dt, blocks=64, layers=1, seed=11, **kw):
 
 def gpu(t):
     return t.cpu().numpy()
-
-
-def check_snapshot(snap, filled, layer, left_pad=False):
-    S = snap["keys"].shape[2]
-    got = {k: gpu(v) for k, v in snap.items()}
-    for b, T in enumerate(filled.lens):
-        kq, ks, kz, vq, vs, vz = filled.expected(layer, b)
-        sl = slice(S - T, S) if left_pad else slice(0, T)
-        pad = slice(0, S - T) if left_pad else slice(T, S)
-        np.testing.assert_array_equal(got["keys"][b, :, sl], kq)
-        np.testing.assert_array_equal(got["values"][b, :, sl], vq)
-        np.testing.assert_array_equal(got["key_scales"][b, :, sl].view(np.uint16), ks)
-        np.testing.assert_array_equal(got["key_zeros"][b, :, sl].view(np.uint16), kz)
-        np.testing.assert_array_equal(got["value_scales"][b, :, sl].view(np.uint16), vs)
-        np.testing.assert_array_equal(got["value_zeros"][b, :, sl].view(np.uint16), vz)
-        for name in got:
-            assert not np.any(got[name][b, :, pad].view(np.uint8)), f"{name} padding not zero"
 
 
 @pytest.mark.parametrize("mode", ["ref_row", "affine_g64"])
