@@ -12,10 +12,12 @@ names and argument meaning:
   (PrefixCache.swift:161-308, :369-400, :511-551)
 
 The caches of one sequence share one block table, so all layers of a
-sequence hold the same token positions: a layer may append only the
-positions the sequence's other layers are also appending, and truncate /
-reset / restore apply to the whole sequence (the engine always does these to
-every layer together, InferenceEngine.swift:1402-1417).
+sequence address the same token positions (each layer has its own bytes at
+each position): the sequence reserves positions up to the longest layer,
+a layer appends at its own length, truncate / reset apply to the whole
+sequence (the engine always does these to every layer together,
+InferenceEngine.swift:1402-1417), and restore_quantized replaces one layer's
+contents, as the reference's does.
 """
 from __future__ import annotations
 
@@ -71,18 +73,25 @@ class SequenceKV:
     def length(self) -> int:
         return self.pool.seq_length(self.seq)
 
-    def slots_for(self, layer: int, n: int) -> np.ndarray:
-        """Physical slots of positions [layer_len, layer_len + n) of `layer`,
-        reserving them when this layer is the first to reach them."""
-        start = self.layer_len[layer]
+    def slots_for(self, layer: int, n: int, start: int | None = None) -> np.ndarray:
+        """Physical slots of positions [start, start + n) (default: the
+        layer's length), reserving the positions beyond the sequence's length
+        (copy-on-write of a shared tail block included)."""
+        start = self.layer_len[layer] if start is None else start
         have = self.length
+        if start > have:
+            raise RuntimeError(f"layer {layer} writes at {start} while the sequence holds {have}")
         if start + n > have:
-            if start != have:
-                raise RuntimeError(f"layer {layer} appends at {start} while the sequence holds {have}")
-            self.pool.reserve_append(self.seq, n)
+            self.pool.reserve_append(self.seq, start + n - have)
         table = self.pool.block_table(self.seq)
         pos = np.arange(start, start + n)
         return (table[pos // 64] * 64 + pos % 64).astype(np.int32)
+
+    def shrink_to_layers(self):
+        """Release the positions beyond the longest layer."""
+        top = max(self.layer_len) if self.layer_len else 0
+        if top < self.length:
+            self.pool.seq_truncate(self.seq, top)
 
     def truncate(self, n: int):
         """QuantizedKVCache.truncate semantics (no-op unless 0 <= n < length)."""
@@ -155,17 +164,29 @@ class PagedQuantizedKVCache:
         return QuantizedKVSnapshot.from_dict(self.s.pool.gather(self.layer, tables, lens, n))
 
     def restore_quantized(self, snap: QuantizedKVSnapshot):
-        """restoreQuantized(_:) (QuantizedKVCache.swift:122-129) into fresh blocks."""
+        """restoreQuantized(_:) (QuantizedKVCache.swift:122-129): this layer's
+        contents become the snapshot's S tokens; the other layers keep
+        theirs.  The bytes are copied into the pool, so later appends or
+        truncates never change the snapshot.  Positions the sequence already
+        holds are overwritten in place, which a block shared with another
+        sequence or a prefix entry must not be: restoring into those raises
+        (restore into a fresh cache instead, as the prefix replay does)."""
         torch = _torch()
+        s, p = self.s, self.s.pool
         S = snap.sequence_length
-        if self.s.layer_len[self.layer] != 0:
-            if any(x != 0 for x in self.s.layer_len) and self.s.length > 0:
-                self.s.reset()
-        slots = self.s.slots_for(self.layer, S)
-        dev = snap.keys.device
-        self.s.pool.scatter(self.layer, snap.as_dict(), torch.zeros(1, dtype=torch.int32, device=dev),
-                            torch.as_tensor(slots.reshape(1, S), device=dev))
-        self.s.layer_len[self.layer] = S
+        in_place = min(S, s.length)
+        if in_place > 0:
+            held = s.pool.block_table(s.seq)[: (in_place + 63) // 64]
+            if (p.refcounts()[held] > 1).any():
+                raise RuntimeError("restore_quantized would overwrite blocks shared with another sequence "
+                                   "or a prefix entry; restore into a fresh cache")
+        if S > 0:
+            slots = s.slots_for(self.layer, S, start=0)
+            dev = snap.keys.device
+            p.scatter(self.layer, snap.as_dict(), torch.zeros(1, dtype=torch.int32, device=dev),
+                      torch.as_tensor(slots.reshape(1, S), device=dev))
+        s.layer_len[self.layer] = S
+        s.shrink_to_layers()
 
     def truncate(self, n: int):
         self.s.truncate(n)
@@ -193,7 +214,9 @@ class PrefixCache:
     Memory tier: the library's entries, frozen forks of a sequence: storing
     shares its blocks (refcounted, no copy) and a hit forks a new sequence
     from the entry.  Disk tier (``cache_dir`` set): every stored entry is also
-    written as ``<key>.q8.safetensors`` (krill_amd.q8file), and a lookup that
+    written as ``<key>.q8.safetensors`` (krill_amd.q8file; the bytes are
+    copied to the host at store time and the file is written behind, on the
+    process's background writer, unless ``write_behind`` is False), and a lookup that
     misses in memory at a length tries the file of that length before the
     next shorter one (PrefixCache.swift:273-308); a file hit is restored into
     fresh blocks and becomes a memory entry again.  The reference always has
@@ -203,7 +226,7 @@ class PrefixCache:
     longest-prefix hits."""
 
     def __init__(self, pool: KVPool, model_id: str = "", cache_dir=None, disk_budget_gb=None,
-                 max_entry_gb=None, min_prefix_len: int = 8):
+                 max_entry_gb=None, min_prefix_len: int = 8, write_behind: bool = True):
         from .q8file import DiskTier, _env_gb
 
         self.pool = pool
@@ -213,6 +236,7 @@ class PrefixCache:
         gb = max_entry_gb if max_entry_gb is not None else _env_gb("KRILL_PREFIX_CACHE_MAX_ENTRY_GB")
         gb = 4.0 if gb is None else gb
         self.max_entry_bytes = -1 if gb <= 0 else int(gb * 1_000_000_000)
+        self.write_behind = write_behind
 
     @staticmethod
     def common_prefix_length(a, b) -> int:
@@ -240,8 +264,18 @@ class PrefixCache:
             return False
         stored = self.pool.prefix_store(seq, tokens, self.model_id, media_hash)
         if stored and self.disk is not None and self.disk.enabled:
-            self.disk.write(self._key(tokens, media_hash), self._layers_of(seq, len(tokens)))
+            # the bytes come to the host now (the entry's blocks may be
+            # evicted and reused later); the file write goes behind
+            self.disk.write(self._key(tokens, media_hash), self._layers_of(seq, len(tokens)),
+                            background=self.write_behind)
         return stored
+
+    def wait_for_disk_writes(self):
+        """Until every queued file write has finished (waitForDiskWrites,
+        PrefixCache.swift:760-766)."""
+        from .q8file import wait_for_disk_writes
+
+        wait_for_disk_writes()
 
     def lookup_quantized(self, tokens, media_hash=None):
         """(prefix_len, entry_seq) of an exact entry, or (0, None)."""
@@ -273,7 +307,10 @@ class PrefixCache:
 
     @property
     def disk_count(self) -> int:
-        return self.disk.count if self.disk is not None else 0
+        if self.disk is None:
+            return 0
+        self.wait_for_disk_writes()
+        return self.disk.count
 
     def clear(self):
         self.pool.prefix_clear()

@@ -11,6 +11,12 @@ and write the reference's files; affine pools store their G = D/64 groups
 under the same names.  File name: the 16-hex-digit FNV-1a v3 entry key
 (PrefixCache.swift:511-532) plus ``.q8.safetensors`` (:499).
 
+Writes can go behind (PrefixCache.swift:20-21, :397-399): one background
+writer thread shared by every disk tier of the process, like the
+reference's serial disk queue; the caller hands over host arrays, so the
+write never touches the pool.  A load of a file whose write is still queued
+waits for the queue first, and the queue drains at interpreter exit.
+
 Disk budget (PrefixCache.swift:98-113, :600-695): a running byte counter,
 seeded by one directory scan on the first write; a write that takes it over
 the budget evicts the oldest files by modification time down to 90 % of the
@@ -19,7 +25,9 @@ the disk tier, a negative budget disables eviction.
 """
 from __future__ import annotations
 
+import atexit
 import os
+import queue
 import threading
 from pathlib import Path
 
@@ -77,6 +85,55 @@ def _env_gb(name: str):
         return None
 
 
+class _WriteQueue:
+    """The process's background writer: jobs run one at a time, in order."""
+
+    def __init__(self):
+        self._q = queue.Queue()
+        self._lock = threading.Lock()
+        self._pending = {}  # path -> queued writes
+        self._thread = None
+        self.errors = 0  # jobs that raised (a write-behind failure is not reported to the caller)
+
+    def submit(self, path: Path, job):
+        with self._lock:
+            self._pending[path] = self._pending.get(path, 0) + 1
+            if self._thread is None:
+                self._thread = threading.Thread(target=self._run, name="krill-disk-writer", daemon=True)
+                self._thread.start()
+        self._q.put((path, job))
+
+    def _run(self):
+        while True:
+            path, job = self._q.get()
+            try:
+                job()
+            except Exception:
+                self.errors += 1
+            finally:
+                with self._lock:
+                    n = self._pending.pop(path, 1) - 1
+                    if n > 0:
+                        self._pending[path] = n
+                self._q.task_done()
+
+    def pending(self, path: Path) -> bool:
+        with self._lock:
+            return path in self._pending
+
+    def wait(self):
+        """Until every write queued so far has finished (waitForDiskWrites)."""
+        self._q.join()
+
+
+_WRITER = _WriteQueue()
+atexit.register(_WRITER.wait)
+
+
+def wait_for_disk_writes():
+    _WRITER.wait()
+
+
 class DiskTier:
     """The prefix cache's disk tier over one directory."""
 
@@ -100,9 +157,17 @@ class DiskTier:
     def _scan_bytes(self) -> int:
         return sum(p.stat().st_size for p in self.dir.iterdir() if p.name.endswith(".safetensors"))
 
-    def write(self, key: int, layers) -> bool:
+    def write(self, key: int, layers, background: bool = False) -> bool:
+        """Write the entry's file (host arrays `layers`), now or on the
+        background writer; True when a write was done or queued."""
         if not self.enabled:
             return False
+        if background:
+            _WRITER.submit(self.path(key), lambda: self._write_now(key, layers))
+            return True
+        return self._write_now(key, layers)
+
+    def _write_now(self, key: int, layers) -> bool:
         p = self.path(key)
         prior = p.stat().st_size if p.exists() else 0
         save_entry(p, layers, metadata={"format": "mlx"})
@@ -123,6 +188,8 @@ class DiskTier:
         if not self.enabled:
             return None
         p = self.path(key)
+        if _WRITER.pending(p):
+            _WRITER.wait()
         if not p.exists():
             return None
         try:
@@ -163,6 +230,7 @@ class DiskTier:
             self._seeded = True
 
     def clear(self):
+        _WRITER.wait()  # no queued write lands after the clear
         for p in list(self.dir.iterdir()):
             if p.is_file():
                 p.unlink()

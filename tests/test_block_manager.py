@@ -647,3 +647,56 @@ def test_disk_scan_probes_each_length_once(tmp_path):
     assert cache.lookup_quantized(toks[:16])[0] == 12
     assert calls == [16, 12]
     p.close()
+
+
+def test_cache_layers_share_positions_and_restore_replaces_one_layer():
+    """The reference-shaped cache's host bookkeeping (no device work): layers
+    append at their own lengths, the sequence holds positions up to the
+    longest layer, truncate applies to all layers, a restore of a shorter
+    layer releases the positions no layer holds any more."""
+    from krill_amd.cache import make_quantized_kv_caches
+
+    p = host_pool()
+    c0, c1 = make_quantized_kv_caches(p)
+    s0 = c0.s.slots_for(0, 70)
+    c0.s.layer_len[0] += 70
+    assert p.seq_length(c0.s.seq) == 70
+    s1 = c1.s.slots_for(1, 70)  # the positions layer 0 reserved
+    c1.s.layer_len[1] += 70
+    np.testing.assert_array_equal(s0, s1)
+    assert p.seq_length(c0.s.seq) == 70
+    c1.s.slots_for(1, 10)  # layer 1 runs ahead
+    c1.s.layer_len[1] += 10
+    assert p.seq_length(c0.s.seq) == 80 and c0.sequence_length == 70
+    c0.truncate(75)  # applies to the sequence: layer 1 drops to 75, layer 0 keeps 70
+    assert (c0.sequence_length, c1.sequence_length, p.seq_length(c0.s.seq)) == (70, 75, 75)
+    with pytest.raises(RuntimeError):
+        c0.s.slots_for(0, 1, start=76)  # beyond the sequence
+    c1.s.layer_len[1] = 70  # as a restore of a 70-token snapshot leaves it
+    c1.s.shrink_to_layers()
+    assert p.seq_length(c0.s.seq) == 70
+    p.close()
+
+
+def test_krill_kernels_validate_the_batch_on_the_host():
+    from krill_amd import KrillKernels
+    from krill_amd.cache import make_quantized_kv_caches
+
+    p = host_pool()
+    a = make_quantized_kv_caches(p)
+    b = make_quantized_kv_caches(p)
+    q = np.zeros((2, 4, 1, 128), np.float32)
+    with pytest.raises(ValueError, match="empty"):
+        KrillKernels.paged_decode_attention(q, [], 0.1)
+    with pytest.raises(ValueError, match="same layer"):
+        KrillKernels.paged_decode_attention(q, [a[0], b[1]], 0.1)
+    with pytest.raises(ValueError, match="twice"):
+        KrillKernels.paged_decode_attention(q, [a[0], a[0]], 0.1)
+    with pytest.raises(ValueError, match="queries"):
+        KrillKernels.paged_decode_attention(q[:1], [a[0], b[0]], 0.1)
+    with pytest.raises(ValueError, match="together"):
+        KrillKernels.paged_decode_attention(q, [a[0], b[0]], 0.1, keys=q)
+    with pytest.raises(TypeError):
+        KrillKernels.paged_decode_attention(q, [a[0], object()], 0.1)
+    assert isinstance(KrillKernels.status(), str)
+    p.close()

@@ -3,8 +3,10 @@ as ``<key>.q8.safetensors`` (key: the library's FNV-1a v3 prefix key); after
 the memory entries are gone, a lookup restores it from the file into fresh
 blocks, and the restored sequence holds the original bytes (every layer,
 token, scale and zero) and gives the same attention output bit for bit.
-The file's arrays equal the pool's gathered snapshot, so a row-mode pool
-writes the reference's on-disk entries (PrefixCache.swift:600-627)."""
+The file's arrays equal the oracle's quantization of the stored rows (shape
+[1, Hkv, T, ...] per layer, as PrefixCache.swift:600-627 writes them), so a
+row-mode pool writes the reference's on-disk entries.  The file is written
+behind the store (PrefixCache.swift:397-399)."""
 import numpy as np
 import pytest
 
@@ -37,15 +39,22 @@ def test_disk_round_trip_restores_identical_cache(mode, tmp_path):
     tokens = np.arange(1000, 1000 + T)
     pc = PrefixCache(pool, "model-x", cache_dir=tmp_path, disk_budget_gb=1)
     assert pc.store_quantized(tokens, seq)
+    pc.wait_for_disk_writes()
     key = prefix_key("model-x", None, 2, tokens)
     path = tmp_path / f"{key:016x}.q8.safetensors"
     assert path.exists() and pc.disk_count == 1
     file_layers = q8file.load_entry(path)
     assert len(file_layers) == layers
     for layer in range(layers):
-        want = _snap(pool, seq, T, layer)
+        kq, ks, kz, vq, vs, vz = f.expected(layer, 0)
+        want = {"keys": kq, "values": vq, "key_scales": ks, "key_zeros": kz, "value_scales": vs,
+                "value_zeros": vz}
         for field, _ in q8file.NAMES:
-            np.testing.assert_array_equal(file_layers[layer][field], want[field])
+            got = file_layers[layer][field]
+            assert got.shape[0] == 1 and got.shape[1:] == want[field].shape, (layer, field, got.shape)
+            if got.dtype == np.float16:
+                got = got.view(np.uint16)
+            np.testing.assert_array_equal(got[0], want[field])
 
     # memory gone, file kept: a fresh cache object on the same directory
     pool.prefix_clear()
@@ -58,6 +67,12 @@ def test_disk_round_trip_restores_identical_cache(mode, tmp_path):
         a, b = _snap(pool, seq, T, layer), _snap(pool, restored, T, layer)
         for field in a:
             assert np.array_equal(a[field].view(np.uint8), b[field].view(np.uint8)), (layer, field)
+        # and the oracle's bytes
+        kq, _, kz, vq, vs, _ = f.expected(layer, 0)
+        np.testing.assert_array_equal(b["keys"][0], kq)
+        np.testing.assert_array_equal(b["values"][0], vq)
+        np.testing.assert_array_equal(b["key_zeros"][0].view(np.uint16), kz)
+        np.testing.assert_array_equal(b["value_scales"][0].view(np.uint16), vs)
 
     # attention over the original and the restored sequence: identical
     q = to_dev(rand_bits(np.random.default_rng(2), (2, H * 4, 1, D), "bf16"), "bf16")

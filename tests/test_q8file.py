@@ -116,3 +116,36 @@ def test_unreadable_file_is_a_miss(tmp_path):
 def test_budget_from_environment(tmp_path, monkeypatch, env, expect):
     monkeypatch.setenv("KRILL_PREFIX_CACHE_GB", env)
     assert q8file.DiskTier(tmp_path).budget == expect
+
+
+def test_write_behind_runs_in_order_and_loads_wait_for_it(tmp_path, monkeypatch):
+    """Background writes (PrefixCache.swift:397-399): queued in order on one
+    writer; a load of a queued file waits for the queue; clear drains it."""
+    import threading
+
+    layers = _layers(n_layers=2)
+    tier = q8file.DiskTier(tmp_path, disk_budget_gb=1)
+    gate = threading.Event()
+    order = []
+    real = q8file.save_entry
+
+    def slow_save(path, lay, metadata=None):
+        gate.wait(10)  # the first write holds the writer until the test lets it go
+        order.append(path.name)
+        real(path, lay, metadata)
+
+    monkeypatch.setattr(q8file, "save_entry", slow_save)
+    assert tier.write(1, layers, background=True)
+    assert tier.write(2, layers, background=True)
+    assert not tier.path(1).exists()  # still queued behind the gate
+    threading.Timer(0.2, gate.set).start()
+    got = tier.load(2)  # waits for both writes
+    assert got is not None and len(got) == 2
+    assert order == [tier.path(1).name, tier.path(2).name]
+    for f, _ in q8file.NAMES:
+        np.testing.assert_array_equal(got[1][f], layers[1][f])
+    tier.write(3, layers, background=True)
+    tier.clear()  # the queued write lands before the directory is cleared
+    assert tier.count == 0
+    q8file.wait_for_disk_writes()
+    assert q8file._WRITER.errors == 0
