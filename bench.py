@@ -487,6 +487,7 @@ def run_decode(args, w):
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": measured_traffic(args, call),
+        "traffic_source": traffic_source(args, call),
         "bytes_per_launch": int(launch_bytes),
         "avg_launch_ms": round(attn_ms, 5),
     }
@@ -972,6 +973,7 @@ def run_verify(args, w):
         "unit": "TFLOP/s" if compute_bound else "GB/s",
         "frac": mfma["frac"] if compute_bound else hbm["frac"],
         "traffic": measured_traffic(args, "verify_attn") if rollback else None,
+        "traffic_source": traffic_source(args, "verify_attn") if rollback else None,
         "bytes_per_launch": int(kv_launch),
         "avg_launch_ms": round(attn_ms, 5),
         "mfma" if not compute_bound else "hbm": mfma if not compute_bound else hbm,
@@ -989,14 +991,24 @@ def run_verify(args, w):
 def measured_traffic(args, call):
     """HBM bytes per call of the timed entry point from the committed
     rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, calibrated against a plain
-    copy), when it was taken on this workload; None otherwise."""
-    path = os.path.join(ROOT, "profiles", f"{call}_{args.workload}_{args.quant}_traffic.json")
+    copy), when it was taken on this workload; None otherwise.  Not measured
+    in this run: the counters need their own rocprofv3 --pmc runs."""
+    name = f"{call}_{args.workload}_{args.quant}_traffic.json"
     try:
-        with open(path) as f:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
             rec = json.load(f)
     except (OSError, ValueError):
         return None
     return rec.get("traffic_bytes_per_call")
+
+
+def traffic_source(args, call):
+    """Where roofline.traffic comes from (None when there is no figure)."""
+    name = f"{call}_{args.workload}_{args.quant}_traffic.json"
+    if measured_traffic(args, call) is None:
+        return None
+    return (f"profiles/{name}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of this call in their own runs, "
+            "scaled by a plain copy's counters; committed, not measured in this run")
 
 
 def cpu_baseline(args, w, lens0, per_tok):
@@ -1023,16 +1035,25 @@ def cpu_baseline(args, w, lens0, per_tok):
         base.step(q, k, v, O.DT_BF16, 1.0 / math.sqrt(D), out)
         reps += 1
         el = time.perf_counter() - t0
-        if el > 12.0 or reps >= 500:
+        if el > 12.0 or reps >= 100000:
             break
     per_layer_s = el / (reps * sample_layers)
     # the same restatement on one thread: one step of one layer
     base.set_threads(1)
+    one_reps = 0
     t1 = time.perf_counter()
-    base.step(q, k, v, O.DT_BF16, 1.0 / math.sqrt(D), out, layers_to_run=1)
-    one_s = time.perf_counter() - t1
+    while True:
+        base.step(q, k, v, O.DT_BF16, 1.0 / math.sqrt(D), out, layers_to_run=1)
+        one_reps += 1
+        one_el = time.perf_counter() - t1
+        if one_el > 2.0 or one_reps >= 100000:
+            break
+    one_s = one_el / one_reps
     base.close()
     ctx = float(np.sum(lens0)) + 1.5 * B
+    # the restatement stores the reference's row layout: per token and layer
+    # 2 Hkv D payload bytes + one fp16 (scale, zero) pair per head for K and V
+    per_tok = algorithmic_bytes_per_token_layer(Hkv, D, 1)
     gbs = ctx * per_tok / per_layer_s / 1e9
     layers = w["layers"]
     return {
@@ -1043,10 +1064,11 @@ def cpu_baseline(args, w, lens0, per_tok):
         "kind": "port",
         "sample": f"{reps} decode steps x {sample_layers} layers of the same batch ({B} seqs, same lengths) "
                   f"through the CPU restatement of the reference step (row quantize, concat, full fp16 dequant, "
-                  f"fp32 SDPA); {el:.1f} s; tokens/s extrapolated to {layers} layers",
+                  f"fp32 SDPA); {el:.1f} s; GB/s on the row layout's {per_tok} B per token and layer; "
+                  f"tokens/s extrapolated to {layers} layers",
         "single_thread": {"value": round(ctx * per_tok / one_s / 1e9, 3), "unit": "GB/s",
                           "tokens_per_s": round(B / (one_s * layers), 4),
-                          "sample": f"one decode step of one layer on one thread, {one_s:.1f} s"},
+                          "sample": f"{one_reps} decode steps of one layer on one thread, {one_el:.1f} s"},
     }
 
 

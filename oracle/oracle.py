@@ -43,6 +43,13 @@ attention_f64 (a7/a8)       closed forms: one key -> output = that value row;
                             equal keys -> output = mean of values; huge masked
                             tail has no effect; brute force against an
                             independent numpy softmax on tiny shapes.
+attention_mlx_composed      MLX's op-by-op SDPA (the reference's CPU path):
+(a7, second oracle)         closed forms (one key -> the value row exactly,
+                            equal keys -> the mean within fp16 rounding);
+                            within the roundings it adds of attention_f64
+                            (its unrounded-query form within 1e-5).  Its exact
+                            agreement with MLX is parity unpinned (MLX is
+                            not in this tree).
 stack_left_padded (a5)      closed form of BatchedDecode.swift:119-147 on
                             integer rows (tests/test_oracle.py).
 prefix_key (a10)            FNV-1a 64 published test vectors ("" and "a").
@@ -284,6 +291,54 @@ def attention_f64(q: np.ndarray, k: np.ndarray, v: np.ndarray, limits, scale: fl
     lim = np.ascontiguousarray(np.broadcast_to(np.asarray(limits, np.int32), (NR,)), np.int32)
     out = np.empty((NR, D), np.float64)
     lib().oracle_attention_f64(_p(q), _p(k), _p(v), NR, T, D, _p(lim), float(scale), _p(out))
+    return out
+
+
+def attention_mlx_composed(q_bits: np.ndarray, q_dt: int, k_f16: np.ndarray, v_f16: np.ndarray, limits,
+                           scale: float) -> np.ndarray:
+    """MLX's composed SDPA on the dequantized cache, op by op: the arithmetic
+    of the reference's decode SDPA (MLXFast.scaledDotProductAttention,
+    Attention.swift:95-98, Gemma4Model.swift:516-517) where MLX runs it as
+    separate ops (its CPU path): q scaled in its own dtype (the scale a
+    scalar of that dtype), scores = q . K^T, softmax (precise: float32
+    inside), out = P . V.  The dtype of the products is the promotion of
+    the query dtype and fp16 (the dequantized K/V): fp16 for fp16 queries --
+    scores, weights and output each rounded once to fp16 (float32
+    accumulation inside each product) -- and float32 for bf16 queries.
+    q_bits [NR, D] in q_dt; k_f16 / v_f16 [T, D] fp16 bits; row r sees keys
+    [0, limits[r]).  Returns float64 copies of the output values.
+
+    MLX (mlx-swift 0.31.4) is not in this tree: this restates its published
+    op sequence; it is pinned by closed forms (one key, equal keys) and by
+    its distance from attention_f64 (within the roundings it adds: the
+    scaled query in its dtype, and in fp16 the scores, weights and output),
+    not against MLX's own outputs."""
+    qv = bits_to_f32(q_bits, q_dt)
+    if q_dt == DT_BF16:
+        sc = float(bf16_bits_to_f32(f32_to_bf16_bits(np.array([scale], np.float32)))[0])
+        qs = bf16_bits_to_f32(f32_to_bf16_bits(qv * np.float32(sc)))
+    else:
+        sc = float(np.float16(scale))
+        qs = (qv * np.float32(sc)).astype(np.float16).astype(np.float32)
+    k = f16_bits_to_f32(k_f16)
+    v = f16_bits_to_f32(v_f16)
+    half = q_dt == DT_F16
+    NR, D = qs.shape
+    lim = np.broadcast_to(np.asarray(limits, np.int64), (NR,))
+    out = np.empty((NR, D), np.float64)
+    for r in range(NR):
+        T = int(lim[r])
+        s_ = k[:T] @ qs[r]  # float32 accumulation
+        if half:
+            s_ = s_.astype(np.float16).astype(np.float32)
+        e = np.exp(s_ - s_.max())
+        p = (e / e.sum(dtype=np.float32)).astype(np.float32)
+        if half:
+            p = p.astype(np.float16).astype(np.float32)
+        o = p @ v[:T]
+        if half:
+            o = o.astype(np.float16).astype(np.float32)
+        out[r] = o
     return out
 
 

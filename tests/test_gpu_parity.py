@@ -333,3 +333,38 @@ def test_chunked_prefill_512_rows():
     got, ref = _attn_case("affine_g64", 128, 2, 5, [600, 1100], Lq=512, seed=31)
     err = np.abs(got - ref).max()
     assert err <= ATOL, f"max abs error {err:.3e}"
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_decode_attention_against_the_reference_op_by_op_sdpa(dt):
+    """The reference's own cache (row mode) and its SDPA arithmetic: the
+    kernel against MLX's op-by-op SDPA over the dequantized fp16 cache
+    (oracle.attention_mlx_composed: fp16 products for fp16 queries, float32
+    for bf16), Qwen3-14B heads, within 2e-3; prints how far each sits from
+    the float64 result."""
+    print(f"\ncase decode_vs_mlx_composed dt={dt}", flush=True)
+    H, R, D = 8, 5, 128
+    lens = [511, 2049, 64, 3000]
+    rng = np.random.default_rng(77)
+    pool = make_pool(H, D, "ref_row", dt, blocks=sum((T + 63) // 64 for T in lens) + 8)
+    f = Filled(pool, lens, rng, dt, max_chunk=512)
+    tables, tl, _ = f.tables()
+    q = rand_bits(rng, (len(lens), H * R, 1, D), dt)
+    scale = 1.0 / np.sqrt(D)
+    out = pool.attention(0, to_dev(q, dt), tables, tl, max(lens), scale)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    ref64 = oracle_attention(pool, f, 0, q, dt, scale)
+    mlx = np.zeros_like(ref64)
+    for b, T in enumerate(lens):
+        kq, ks, kz, vq, vs, vz = f.expected(0, b)
+        k16, v16 = O.dequant_ref_f16(kq, ks, kz), O.dequant_ref_f16(vq, vs, vz)
+        for hk in range(H):
+            rows = q[b, hk * R:(hk + 1) * R, 0]
+            mlx[b, hk * R:(hk + 1) * R, 0] = O.attention_mlx_composed(rows, DT[dt], k16[hk], v16[hk], [T] * R,
+                                                                      scale)
+    e_kernel, e_mlx, e_between = (np.abs(got - ref64).max(), np.abs(mlx - ref64).max(), np.abs(got - mlx).max())
+    print(f"kernel-f64 {e_kernel:.3e}  mlx_composed-f64 {e_mlx:.3e}  kernel-mlx_composed {e_between:.3e}",
+          flush=True)
+    assert e_kernel <= ATOL and e_between <= ATOL
+    pool.close()

@@ -456,6 +456,53 @@ def test_attention_closed_forms(oracle):
                                atol=1e-12)
 
 
+def test_mlx_composed_attention_closed_forms(oracle):
+    """One key: the output is that value row exactly (p = 1 in any dtype);
+    equal keys: the mean of the values, within the output's rounding."""
+    rng = np.random.default_rng(18)
+    D = 64
+    v16 = oracle.f32_to_f16_bits(rng.standard_normal((6, D)).astype(np.float32))
+    k16 = oracle.f32_to_f16_bits(rng.standard_normal((6, D)).astype(np.float32))
+    vf = oracle.f16_bits_to_f32(v16).astype(np.float64)
+    for dt in (oracle.DT_F16, oracle.DT_BF16):
+        qb = (oracle.f32_to_f16_bits if dt == oracle.DT_F16 else oracle.f32_to_bf16_bits)(
+            rng.standard_normal((3, D)).astype(np.float32))
+        one = oracle.attention_mlx_composed(qb, dt, k16, v16, [1, 1, 1], 0.125)
+        np.testing.assert_array_equal(one, np.tile(vf[0], (3, 1)))
+        same = np.tile(k16[0], (6, 1))
+        mean = oracle.attention_mlx_composed(qb, dt, same, v16, [6, 6, 6], 0.125)
+        tol = 2.0 ** -11 * np.abs(vf).max() * 2 if dt == oracle.DT_F16 else 1e-6
+        np.testing.assert_allclose(mean, np.tile(vf.mean(0), (3, 1)), atol=tol)
+
+
+def test_mlx_composed_attention_against_f64(oracle):
+    """How far the reference's op-by-op SDPA sits from the exact result on
+    N(0,1) data (T 2048, D 128, scale 1/sqrt(D)): with bf16 queries the
+    query scaled and rounded to bf16 dominates (2^-9 relative per element),
+    with fp16 queries the fp16 roundings of scores, weights and output add
+    to it -- measurably off, but within the 2e-3 tolerance.  With the query
+    scaling taken out (scale 1, queries pre-scaled exactly in float32 and
+    exactly representable) the float32 form is within 1e-5."""
+    rng = np.random.default_rng(19)
+    T, D = 2048, 128
+    k16 = oracle.f32_to_f16_bits(rng.standard_normal((T, D)).astype(np.float32))
+    v16 = oracle.f32_to_f16_bits(rng.standard_normal((T, D)).astype(np.float32))
+    qf = rng.standard_normal((8, D)).astype(np.float32)
+    kd, vd = oracle.f16_bits_to_f32(k16), oracle.f16_bits_to_f32(v16)
+    lim = [T, T - 1, 1000, 1, T, T, 64, 65]
+    for dt, lo, hi in ((oracle.DT_BF16, 1e-5, 2e-3), (oracle.DT_F16, 1e-5, 2e-3)):
+        qb = (oracle.f32_to_f16_bits if dt == oracle.DT_F16 else oracle.f32_to_bf16_bits)(qf)
+        got = oracle.attention_mlx_composed(qb, dt, k16, v16, lim, 1 / np.sqrt(D))
+        ref = oracle.attention_f64(oracle.bits_to_f32(qb, dt), kd, vd, lim, 1 / np.sqrt(D))
+        err = np.abs(got - ref).max()
+        assert lo <= err <= hi, (dt, err)
+    # bf16 queries already scaled: scale 1 rounds nothing, the rest is float32
+    qb = oracle.f32_to_bf16_bits(qf * np.float32(1 / np.sqrt(D)))
+    got = oracle.attention_mlx_composed(qb, oracle.DT_BF16, k16, v16, lim, 1.0)
+    ref = oracle.attention_f64(oracle.bits_to_f32(qb, oracle.DT_BF16), kd, vd, lim, 1.0)
+    assert np.abs(got - ref).max() <= 1e-5
+
+
 def test_masked_minus_10000_underflows_to_zero():
     """BatchedDecode.swift:22-28: exp(score - 10000) is 0 in f16, bf16, f32,
     so a length bound equals the reference's additive mask."""
