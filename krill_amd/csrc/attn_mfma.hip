@@ -39,19 +39,6 @@
 
 namespace krill {
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-__device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-// Eight bytes as exact fp16 u - 128.
-__device__ __forceinline__ half8_t bytes8_centred(uint2 w) {
-  const half2_t m1152 = half2_t{(_Float16)-1152.0f, (_Float16)-1152.0f};
-  const half2_t a = bytes01_plus1024(w.x) + m1152, b = bytes23_plus1024(w.x) + m1152;
-  const half2_t c = bytes01_plus1024(w.y) + m1152, d = bytes23_plus1024(w.y) + m1152;
-  return half8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-}
 
 // LDS bytes of one staged block: the head region rounded up to whole 1 KB
 // runs (one 16-byte-per-lane direct load each).

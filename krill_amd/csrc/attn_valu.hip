@@ -1,5 +1,5 @@
-// Paged int8 decode attention on the VALU (no MFMA): the path for up to 8
-// query rows per KV head (GQA group x query length).
+// Paged int8 decode attention, one token per lane for the scores: the path
+// for up to 8 query rows per KV head (GQA group x query length).
 //
 // Computes o = softmax(scale * q K^T) V over each sequence's paged int8
 // cache -- what MLXFast.scaledDotProductAttention computes on the
@@ -28,15 +28,19 @@
 //  * online softmax in the log2 domain with a lazily raised running max: a
 //    block only pays for a wave reduction when some score exceeds the
 //    running max by more than 8 (a wave vote), so weights stay below 2^8;
-//  * weights w = p * s_v (binary32) go to LDS in V storage order; each lane
-//    then owns D/64 V^T rows (d values), loaded as contiguous 16-byte pieces,
-//    turns 4 bytes at a time into exact binary32 values and accumulates
-//    w * u with fp32 FMAs.  The V zero points collapse into one per-(row,
-//    group) term.  (fp16 weights, as an earlier version used, put an error
-//    of up to 2^-11 of a group's value range into the output whenever a few
-//    keys hold the softmax weight.)
-//  * the next block's K and V are loaded as soon as the current block's
-//    registers are consumed, so loads overlap the other phase's math.
+//  * weights w = p * s_v (binary32) go to LDS in V storage order, and P.V
+//    runs on the matrix cores: O^T += V^T . P^T per 16-row d tile with
+//    v_mfma_f32_16x16x32_f16, A = the V bytes as exact fp16 (u - 128; row
+//    mode: dequantized), B = each weight as an fp16 high part plus the fp16
+//    rounding of its remainder (two MFMAs, about 2^-22 relative error left;
+//    one fp16 weight would put up to 2^-11 of a group's value range into the
+//    output whenever a few keys hold the softmax weight).  The V zero points
+//    collapse into one per-(row, group) term.  On the VALU this product was
+//    two thirds of the kernel's instructions, which made the kernel issue-
+//    bound; on the matrix cores it is 32 MFMAs per block.
+//  * the next block's K bytes and metadata are loaded as soon as the
+//    current block's K registers are consumed (in flight through the
+//    softmax and P.V), its V bytes once the V registers are.
 // A sequence that lies inside one wave's range is written directly;
 // otherwise each wave writes its segment's (m, l, o) to the workspace and
 // k_attn_merge_flat combines them in a second launch.  (Merging inside the
@@ -103,11 +107,16 @@ __device__ __forceinline__ void ld_stream_words(__amdgpu_buffer_rsrc_t r, int of
   }
 }
 
-// Waves per SIMD the register budget aims for: 3 (168 VGPRs) where the
-// kernel fits without spilling, else 2.
+// Waves per SIMD the register budget aims for: 3 (168 VGPRs) for D = 64,
+// else 2 (the MFMA accumulators of 16 rows x D take 2 D / 16 VGPRs; with K
+// and V both in registers D = 128 needs about 220).  Measured on the
+// Qwen3-14B B = 32 step (D = 128, 5 rows): 2 waves with K and V in
+// registers 68.4 us per call; 3 waves with K staged in LDS 75.0 us (the
+// compiler orders every LDS access after the outstanding direct-to-LDS
+// loads, which drains the K prefetch); 2 waves with K in LDS 70.0 us.
 template <int D, int NR>
 constexpr int valu_waves_per_simd() {
-  return D <= 64 || (D == 128 && NR <= 5) ? 3 : 2;
+  return D <= 64 ? 3 : 2;
 }
 
 // The step's new K/V rows of sequence b, head hk: lane l loads the raw
@@ -201,7 +210,6 @@ __device__ __forceinline__ void store_newest(const AttnArgs &a, int hk, int phys
 template <int D, int NR, int MODE, int VAR>
 __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_valu(AttnArgs a) {
   constexpr bool ROPE = VAR == 1, WIN = VAR == 2;
-  constexpr bool LOAD_TOGETHER = valu_waves_per_simd<D, NR>() >= 3;  // next block's loads in one pass
   constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
   constexpr int NP = D / 16;   // 16-byte K pieces per token row
   constexpr int PPG = NP / G;  // pieces per scale group
@@ -321,23 +329,27 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     return block_rsrc(head_region(a.lv, phys, hk), ok ? a.lv.head_bytes : 0);
   };
 
-  const int gl = MODE == MODE_AFFINE ? (DPL * lane) / 64 : 0;  // scale group of this lane's V rows
   const int pos = ((lane >> 5) << 5) + vpos(lane & 31);        // this lane's token in V order
   const half2_t m1024 = half2_t{(_Float16)-1024.0f, (_Float16)-1024.0f};
   const half2_t m1152 = half2_t{(_Float16)-1152.0f, (_Float16)-1152.0f};
 
+  // V^T tiles for the matrix-core P.V: tile dt, MFMA row m holds row
+  // d = tile_d(dt, m); lane l loads the 16 storage positions 16 (l >> 4) ..
+  // +15 of that row (group l >> 5, half (l >> 4) & 1): for a fixed tile the
+  // 16 lanes of a quarter read 16 consecutive 16-byte pieces.
+  constexpr int ND = D / 16;
+  auto tile_d = [](int dt, int m) { return DPL * (16 * (dt / DPL) + m) + dt % DPL; };
   uint4 kr[NP];
-  uint4 vr[2][2 * DPL];
+  uint4 vr[ND];
   auto load_k = [&](__amdgpu_buffer_rsrc_t r) {
 #pragma unroll
     for (int p = 0; p < NP; ++p) kr[p] = ld_stream16(r, k_byte(lane, 16 * p));
   };
   auto load_v = [&](__amdgpu_buffer_rsrc_t r) {
+    const int tg = lane >> 5, h = (lane >> 4) & 1, m = lane & 15;
 #pragma unroll
-    for (int tg = 0; tg < 2; ++tg)
-#pragma unroll
-      for (int i = 0; i < 2 * DPL; ++i)
-        vr[tg][i] = ld_stream16(r, v_offset(D) + tg * 32 * D + ((i * 64 + lane) << 4));  // d = DPL*lane + i/2, half i%2
+    for (int dt = 0; dt < ND; ++dt)
+      vr[dt] = ld_stream16(r, v_offset(D) + tg * 32 * D + (((2 * (dt % DPL) + h) * 64 + 16 * (dt / DPL) + m) << 4));
   };
   // this lane's token's (scale, zero) pairs, K and V
   uint32_t km[G], vm[G];
@@ -424,9 +436,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
 #pragma unroll
   for (int p = 0; p < NP; ++p) settle(kr[p]);
 #pragma unroll
-  for (int tg = 0; tg < 2; ++tg)
-#pragma unroll
-    for (int i = 0; i < 2 * DPL; ++i) settle(vr[tg][i]);
+  for (int dt = 0; dt < ND; ++dt) settle(vr[dt]);
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     settle(km[g]);
@@ -458,16 +468,18 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       for (int r = 0; r < NR; ++r) lo[r] = max(wst, len - a.Lq + r / a.R - a.window + 1);
     }
 
-    float m_run[NR], l_part[NR], c_part[NR][G], acc[NR][DPL];
+    // acc[dt]: O^T tile dt, lane l: query row l & 15, d = tile_d(dt, 4 (l >> 4) + j)
+    float m_run[NR], l_part[NR], c_part[NR][G];
+    float4_t acc[ND];
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       m_run[r] = -INFINITY;
       l_part[r] = 0.0f;
 #pragma unroll
       for (int g = 0; g < G; ++g) c_part[r][g] = 0.0f;
-#pragma unroll
-      for (int e2 = 0; e2 < DPL; ++e2) acc[r][e2] = 0.0f;
     }
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) acc[dt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   for (; i < seg_end; ++i) {
     if (i == pq1) __builtin_amdgcn_s_setprio(2);
@@ -542,13 +554,11 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
         }
       }
     }
-    // With two waves per SIMD the next block's K bytes and metadata are
-    // fetched here, as soon as the K registers are consumed (see below).
+    // The K registers are consumed: the next block's K bytes and metadata
+    // are fetched now, in flight through the softmax and P.V.
     uint32_t km_next[G], vm_next[G];
-    if constexpr (!LOAD_TOGETHER) {
-      load_k(nrs);
-      load_meta(nrs, km_next, vm_next);
-    }
+    load_k(nrs);
+    load_meta(nrs, km_next, vm_next);
 
     float s[NR];
 #pragma unroll
@@ -579,6 +589,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       raise = __any(over);
     }
     if (raise) {
+      float aln = 1.0f;  // the factor of this lane's accumulator row
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
         const float mb = wave_allmax(s[r]);
@@ -588,9 +599,10 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
         l_part[r] *= al;
 #pragma unroll
         for (int g = 0; g < G; ++g) c_part[r][g] *= al;
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[r][e] *= al;
+        aln = (lane & 15) == r ? al : aln;
       }
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) acc[dt] *= aln;
     }
     float pr[NR];
 #pragma unroll
@@ -613,7 +625,8 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
           w_lds[(r * G + g) * 64 + pos] = pr[r] * vsf;
-          c_part[r][g] = fmaf(pr[r], vzf, c_part[r][g]);
+          // the zero point and the 128 taken off the V bytes: p (z + 128 s)
+          c_part[r][g] = fmaf(pr[r], fmaf(128.0f, vsf, vzf), c_part[r][g]);
         }
       }
     } else {
@@ -624,92 +637,68 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     }
     __syncthreads();
     if (i == patch_i) {
-      // the newest token's V bytes: position p of group tg, byte p % 16 of the
-      // piece (2 (d % DPL) + p / 16) of every lane's d rows
-      const int tg = patch_t >> 5, p = vpos(patch_t & 31), hi = p >> 4, bp = p & 15;
+      // the newest token's V bytes: storage position p of group tg is byte
+      // p % 16 of every tile register of the lanes of quarter 2 tg + p / 16
+      const int tg = patch_t >> 5, p = vpos(patch_t & 31), bp = p & 15;
       const int sh = 8 * (bp & 3);
       const uint32_t keep = ~(0xffu << sh);
+      const bool mine = (lane >> 4) == 2 * tg + (p >> 4);
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) {
-        const uint32_t nv = (uint32_t)newrow[D + DPL * lane + e] << sh;
-#pragma unroll
-        for (int tgi = 0; tgi < 2; ++tgi)
-#pragma unroll
-          for (int h2 = 0; h2 < 2; ++h2)
-            if (tgi == tg && h2 == hi) {
-              uint4 &x = vr[tgi][2 * e + h2];
-              if ((bp >> 2) == 0) x.x = (x.x & keep) | nv;
-              else if ((bp >> 2) == 1) x.y = (x.y & keep) | nv;
-              else if ((bp >> 2) == 2) x.z = (x.z & keep) | nv;
-              else x.w = (x.w & keep) | nv;
-            }
+      for (int dt = 0; dt < ND; ++dt) {
+        const uint32_t nv = (uint32_t)newrow[D + tile_d(dt, lane & 15)] << sh;
+        uint4 &x = vr[dt];
+        if (mine) {
+          if ((bp >> 2) == 0) x.x = (x.x & keep) | nv;
+          else if ((bp >> 2) == 1) x.y = (x.y & keep) | nv;
+          else if ((bp >> 2) == 2) x.z = (x.z & keep) | nv;
+          else x.w = (x.w & keep) | nv;
+        }
       }
     }
 
-    // ---- P.V: lane owns V^T rows d = DPL*lane .. +DPL.  Steps of 4 tokens
-    // (one V word per row d): affine mode turns the 4 bytes into exact
-    // binary32 values u (v_cvt_f32_ubyte) and accumulates w * u with fp32
-    // FMAs, the bias term sum p * z coming per (row, group) at the end; row
-    // mode dequantizes as the reference does, f16(f16(u * s) + z), and
-    // accumulates p * v.  The 4 weights of one (step, row) are one 16-byte
-    // LDS read, issued two steps ahead of their use.
-    constexpr int NSTEP = 16 * NR;  // (tg, chunk, half, row) steps
-    auto wread = [&](int k) -> float4 {
-      const int r = k % NR, c = k / NR;  // c = 2 * (tg * 4 + chunk) + half: positions 4c .. 4c + 3
-      return *reinterpret_cast<const float4 *>(w_lds + (r * G + gl) * 64 + 4 * c);
-    };
-    float4 wq0 = wread(0), wq1 = wread(1 < NSTEP ? 1 : 0);
+    // ---- P.V on the matrix cores: O^T += V^T . P^T per 16-row d tile, two
+    // 32-position sub-steps per block.  Sub-step sh of lane quarter q covers
+    // positions 16 q + 8 sh .. +7: A = those bytes of the lane's tile row
+    // (affine: exact fp16 u - 128; row mode: dequantized as the reference
+    // does, f16(f16(u * s) + z)), B = the same positions' weights of query
+    // row l & 15 (rows beyond NR repeat the last one; their outputs are never
+    // read), each binary32 weight as an fp16 high part and the fp16 rounding
+    // of its remainder (about 2^-22 relative left), two MFMAs per tile.
+    {
+      const int nb = (lane & 15) < NR ? (lane & 15) : NR - 1, q = lane >> 4;
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      const int tg = c >> 3, ch = (c >> 1) & 3, hf = c & 1;
-      float vf[DPL][4];
+      for (int g = 0; g < G; ++g) {
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) {
-        // conversion of this step waits for the previous step's FMAs
-        if (c > 0) order_after(vr[tg][2 * e + (ch >> 1)], acc[NR - 1][DPL - 1]);
-        const uint4 w = vr[tg][2 * e + (ch >> 1)];
-        const uint32_t wd = (ch & 1) ? (hf ? w.w : w.z) : (hf ? w.y : w.x);
-        if constexpr (MODE == MODE_AFFINE) {
+        for (int sh = 0; sh < 2; ++sh) {
+          const float *wp = w_lds + (nb * G + g) * 64 + 16 * q + 8 * sh;
+          half8_t bh, bl;
+          split_hi_lo(*reinterpret_cast<const float4 *>(wp), *reinterpret_cast<const float4 *>(wp + 4), bh, bl);
+          uint4 sc = {0u, 0u, 0u, 0u}, zc = {0u, 0u, 0u, 0u};
+          if constexpr (MODE == MODE_REF) {
+            sc = *reinterpret_cast<const uint4 *>(sz_lds + 16 * q + 8 * sh);
+            zc = *reinterpret_cast<const uint4 *>(sz_lds + 64 + 16 * q + 8 * sh);
+          }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) vf[e][i] = (float)((wd >> (8 * i)) & 0xffu);
-        } else {
-          const half2_t lo = bytes01_plus1024(wd), hi = bytes23_plus1024(wd);
-          const uint2 sp2 = *reinterpret_cast<const uint2 *>(sz_lds + 4 * c);
-          const uint2 zp2 = *reinterpret_cast<const uint2 *>(sz_lds + 64 + 4 * c);
-          const half2_t v0 = (lo + m1024) * u32_as_h2(sp2.x) + u32_as_h2(zp2.x);
-          const half2_t v1 = (hi + m1024) * u32_as_h2(sp2.y) + u32_as_h2(zp2.y);
-          vf[e][0] = (float)v0.x;
-          vf[e][1] = (float)v0.y;
-          vf[e][2] = (float)v1.x;
-          vf[e][3] = (float)v1.y;
+          for (int t = 0; t < ND / G; ++t) {
+            const int dt = g * (ND / G) + t;
+            const uint4 v = vr[dt];
+            const uint2 w8 = sh ? uint2{v.z, v.w} : uint2{v.x, v.y};
+            half8_t av;
+            if constexpr (MODE == MODE_AFFINE)
+              av = bytes8_centred(w8);
+            else
+              av = bytes8_dequant_ref(w8, sc, zc);
+            acc[dt] = mfma16x16x32(av, bh, acc[dt]);
+            acc[dt] = mfma16x16x32(av, bl, acc[dt]);
+          }
         }
       }
-#pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        const int k = c * NR + r;
-        const float4 wc = wq0;
-        asm volatile("" ::: "memory");
-        wq0 = wq1;
-        if (k + 2 < NSTEP) wq1 = wread(k + 2);
-        const float ww[4] = {wc.x, wc.y, wc.z, wc.w};
-#pragma unroll
-        for (int e = 0; e < DPL; ++e)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[r][e] = __builtin_fmaf(ww[i], vf[e][i], acc[r][e]);
-      }
     }
-    // K and V registers are free.  With three waves per SIMD the next
-    // block's K bytes, V bytes and metadata are fetched together, one pass
-    // over its region (2.9 % faster per call on the Qwen3-14B step than
-    // fetching K and metadata after the scores and V here); with two waves
-    // per SIMD the earlier K fetch hides more latency (the 128k Hkv-4 step
-    // is 2.8 % faster that way).  Unconditional on purpose (after the wave's
-    // last block the resource is empty and the loads return zeros without a
-    // memory access): a conditional load would keep the consumed registers
-    // alive through the loop header.
-    if constexpr (LOAD_TOGETHER) load_k(nrs);
+    // The V registers are free: the next block's V bytes.  Unconditional on
+    // purpose (after the wave's last block the resource is empty and the
+    // loads return zeros without a memory access): a conditional load would
+    // keep the consumed registers alive through the loop header.
     load_v(nrs);
-    if constexpr (LOAD_TOGETHER) load_meta(nrs, km_next, vm_next);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       km[g] = km_next[g];
@@ -722,39 +711,44 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     if (patch_i >= 0) store_newest<D, MODE>(a, hk, __builtin_amdgcn_readlane(tab, patch_i - i0), patch_t, newrow, pkm, pvm);
 
     // ---- end of the segment: the whole sequence in this wave -> output;
-    // otherwise a partial in slot hk * (waves + B) + wave + b
-    float lsum[NR];
+    // otherwise a partial in slot hk * (waves + B) + wave + b.  Lane l holds
+    // query row n = l & 15 (rows n >= NR are padding).
+    const int n = lane & 15, q4 = 4 * (lane >> 4);
+    float lsum_n = 0.0f, m_n = 0.0f, cg[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) cg[g] = 0.0f;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      lsum[r] = uniform_f32(wave_allsum(l_part[r]));
-      float cg = 0.0f;
+      const float ls = uniform_f32(wave_allsum(l_part[r]));
+      lsum_n = n == r ? ls : lsum_n;
+      m_n = n == r ? m_run[r] : m_n;
       if constexpr (MODE == MODE_AFFINE) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           const float c = wave_allsum(c_part[r][g]);
-          cg = g == gl ? c : cg;
+          cg[g] = n == r ? c : cg[g];
         }
       }
-#pragma unroll
-      for (int e2 = 0; e2 < DPL; ++e2) acc[r][e2] += cg;
     }
-    if (!a.partial_only && s >= i0 && e <= iend) {
 #pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        const float inv = lsum[r] > 0.0f ? 1.0f / lsum[r] : 0.0f;
-        const int64_t ob = out_row_base(a, b, hk, r, D);
+    for (int dt = 0; dt < ND; ++dt) acc[dt] += cg[dt / (ND / G)];
+    // The lane's values of tiles DPL k .. DPL k + DPL - 1 form one run of
+    // 4 DPL consecutive d: d = DPL (16 k + q4 + j) + e for j < 4, e < DPL.
+    if (n < NR) {
+      const bool whole = !a.partial_only && s >= i0 && e <= iend;
+      const float mul = !whole ? 1.0f : lsum_n > 0.0f ? 1.0f / lsum_n : 0.0f;
+      const int64_t pi = ((int64_t)hk * (a.waves + a.B) + wv + b) * NR + n;
+      const int64_t ob = whole ? out_row_base(a, b, hk, n, D) : pi * D;
 #pragma unroll
-        for (int e2 = 0; e2 < DPL; ++e2) store_out(a.out, ob + DPL * lane + e2, acc[r][e2] * inv, a.out_dtype);
+      for (int k = 0; k < ND / DPL; ++k) {
+        float run[4 * DPL];
+#pragma unroll
+        for (int j2 = 0; j2 < 4; ++j2)
+#pragma unroll
+          for (int e2 = 0; e2 < DPL; ++e2) run[DPL * j2 + e2] = acc[DPL * k + e2][j2] * mul;
+        store_run<4 * DPL>(whole ? a.out : (void *)a.ws_o, ob + DPL * (16 * k + q4), run, whole ? a.out_dtype : DT_F32);
       }
-    } else {
-      const int64_t slot = (int64_t)hk * (a.waves + a.B) + wv + b;
-#pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        const int64_t pi = slot * NR + r;
-#pragma unroll
-        for (int e2 = 0; e2 < DPL; ++e2) a.ws_o[pi * D + DPL * lane + e2] = acc[r][e2];
-        if (lane == 0) reinterpret_cast<float2 *>(a.ws_ml)[pi] = float2{m_run[r], lsum[r]};
-      }
+      if (!whole && lane < 16) reinterpret_cast<float2 *>(a.ws_ml)[pi] = float2{m_n, lsum_n};
     }
     if (i >= iend_eff) break;
     // next sequence with blocks (empty ones get zeros from the merge)

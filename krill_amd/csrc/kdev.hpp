@@ -111,6 +111,34 @@ __device__ __forceinline__ void store_out(void *out, int64_t idx, float v, int d
     reinterpret_cast<uint16_t *>(out)[idx] = f32_to_bf16_bits(v);
 }
 
+// N consecutive outputs (N a multiple of 4; idx a multiple of N) in 16-byte
+// stores where they fill them.
+template <int N>
+__device__ __forceinline__ void store_run(void *out, int64_t idx, const float (&v)[N], int dt) {
+  static_assert(N % 4 == 0, "runs of 4k values");
+  if (dt == DT_F32) {
+#pragma unroll
+    for (int k = 0; k < N; k += 4)
+      *reinterpret_cast<float4 *>(reinterpret_cast<float *>(out) + idx + k) = float4{v[k], v[k + 1], v[k + 2], v[k + 3]};
+    return;
+  }
+  uint32_t w[N / 2];
+#pragma unroll
+  for (int k = 0; k < N / 2; ++k) {
+    const uint32_t lo = dt == DT_F16 ? f32_to_f16_bits(v[2 * k]) : f32_to_bf16_bits(v[2 * k]);
+    const uint32_t hi = dt == DT_F16 ? f32_to_f16_bits(v[2 * k + 1]) : f32_to_bf16_bits(v[2 * k + 1]);
+    w[k] = lo | (hi << 16);
+  }
+  uint16_t *o = reinterpret_cast<uint16_t *>(out) + idx;
+  if constexpr (N % 8 == 0) {
+#pragma unroll
+    for (int k = 0; k < N / 2; k += 4) *reinterpret_cast<uint4 *>(o + 2 * k) = uint4{w[k], w[k + 1], w[k + 2], w[k + 3]};
+  } else {
+#pragma unroll
+    for (int k = 0; k < N / 2; k += 2) *reinterpret_cast<uint2 *>(o + 2 * k) = uint2{w[k], w[k + 1]};
+  }
+}
+
 // ---------------------------------------------------------- byte unpacking
 
 // Two bytes of `w` as fp16 (1024 + byte): byte values ride in the mantissa of
@@ -128,6 +156,46 @@ __device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {
 
 __device__ __forceinline__ half2_t u32_as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 __device__ __forceinline__ uint32_t h2_as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// LDS address space (destination of the direct-to-LDS buffer loads)
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+// Eight bytes as exact fp16 u - 128.
+__device__ __forceinline__ half8_t bytes8_centred(uint2 w) {
+  const half2_t m1152 = half2_t{(_Float16)-1152.0f, (_Float16)-1152.0f};
+  const half2_t a = bytes01_plus1024(w.x) + m1152, b = bytes23_plus1024(w.x) + m1152;
+  const half2_t c = bytes01_plus1024(w.y) + m1152, d = bytes23_plus1024(w.y) + m1152;
+  return half8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+// Eight bytes dequantized as the reference does, f16(f16(u * s) + z), with
+// the eight positions' fp16 scales `sc` and zero points `zc` (pairs per word).
+__device__ __forceinline__ half8_t bytes8_dequant_ref(uint2 w, uint4 sc, uint4 zc) {
+  const half2_t m1024 = half2_t{(_Float16)-1024.0f, (_Float16)-1024.0f};
+  const half2_t a = (bytes01_plus1024(w.x) + m1024) * u32_as_h2(sc.x) + u32_as_h2(zc.x);
+  const half2_t b = (bytes23_plus1024(w.x) + m1024) * u32_as_h2(sc.y) + u32_as_h2(zc.y);
+  const half2_t c = (bytes01_plus1024(w.y) + m1024) * u32_as_h2(sc.z) + u32_as_h2(zc.z);
+  const half2_t d = (bytes23_plus1024(w.y) + m1024) * u32_as_h2(sc.w) + u32_as_h2(zc.w);
+  return half8_t{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+// Eight binary32 weights as fp16 high parts (round to nearest) and the fp16
+// rounding of their remainders: hi + lo is within about 2^-22 of each weight.
+__device__ __forceinline__ void split_hi_lo(float4 a, float4 b, half8_t &hi, half8_t &lo) {
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  const f2_t f[4] = {f2_t{a.x, a.y}, f2_t{a.z, a.w}, f2_t{b.x, b.y}, f2_t{b.z, b.w}};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const half2_t h = __builtin_convertvector(f[k], half2_t);
+    const f2_t back = __builtin_convertvector(h, f2_t);
+    const half2_t l = __builtin_convertvector(f2_t{f[k].x - back.x, f[k].y - back.y}, half2_t);
+    hi[2 * k] = h[0];
+    hi[2 * k + 1] = h[1];
+    lo[2 * k] = l[0];
+    lo[2 * k + 1] = l[1];
+  }
+}
 
 // ---------------------------------------------------------- wave helpers
 
