@@ -115,8 +115,13 @@ __device__ __forceinline__ void ld_stream_words(__amdgpu_buffer_rsrc_t r, int of
 // compiler orders every LDS access after the outstanding direct-to-LDS
 // loads, which drains the K prefetch); 2 waves with K in LDS 70.0 us.
 template <int D, int NR>
+constexpr bool pv_on_mfma() {
+  return D <= 128 && NR >= 3;
+}
+template <int D, int NR>
 constexpr int valu_waves_per_simd() {
-  return D <= 64 ? 3 : 2;
+  if constexpr (pv_on_mfma<D, NR>()) return D <= 64 ? 3 : 2;
+  return D <= 64 || (D == 128 && NR <= 5) ? 3 : 2;
 }
 
 // The step's new K/V rows of sequence b, head hk: lane l loads the raw
@@ -214,6 +219,11 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   constexpr int NP = D / 16;   // 16-byte K pieces per token row
   constexpr int PPG = NP / G;  // pieces per scale group
   constexpr int DPL = D / 64;  // V^T rows (d values) per lane
+  // P.V on the matrix cores (16 query rows per MFMA tile, so worth it from 3
+  // rows on and while its 2 D / 16 accumulator registers per lane fit) or on
+  // the VALU (lane owns D / 64 rows of V^T, fp32 FMAs)
+  constexpr bool PVM = pv_on_mfma<D, NR>();
+  constexpr bool LOAD_TOGETHER = !PVM && valu_waves_per_simd<D, NR>() >= 3;  // next block's loads in one pass
 
   __shared__ __attribute__((aligned(16))) float w_lds[NR * G * 64];
   __shared__ __attribute__((aligned(16))) uint16_t sz_lds[2 * 64];
@@ -339,17 +349,28 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   // 16 lanes of a quarter read 16 consecutive 16-byte pieces.
   constexpr int ND = D / 16;
   auto tile_d = [](int dt, int m) { return DPL * (16 * (dt / DPL) + m) + dt % DPL; };
+  const int gl = MODE == MODE_AFFINE ? (DPL * lane) / 64 : 0;  // VALU P.V: scale group of this lane's V rows
+  constexpr int NV = PVM ? ND : 4 * DPL;  // 16-byte V pieces per lane
   uint4 kr[NP];
-  uint4 vr[ND];
+  uint4 vr[NV];
   auto load_k = [&](__amdgpu_buffer_rsrc_t r) {
 #pragma unroll
     for (int p = 0; p < NP; ++p) kr[p] = ld_stream16(r, k_byte(lane, 16 * p));
   };
   auto load_v = [&](__amdgpu_buffer_rsrc_t r) {
-    const int tg = lane >> 5, h = (lane >> 4) & 1, m = lane & 15;
+    if constexpr (PVM) {
+      const int tg = lane >> 5, h = (lane >> 4) & 1, m = lane & 15;
 #pragma unroll
-    for (int dt = 0; dt < ND; ++dt)
-      vr[dt] = ld_stream16(r, v_offset(D) + tg * 32 * D + (((2 * (dt % DPL) + h) * 64 + 16 * (dt / DPL) + m) << 4));
+      for (int dt = 0; dt < ND; ++dt)
+        vr[dt] = ld_stream16(r, v_offset(D) + tg * 32 * D + (((2 * (dt % DPL) + h) * 64 + 16 * (dt / DPL) + m) << 4));
+    } else {
+      // vr[tg 2 DPL + i]: d = DPL lane + i / 2, half i % 2 of token group tg
+#pragma unroll
+      for (int tg = 0; tg < 2; ++tg)
+#pragma unroll
+        for (int i2 = 0; i2 < 2 * DPL; ++i2)
+          vr[tg * 2 * DPL + i2] = ld_stream16(r, v_offset(D) + tg * 32 * D + ((i2 * 64 + lane) << 4));
+    }
   };
   // this lane's token's (scale, zero) pairs, K and V
   uint32_t km[G], vm[G];
@@ -436,7 +457,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
 #pragma unroll
   for (int p = 0; p < NP; ++p) settle(kr[p]);
 #pragma unroll
-  for (int dt = 0; dt < ND; ++dt) settle(vr[dt]);
+  for (int k = 0; k < NV; ++k) settle(vr[k]);
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     settle(km[g]);
@@ -470,7 +491,8 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
 
     // acc[dt]: O^T tile dt, lane l: query row l & 15, d = tile_d(dt, 4 (l >> 4) + j)
     float m_run[NR], l_part[NR], c_part[NR][G];
-    float4_t acc[ND];
+    float4_t acc[PVM ? ND : 1];          // matrix-core P.V
+    float accv[PVM ? 1 : NR][DPL];       // VALU P.V: row r, d = DPL lane + e
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       m_run[r] = -INFINITY;
@@ -479,7 +501,11 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       for (int g = 0; g < G; ++g) c_part[r][g] = 0.0f;
     }
 #pragma unroll
-    for (int dt = 0; dt < ND; ++dt) acc[dt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int dt = 0; dt < (PVM ? ND : 1); ++dt) acc[dt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int r = 0; r < (PVM ? 1 : NR); ++r)
+#pragma unroll
+      for (int e2 = 0; e2 < DPL; ++e2) accv[r][e2] = 0.0f;
 
   for (; i < seg_end; ++i) {
     if (i == pq1) __builtin_amdgcn_s_setprio(2);
@@ -557,8 +583,10 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     // The K registers are consumed: the next block's K bytes and metadata
     // are fetched now, in flight through the softmax and P.V.
     uint32_t km_next[G], vm_next[G];
-    load_k(nrs);
-    load_meta(nrs, km_next, vm_next);
+    if constexpr (!LOAD_TOGETHER) {
+      load_k(nrs);
+      load_meta(nrs, km_next, vm_next);
+    }
 
     float s[NR];
 #pragma unroll
@@ -600,9 +628,15 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
 #pragma unroll
         for (int g = 0; g < G; ++g) c_part[r][g] *= al;
         aln = (lane & 15) == r ? al : aln;
-      }
+        if constexpr (!PVM) {
 #pragma unroll
-      for (int dt = 0; dt < ND; ++dt) acc[dt] *= aln;
+          for (int e2 = 0; e2 < DPL; ++e2) accv[r][e2] *= al;
+        }
+      }
+      if constexpr (PVM) {
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt) acc[dt] *= aln;
+      }
     }
     float pr[NR];
 #pragma unroll
@@ -625,8 +659,9 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
           w_lds[(r * G + g) * 64 + pos] = pr[r] * vsf;
-          // the zero point and the 128 taken off the V bytes: p (z + 128 s)
-          c_part[r][g] = fmaf(pr[r], fmaf(128.0f, vsf, vzf), c_part[r][g]);
+          // the zero point, plus on the matrix cores the 128 taken off the V
+          // bytes: p (z + 128 s); the VALU takes the bytes as they are: p z
+          c_part[r][g] = fmaf(pr[r], PVM ? fmaf(128.0f, vsf, vzf) : vzf, c_part[r][g]);
         }
       }
     } else {
@@ -636,6 +671,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       sz_lds[64 + pos] = valid ? (uint16_t)(vm[0] >> 16) : (uint16_t)0;
     }
     __syncthreads();
+    if constexpr (PVM) {
     if (i == patch_i) {
       // the newest token's V bytes: storage position p of group tg is byte
       // p % 16 of every tile register of the lanes of quarter 2 tg + p / 16
@@ -656,6 +692,32 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       }
     }
 
+    } else {
+    if (i == patch_i) {
+      // the newest token's V bytes: position p of group tg, byte p % 16 of the
+      // piece (2 (d % DPL) + p / 16) of every lane's d rows
+      const int tg = patch_t >> 5, p = vpos(patch_t & 31), hi = p >> 4, bp = p & 15;
+      const int sh = 8 * (bp & 3);
+      const uint32_t keep = ~(0xffu << sh);
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        const uint32_t nv = (uint32_t)newrow[D + DPL * lane + e] << sh;
+#pragma unroll
+        for (int tgi = 0; tgi < 2; ++tgi)
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)
+            if (tgi == tg && h2 == hi) {
+              uint4 &x = vr[tgi * 2 * DPL + 2 * e + h2];
+              if ((bp >> 2) == 0) x.x = (x.x & keep) | nv;
+              else if ((bp >> 2) == 1) x.y = (x.y & keep) | nv;
+              else if ((bp >> 2) == 2) x.z = (x.z & keep) | nv;
+              else x.w = (x.w & keep) | nv;
+            }
+      }
+    }
+
+    }
+    if constexpr (PVM) {
     // ---- P.V on the matrix cores: O^T += V^T . P^T per 16-row d tile, two
     // 32-position sub-steps per block.  Sub-step sh of lane quarter q covers
     // positions 16 q + 8 sh .. +7: A = those bytes of the lane's tile row
@@ -694,11 +756,69 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
         }
       }
     }
-    // The V registers are free: the next block's V bytes.  Unconditional on
-    // purpose (after the wave's last block the resource is empty and the
-    // loads return zeros without a memory access): a conditional load would
-    // keep the consumed registers alive through the loop header.
+    } else {
+    // ---- P.V: lane owns V^T rows d = DPL*lane .. +DPL.  Steps of 4 tokens
+    // (one V word per row d): affine mode turns the 4 bytes into exact
+    // binary32 values u (v_cvt_f32_ubyte) and accumulates w * u with fp32
+    // FMAs, the bias term sum p * z coming per (row, group) at the end; row
+    // mode dequantizes as the reference does, f16(f16(u * s) + z), and
+    // accumulates p * v.  The 4 weights of one (step, row) are one 16-byte
+    // LDS read, issued two steps ahead of their use.
+    constexpr int NSTEP = 16 * NR;  // (tg, chunk, half, row) steps
+    auto wread = [&](int k) -> float4 {
+      const int r = k % NR, c = k / NR;  // c = 2 * (tg * 4 + chunk) + half: positions 4c .. 4c + 3
+      return *reinterpret_cast<const float4 *>(w_lds + (r * G + gl) * 64 + 4 * c);
+    };
+    float4 wq0 = wread(0), wq1 = wread(1 < NSTEP ? 1 : 0);
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const int tg = c >> 3, ch = (c >> 1) & 3, hf = c & 1;
+      float vf[DPL][4];
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        // conversion of this step waits for the previous step's FMAs
+        if (c > 0) order_after(vr[tg * 2 * DPL + 2 * e + (ch >> 1)], accv[NR - 1][DPL - 1]);
+        const uint4 w = vr[tg * 2 * DPL + 2 * e + (ch >> 1)];
+        const uint32_t wd = (ch & 1) ? (hf ? w.w : w.z) : (hf ? w.y : w.x);
+        if constexpr (MODE == MODE_AFFINE) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) vf[e][i] = (float)((wd >> (8 * i)) & 0xffu);
+        } else {
+          const half2_t lo = bytes01_plus1024(wd), hi = bytes23_plus1024(wd);
+          const uint2 sp2 = *reinterpret_cast<const uint2 *>(sz_lds + 4 * c);
+          const uint2 zp2 = *reinterpret_cast<const uint2 *>(sz_lds + 64 + 4 * c);
+          const half2_t v0 = (lo + m1024) * u32_as_h2(sp2.x) + u32_as_h2(zp2.x);
+          const half2_t v1 = (hi + m1024) * u32_as_h2(sp2.y) + u32_as_h2(zp2.y);
+          vf[e][0] = (float)v0.x;
+          vf[e][1] = (float)v0.y;
+          vf[e][2] = (float)v1.x;
+          vf[e][3] = (float)v1.y;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const int k = c * NR + r;
+        const float4 wc = wq0;
+        asm volatile("" ::: "memory");
+        wq0 = wq1;
+        if (k + 2 < NSTEP) wq1 = wread(k + 2);
+        const float ww[4] = {wc.x, wc.y, wc.z, wc.w};
+#pragma unroll
+        for (int e = 0; e < DPL; ++e)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) accv[r][e] = __builtin_fmaf(ww[i], vf[e][i], accv[r][e]);
+      }
+    }
+    }
+    // The V registers are free: the next block's V bytes (with three waves
+    // per SIMD on the VALU path, its K bytes and metadata too, one pass over
+    // the region).  Unconditional on purpose (after the wave's last block the
+    // resource is empty and the loads return zeros without a memory access):
+    // a conditional load would keep the consumed registers alive through the
+    // loop header.
+    if constexpr (LOAD_TOGETHER) load_k(nrs);
     load_v(nrs);
+    if constexpr (LOAD_TOGETHER) load_meta(nrs, km_next, vm_next);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       km[g] = km_next[g];
@@ -710,6 +830,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     // the segment's newest token goes to the pool with the segment's output
     if (patch_i >= 0) store_newest<D, MODE>(a, hk, __builtin_amdgcn_readlane(tab, patch_i - i0), patch_t, newrow, pkm, pvm);
 
+    if constexpr (PVM) {
     // ---- end of the segment: the whole sequence in this wave -> output;
     // otherwise a partial in slot hk * (waves + B) + wave + b.  Lane l holds
     // query row n = l & 15 (rows n >= NR are padding).
@@ -749,6 +870,43 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
         store_run<4 * DPL>(whole ? a.out : (void *)a.ws_o, ob + DPL * (16 * k + q4), run, whole ? a.out_dtype : DT_F32);
       }
       if (!whole && lane < 16) reinterpret_cast<float2 *>(a.ws_ml)[pi] = float2{m_n, lsum_n};
+    }
+    } else {
+    // ---- end of the segment: the whole sequence in this wave -> output;
+    // otherwise a partial in slot hk * (waves + B) + wave + b
+    float lsum[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      lsum[r] = uniform_f32(wave_allsum(l_part[r]));
+      float cg = 0.0f;
+      if constexpr (MODE == MODE_AFFINE) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float c = wave_allsum(c_part[r][g]);
+          cg = g == gl ? c : cg;
+        }
+      }
+#pragma unroll
+      for (int e2 = 0; e2 < DPL; ++e2) accv[r][e2] += cg;
+    }
+    if (!a.partial_only && s >= i0 && e <= iend) {
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const float inv = lsum[r] > 0.0f ? 1.0f / lsum[r] : 0.0f;
+        const int64_t ob = out_row_base(a, b, hk, r, D);
+#pragma unroll
+        for (int e2 = 0; e2 < DPL; ++e2) store_out(a.out, ob + DPL * lane + e2, accv[r][e2] * inv, a.out_dtype);
+      }
+    } else {
+      const int64_t slot = (int64_t)hk * (a.waves + a.B) + wv + b;
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const int64_t pi = slot * NR + r;
+#pragma unroll
+        for (int e2 = 0; e2 < DPL; ++e2) a.ws_o[pi * D + DPL * lane + e2] = accv[r][e2];
+        if (lane == 0) reinterpret_cast<float2 *>(a.ws_ml)[pi] = float2{m_run[r], lsum[r]};
+      }
+    }
     }
     if (i >= iend_eff) break;
     // next sequence with blocks (empty ones get zeros from the merge)
