@@ -562,6 +562,8 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
 #pragma unroll
         for (int i = 0; i < 8; ++i) kp[i] = kp[i] + m1152;  // u - 128, exact
       }
+      // the piece is converted: its register takes the next block's piece
+      if constexpr (!LOAD_TOGETHER) kr[p] = ld_stream16(nrs, k_byte(lane, 16 * p));
       const int g = MODE == MODE_AFFINE ? p / PPG : 0;
       // the last piece of a scale group finishes accg[.][g]
       const bool tail = MODE == MODE_AFFINE ? (p + 1) % PPG == 0 : p == NP - 1;
@@ -583,10 +585,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     // The K registers are consumed: the next block's K bytes and metadata
     // are fetched now, in flight through the softmax and P.V.
     uint32_t km_next[G], vm_next[G];
-    if constexpr (!LOAD_TOGETHER) {
-      load_k(nrs);
-      load_meta(nrs, km_next, vm_next);
-    }
+    if constexpr (!LOAD_TOGETHER) load_meta(nrs, km_next, vm_next);
 
     float s[NR];
 #pragma unroll
@@ -754,6 +753,15 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
             acc[dt] = mfma16x16x32(av, bl, acc[dt]);
           }
         }
+        // the group's tiles are consumed: their registers take the next block's
+        {
+          const int tg = lane >> 5, h = (lane >> 4) & 1, m = lane & 15;
+#pragma unroll
+          for (int t = 0; t < ND / G; ++t) {
+            const int dt = g * (ND / G) + t;
+            vr[dt] = ld_stream16(nrs, v_offset(D) + tg * 32 * D + (((2 * (dt % DPL) + h) * 64 + 16 * (dt / DPL) + m) << 4));
+          }
+        }
       }
     }
     } else {
@@ -817,7 +825,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     // a conditional load would keep the consumed registers alive through the
     // loop header.
     if constexpr (LOAD_TOGETHER) load_k(nrs);
-    load_v(nrs);
+    if constexpr (!PVM) load_v(nrs);
     if constexpr (LOAD_TOGETHER) load_meta(nrs, km_next, vm_next);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
