@@ -412,85 +412,68 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
 #pragma unroll
       for (int tg = 0; tg < 2; ++tg) {
         // logical k = 8*q4 + i  <->  token 32*tg + (i < 4 ? 4*q4 + i : 16 + 4*q4 + i - 4)
-        float vss[8][G], vzz[8][G];
+        // the (scale, zero) words of the 8 k positions (zero past the data)
+        uint32_t vmw[8][G];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int tokh = 32 * tg + 16 * h + 4 * q4;  // 4 tokens, G pairs each: 16 G bytes
-          uint32_t vm[4 * G];
 #pragma unroll
           for (int c = 0; c < G; ++c) {
             const uint4 w = *reinterpret_cast<const uint4 *>(st + vm_offset(D, G) + ((tokh * G) << 2) + 16 * c);
-            vm[4 * c] = w.x;
-            vm[4 * c + 1] = w.y;
-            vm[4 * c + 2] = w.z;
-            vm[4 * c + 3] = w.w;
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int k2 = 0; k2 < 4; ++k2) vmw[4 * h + (4 * c + k2) / G][(4 * c + k2) % G] = ww[k2];
           }
           if (edge) {  // metadata past the sequence's end is not data
 #pragma unroll
             for (int e = 0; e < 4; ++e)
               if (tbase + tokh + e >= len || (WIN && tbase + tokh + e < wst))
 #pragma unroll
-                for (int g = 0; g < G; ++g) vm[e * G + g] = 0u;
+                for (int g = 0; g < G; ++g) vmw[4 * h + e][g] = 0u;
           }
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-              vss[4 * h + e][g] = f16_bits_to_f32((uint16_t)(vm[e * G + g] & 0xffffu));
-              vzz[4 * h + e][g] = f16_bits_to_f32((uint16_t)(vm[e * G + g] >> 16));
-            }
         }
         // Each binary32 weight w = p * s_v (affine) or p (row mode) goes in as
         // two fp16 operands, w_hi = f16(w) and w_lo = f16(w - w_hi), against
         // the same exact V operand: one fp16 weight would carry a relative
         // error of 2^-11 into every product, up to 2^-11 of a group's value
         // range in the output when a few keys hold the softmax weight; the
-        // pair leaves about 2^-22.
-        half8_t Bh[NRT][G], Bl[NRT][G];
+        // pair leaves about 2^-22.  One scale group at a time, so only its
+        // operands are live.
 #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            const float p = sc[2 * tg + (k >> 2)][rt][k & 3];
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-              const float w = MODE == MODE_AFFINE ? p * vss[k][g] : p;
-              const _Float16 wh = (_Float16)w;
-              Bh[rt][g][k] = wh;
-              Bl[rt][g][k] = (_Float16)(w - (float)wh);
-              // the zero point and the 128 taken off the V bytes: p (z + 128 s)
-              if constexpr (MODE == MODE_AFFINE)
-                c_part[rt][g] = fmaf(p, fmaf(128.0f, vss[k][g], vzz[k][g]), c_part[rt][g]);
-            }
-          }
-        }
-        half2_t sp[4], zp[4];
-        if constexpr (MODE == MODE_REF) {
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            sp[k] = half2_t{(_Float16)vss[2 * k][0], (_Float16)vss[2 * k + 1][0]};
-            zp[k] = half2_t{(_Float16)vzz[2 * k][0], (_Float16)vzz[2 * k + 1][0]};
-          }
-        }
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          const int d = 16 * dt + n;
-          const uint2 vb = *reinterpret_cast<const uint2 *>(st + v_pos_byte(D, tg, d, 8 * q4));
-          half8_t A;
-          if constexpr (MODE == MODE_REF) {
-            half2_t p0 = (bytes01_plus1024(vb.x) + m1024) * sp[0] + zp[0];
-            half2_t p1 = (bytes23_plus1024(vb.x) + m1024) * sp[1] + zp[1];
-            half2_t p2 = (bytes01_plus1024(vb.y) + m1024) * sp[2] + zp[2];
-            half2_t p3 = (bytes23_plus1024(vb.y) + m1024) * sp[3] + zp[3];
-            A = half8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-          } else {
-            A = bytes8_centred(vb);
-          }
-          const int g = MODE == MODE_AFFINE ? dt / 4 : 0;
+        for (int g = 0; g < G; ++g) {
+          half8_t Bh[NRT], Bl[NRT];
 #pragma unroll
           for (int rt = 0; rt < NRT; ++rt) {
-            oacc[rt][dt] = mfma16x16x32(A, Bh[rt][g], oacc[rt][dt]);
-            oacc[rt][dt] = mfma16x16x32(A, Bl[rt][g], oacc[rt][dt]);
+            float w8[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              const float p = sc[2 * tg + (k >> 2)][rt][k & 3];
+              const float vsf = f16_bits_to_f32((uint16_t)(vmw[k][g] & 0xffffu));
+              w8[k] = MODE == MODE_AFFINE ? p * vsf : p;
+              // the zero point and the 128 taken off the V bytes: p (z + 128 s)
+              if constexpr (MODE == MODE_AFFINE)
+                c_part[rt][g] = fmaf(p, fmaf(128.0f, vsf, f16_bits_to_f32((uint16_t)(vmw[k][g] >> 16))), c_part[rt][g]);
+            }
+            split_hi_lo(float4{w8[0], w8[1], w8[2], w8[3]}, float4{w8[4], w8[5], w8[6], w8[7]}, Bh[rt], Bl[rt]);
+          }
+          uint4 sc4 = {0u, 0u, 0u, 0u}, zc4 = {0u, 0u, 0u, 0u};
+          if constexpr (MODE == MODE_REF) {
+            sc4 = uint4{(vmw[0][0] & 0xffffu) | (vmw[1][0] << 16), (vmw[2][0] & 0xffffu) | (vmw[3][0] << 16),
+                        (vmw[4][0] & 0xffffu) | (vmw[5][0] << 16), (vmw[6][0] & 0xffffu) | (vmw[7][0] << 16)};
+            zc4 = uint4{(vmw[0][0] >> 16) | (vmw[1][0] & 0xffff0000u), (vmw[2][0] >> 16) | (vmw[3][0] & 0xffff0000u),
+                        (vmw[4][0] >> 16) | (vmw[5][0] & 0xffff0000u), (vmw[6][0] >> 16) | (vmw[7][0] & 0xffff0000u)};
+          }
+#pragma unroll
+          for (int t2 = 0; t2 < NDT / G; ++t2) {
+            const int dt = g * (NDT / G) + t2;
+            const int d = 16 * dt + n;
+            const uint2 vb = *reinterpret_cast<const uint2 *>(st + v_pos_byte(D, tg, d, 8 * q4));
+            const half8_t A = MODE == MODE_REF ? bytes8_dequant_ref(vb, sc4, zc4) : bytes8_centred(vb);
+#pragma unroll
+            for (int rt = 0; rt < NRT; ++rt) {
+              oacc[rt][dt] = mfma16x16x32(A, Bh[rt], oacc[rt][dt]);
+              oacc[rt][dt] = mfma16x16x32(A, Bl[rt], oacc[rt][dt]);
+            }
           }
         }
       }
