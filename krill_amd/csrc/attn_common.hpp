@@ -41,7 +41,8 @@ struct AttnArgs {
   float scale_log2;  // softmax scale * log2(e)
   int32_t split_blocks;
   int32_t row_groups, rows_per_group;  // query rows per wave (all NR on the VALU path)
-  int32_t waves;  // waves per (KV head, row group)
+  int32_t group_waves;  // row groups per workgroup (MFMA path; 1 on the VALU path)
+  int32_t waves;  // workgroups per (KV head, row group)
   float *ws_o;
   float *ws_ml;
   void *out;  // [B][Hq][Lq][D]
@@ -87,6 +88,7 @@ inline AttnArgs make_attn_args(const PoolGeometry &g, int32_t layer, const AttnL
   r.split_blocks = p.split_blocks;
   r.row_groups = p.row_groups;
   r.rows_per_group = p.rows_per_group;
+  r.group_waves = p.group_waves;
   r.waves = p.waves;
   const WsLayout w = ws_layout(p.slots, p.rows_per_group, g.D);
   uint8_t *base = static_cast<uint8_t *>(a.ws);
@@ -236,10 +238,14 @@ __device__ __forceinline__ int wave_allsum_int(int v) {
 // Blocks of a sequence of length len that row group rg reads: with several
 // row groups (long query windows) a group stops at the block holding the
 // last key its last row sees (causal window); a single group reads them all.
+// The row groups of one workgroup (group_waves of them, sharing its LDS
+// ring) read the same blocks: those of the workgroup's last row group.
 __device__ __forceinline__ int seq_blocks_rg(const AttnArgs &a, int len, int rg) {
   const int nb = seq_blocks(a, len);
   if (a.row_groups <= 1 || !a.causal) return nb;
-  const int rlast = min(a.NR, (rg + 1) * a.rows_per_group) - 1;
+  const int gw = a.group_waves;
+  const int rg_last = min(a.row_groups, (rg / gw + 1) * gw) - 1;
+  const int rlast = min(a.NR, (rg_last + 1) * a.rows_per_group) - 1;
   const int lim = len - a.Lq + rlast / a.R + 1;
   const int nv = lim > 0 ? (lim + 63) >> 6 : 0;
   return nb < nv ? nb : nv;

@@ -8,16 +8,19 @@
 //
 // Work split as on the decode path: per (KV head, row group of 16 * NRT
 // query rows) the blocks of all sequences are laid end to end and split
-// evenly over the waves of the grid, crossing sequence boundaries; a
-// sequence covered by several waves is combined by k_attn_merge_flat.  With
-// several row groups (long query windows) each group only walks the blocks
-// its rows can see.
+// evenly over the workgroups of the grid, crossing sequence boundaries; a
+// sequence covered by several workgroups is combined by k_attn_merge_flat.
+// A workgroup holds W waves, one row group each, that walk the same blocks
+// (those the workgroup's last row group can see, for a causal window) and
+// share one LDS ring.
 //
 // Memory: every block's head region (K, V and metadata, a whole number of
-// contiguous 1 KB runs in the pool layout) is copied verbatim into an LDS
+// contiguous 1 KB runs in the pool layout) is copied verbatim into the LDS
 // ring with direct-to-LDS buffer loads (16 bytes per lane, no registers
-// involved), the next blocks in flight while the current one is computed;
-// MFMA operands are then read from LDS.
+// involved; with W waves each issues every W-th run), the next blocks in
+// flight while the current one is computed; MFMA operands are then read from
+// LDS.  One workgroup barrier per block (W > 1) publishes the block's runs to
+// every wave and releases the stage the previous block used.
 //
 // Math: transposed scores, so no operand is ever transposed in registers:
 //   S^T[tok][row] = K[tok][d] . Q^T[d][row]      v_mfma_f32_16x16x32_f16
@@ -43,14 +46,18 @@ namespace krill {
 // LDS bytes of one staged block: the head region rounded up to whole 1 KB
 // runs (one 16-byte-per-lane direct load each).
 __host__ __device__ constexpr int mfma_stage_bytes(int D, int G) { return (head_region_bytes(D, G) + 1023) & ~1023; }
-// Ring depth: two stages (measured: a third stage per wave costs a wave per
-// compute unit, which costs more than the deeper prefetch gains).
-__host__ __device__ constexpr int mfma_stages(int D) { return 2; }
+// Ring depth.  One wave per workgroup: two stages (measured: a third stage
+// per wave costs a wave per compute unit, which costs more than the deeper
+// prefetch gains).  W > 1 waves: three stages when 8 / W workgroups (two
+// waves per SIMD) still fit the 160 KB of LDS of a compute unit, else two.
+__host__ __device__ constexpr int mfma_stages(int D, int G, int W) {
+  return W > 1 && 3 * mfma_stage_bytes(D, G) * (8 / W) <= 160 * 1024 ? 3 : 2;
+}
 
 // VAR: 0 plain; 1 RoPE of the queries; 2 sliding window (keys below
 // max(win_start[b], position - window + 1) masked).
-template <int D, int MODE, int NRT, int VAR>
-__global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
+template <int D, int MODE, int NRT, int VAR, int W>
+__global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
   constexpr bool ROPE = VAR == 1, WIN = VAR == 2;
   constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
   constexpr int KS = D / 32;   // 32-d steps of Q.K^T
@@ -58,19 +65,24 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
   constexpr int RR = 16 * NRT; // query rows of this wave
   constexpr int STAGE = mfma_stage_bytes(D, G);
   constexpr int NCH = STAGE / 1024;  // direct loads per block
-  constexpr int NST = mfma_stages(D);
+  constexpr int NST = mfma_stages(D, G, W);
   constexpr int NK = 64 * D / 1024;  // runs holding the K bytes
+  // W > 1: the fewest runs of a stage any wave of the group issues
+  constexpr int NCH_W = NCH / W;
   static_assert((NST - 1) * NCH <= 63, "vmcnt immediate range");
+  static_assert(W == 1 || W == 2 || W == 4, "waves per workgroup");
   __shared__ __attribute__((aligned(1024))) uint8_t ring[NST * STAGE];
 
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wid = W > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;
   const int n = lane & 15, q4 = lane >> 4;
+  const int RGB = (a.row_groups + W - 1) / W;  // workgroups per KV head and block range
+  const int wv = blockIdx.x, hk = blockIdx.y / RGB, rg = (blockIdx.y % RGB) * W + wid;
   const int RG = a.row_groups;
-  const int wv = blockIdx.x, hk = blockIdx.y / RG, rg = blockIdx.y % RG;
-  const int rbase = rg * RR;
+  const int rbase = rg * RR;  // rg >= RG (a group's spare wave): no valid row
 
-  // ---- this wave's flat blocks [i0, iend) of the (head, row group) order
-  const int W = a.waves;
+  // ---- this workgroup's flat blocks [i0, iend) of the (head, row group) order
+  const int NWG = a.waves;
   int c0 = 0, lenv = lane < a.B ? seq_len_view<WIN>(a, lane) : 0;
   int nbv = seq_blocks_rg(a, lenv, rg);
   int incl = wave_incl_scan(nbv);
@@ -79,7 +91,7 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
     const int bb = cc + lane;
     T += __builtin_amdgcn_readfirstlane(wave_allsum_int(bb < a.B ? seq_blocks_rg(a, seq_len_view<WIN>(a, bb), rg) : 0));
   }
-  const int Wt = min(W, T);  // every participating wave holds >= 1 block
+  const int Wt = min(NWG, T);  // every participating workgroup holds >= 1 block
   if (wv >= Wt) return;
   const int i0 = (int)(((int64_t)wv * T + Wt - 1) / Wt);
   const int iend = (int)(((int64_t)(wv + 1) * T + Wt - 1) / Wt);
@@ -123,17 +135,27 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
     if (ss < iend) iend_eff = ss;
   }
   // Copies 1 KB runs [C0, C1) of flat block i into stage `buf` (after the
-  // wave's last block the resource is empty: the loads return zeros without
+  // group's last block the resource is empty: the loads return zeros without
   // a memory access).  Runs [0, NK) are the K bytes, the rest V and metadata.
+  // With W waves, wave wid copies runs C0 + wid, C0 + wid + W, ...
   auto issue = [&](int i, int buf, auto c0_, auto c1_) {
     constexpr int C0 = decltype(c0_)::value, C1 = decltype(c1_)::value;
     const bool ok = i < iend_eff;
     const int phys = __builtin_amdgcn_readlane(tab, ok ? i - i0 : 0);
     const __amdgpu_buffer_rsrc_t r = block_rsrc(head_region(a.lv, phys, hk), ok ? a.lv.head_bytes : 0);
     uint8_t *dst = ring + buf * STAGE;
+    if constexpr (W == 1) {
 #pragma unroll
-    for (int c = C0; c < C1; ++c)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(dst + c * 1024), 16, c * 1024 + lane * 16, 0, 0, 2);
+      for (int c = C0; c < C1; ++c)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(dst + c * 1024), 16, c * 1024 + lane * 16, 0, 0, 2);
+    } else {
+#pragma unroll
+      for (int c0 = C0; c0 < C1; c0 += W) {
+        const int c = c0 + wid;
+        if (c0 + W <= C1 || c < C1)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(dst + c * 1024), 16, c * 1024 + lane * 16, 0, 0, 2);
+      }
+    }
   };
   using KRuns0 = std::integral_constant<int, 0>;
   using KRuns1 = std::integral_constant<int, NK>;
@@ -219,11 +241,12 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
     }
   };
 
-  // queries first, then the first NST blocks: waits on the queries do not
-  // cover the block copies
+  // queries first, then the first blocks (NST of them; W > 1: NST - 1, the
+  // next one goes out once every wave is past the first barrier): waits on
+  // the queries do not cover the block copies
   load_q(b);
 #pragma unroll
-  for (int k = 0; k < NST; ++k) issue(i0 + k, k, KRuns0{}, AllRuns{});
+  for (int k = 0; k < (W == 1 ? NST : NST - 1); ++k) issue(i0 + k, k, KRuns0{}, AllRuns{});
   finish_q();
 
   const half2_t m1024 = half2_t{(_Float16)-1024.0f, (_Float16)-1024.0f};
@@ -264,10 +287,20 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
 
     for (; i < seg_end; ++i) {
       const int buf = (i - i0) % NST;
-      // stage `buf` holds block i once every load but the (NST - 1) * NCH
-      // youngest (the other stages' copies, issued in the same K-then-rest
-      // order) has completed
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NST - 1) * NCH) : "memory");
+      if constexpr (W == 1) {
+        // stage `buf` holds block i once every load but the (NST - 1) * NCH
+        // youngest (the other stages' copies, issued in the same K-then-rest
+        // order) has completed
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NST - 1) * NCH) : "memory");
+      } else {
+        // this wave's runs of block i have landed once at most the runs of
+        // the NST - 2 later blocks in flight remain (at least NCH_W each);
+        // its reads of block i - 1 have returned; the barrier then holds
+        // every wave's runs of block i and frees the stage of block i - 1
+        // for block i + NST - 1
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"((NST - 2) * NCH_W) : "memory");
+        issue(i + NST - 1, (i + NST - 1 - i0) % NST, KRuns0{}, AllRuns{});
+      }
       const uint8_t *st = ring + buf * STAGE;
       const int tbase = (i - s) << 6;
       // some row of this group does not see every token of the block (causal
@@ -349,8 +382,10 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
         }
       }
       // the K bytes of this stage are consumed: refill them NST blocks ahead
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      issue(i + NST, buf, KRuns0{}, KRuns1{});
+      if constexpr (W == 1) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        issue(i + NST, buf, KRuns0{}, KRuns1{});
+      }
       if (edge) {
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt)
@@ -478,8 +513,10 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
         }
       }
       // every LDS read of this stage has returned: refill the rest
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      issue(i + NST, buf, KRuns1{}, AllRuns{});
+      if constexpr (W == 1) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        issue(i + NST, buf, KRuns1{}, AllRuns{});
+      }
     }
 
     // ---- end of the segment: lane holds O^T[d = 16*dt + 4*q4 + e][row n].
@@ -542,82 +579,86 @@ __global__ __launch_bounds__(64) void k_attn_mfma(AttnArgs a) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+template <int D, int MODE, int W>
+static hipError_t launch_mfma_w(const AttnArgs &args, dim3 grid, hipStream_t st) {
+  const dim3 block(64 * W);
+  if (args.rope_cs)
+    k_attn_mfma<D, MODE, 1, 1, W><<<grid, block, 0, st>>>(args);
+  else if (args.window > 0)
+    k_attn_mfma<D, MODE, 1, 2, W><<<grid, block, 0, st>>>(args);
+  else
+    k_attn_mfma<D, MODE, 1, 0, W><<<grid, block, 0, st>>>(args);
+  return hipGetLastError();
+}
+
 template <int D, int MODE>
-static hipError_t launch_mfma_nrt(const AttnArgs &args, int NRT, dim3 grid, hipStream_t st) {
-  switch (NRT) {
-    case 1:
-      if (args.rope_cs)
-        k_attn_mfma<D, MODE, 1, 1><<<grid, dim3(64), 0, st>>>(args);
-      else if (args.window > 0)
-        k_attn_mfma<D, MODE, 1, 2><<<grid, dim3(64), 0, st>>>(args);
-      else
-        k_attn_mfma<D, MODE, 1, 0><<<grid, dim3(64), 0, st>>>(args);
-      break;
-    case 2:
-      if (args.rope_cs)
-        k_attn_mfma<D, MODE, 2, 1><<<grid, dim3(64), 0, st>>>(args);
-      else if (args.window > 0)
-        k_attn_mfma<D, MODE, 2, 2><<<grid, dim3(64), 0, st>>>(args);
-      else
-        k_attn_mfma<D, MODE, 2, 0><<<grid, dim3(64), 0, st>>>(args);
-      break;
+static hipError_t launch_mfma_dm(const AttnArgs &args, int W, dim3 grid, hipStream_t st) {
+  switch (W) {
+    case 1: return launch_mfma_w<D, MODE, 1>(args, grid, st);
+    case 2: return launch_mfma_w<D, MODE, 2>(args, grid, st);
+    case 4: return launch_mfma_w<D, MODE, 4>(args, grid, st);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 hipError_t launch_attn_mfma(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
                             hipStream_t st) {
-  // one VGPR of block-table entries per wave
+  // one VGPR of block-table entries per workgroup
   if (p.waves < 1 || (int64_t)p.waves * 64 < (int64_t)a.B * p.nb_cap) return hipErrorInvalidValue;
-  if (p.nrt < 1 || p.nrt > 2 || (g.D >= 256 && p.nrt != 1) || p.rows_per_group != 16 * p.nrt ||
-      p.row_groups * p.rows_per_group < p.NR)
+  if (p.nrt != 1 || p.rows_per_group != 16 || p.row_groups * p.rows_per_group < p.NR ||
+      (p.group_waves != 1 && p.group_waves != 2 && p.group_waves != 4))
     return hipErrorInvalidValue;
   const AttnArgs args = make_attn_args(g, layer, a, p);
-  const dim3 grid((unsigned)p.waves, (unsigned)(g.Hkv * p.row_groups));
+  const int groups = (p.row_groups + p.group_waves - 1) / p.group_waves;
+  const dim3 grid((unsigned)p.waves, (unsigned)(g.Hkv * groups));
   switch (g.D) {
     case 64:
-      return g.mode == MODE_REF ? launch_mfma_nrt<64, MODE_REF>(args, p.nrt, grid, st)
-                                : launch_mfma_nrt<64, MODE_AFFINE>(args, p.nrt, grid, st);
+      return g.mode == MODE_REF ? launch_mfma_dm<64, MODE_REF>(args, p.group_waves, grid, st)
+                                : launch_mfma_dm<64, MODE_AFFINE>(args, p.group_waves, grid, st);
     case 128:
-      return g.mode == MODE_REF ? launch_mfma_nrt<128, MODE_REF>(args, p.nrt, grid, st)
-                                : launch_mfma_nrt<128, MODE_AFFINE>(args, p.nrt, grid, st);
+      return g.mode == MODE_REF ? launch_mfma_dm<128, MODE_REF>(args, p.group_waves, grid, st)
+                                : launch_mfma_dm<128, MODE_AFFINE>(args, p.group_waves, grid, st);
     case 256:
-      return g.mode == MODE_REF ? launch_mfma_nrt<256, MODE_REF>(args, p.nrt, grid, st)
-                                : launch_mfma_nrt<256, MODE_AFFINE>(args, p.nrt, grid, st);
+      return g.mode == MODE_REF ? launch_mfma_dm<256, MODE_REF>(args, p.group_waves, grid, st)
+                                : launch_mfma_dm<256, MODE_AFFINE>(args, p.group_waves, grid, st);
     default:
       return hipErrorInvalidValue;
   }
 }
 
-template <int D, int MODE>
-static int32_t occupancy_mfma(int nrt) {
+template <int D, int MODE, int W>
+static int32_t occupancy_mfma() {
   int n = 0;
-  hipError_t e = nrt == 2 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                                &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, 2, 0>), 64, 0)
-                          : hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                                &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, 1, 0>), 64, 0);
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+      &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, 1, 0, W>), 64 * W, 0);
   if (e != hipSuccess || n <= 0) {
     (void)hipGetLastError();
-    n = (160 * 1024) / (mfma_stages(D) * mfma_stage_bytes(D, MODE == MODE_AFFINE ? D / 64 : 1));
+    constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
+    n = (160 * 1024) / (mfma_stages(D, G, W) * mfma_stage_bytes(D, G));
   }
   return n;
 }
 
-int32_t mfma_waves_per_cu(const PoolGeometry &g, int32_t nrt) {
+template <int D, int MODE>
+static int32_t occupancy_mfma_w(int W) {
+  return W == 1 ? occupancy_mfma<D, MODE, 1>() : W == 2 ? occupancy_mfma<D, MODE, 2>() : occupancy_mfma<D, MODE, 4>();
+}
+
+int32_t mfma_groups_per_cu(const PoolGeometry &g, int32_t nrt, int32_t group_waves) {
   const int dsel = g.D == 64 ? 0 : g.D == 128 ? 1 : 2;
-  if (nrt < 1 || nrt > 2) return 4;
-  if (g.num_cus <= 0) {  // host-only pool: the LDS bound (the ring per wave, 160 KB per CU)
-    static const int est[3] = {5, 3, 2};
-    return est[dsel];
+  const int wsel = group_waves == 4 ? 2 : group_waves == 2 ? 1 : 0;
+  if (g.num_cus <= 0) {  // host-only pool: the LDS bound (the ring per workgroup, 160 KB per CU)
+    static const int est[3][3] = {{5, 5, 3}, {3, 3, 2}, {1, 1, 1}};
+    return est[dsel][wsel];
   }
-  static int cache[2][3][3] = {};  // [mode][D][nrt], filled on first use per process
-  int &c = cache[g.mode == MODE_AFFINE][dsel][nrt];
+  static int cache[2][3][3] = {};  // [mode][D][W], filled on first use per process
+  int &c = cache[g.mode == MODE_AFFINE][dsel][wsel];
   if (c == 0) {
-    int v = 4;
-    if (g.D == 64) v = g.mode == MODE_REF ? occupancy_mfma<64, MODE_REF>(nrt) : occupancy_mfma<64, MODE_AFFINE>(nrt);
-    else if (g.D == 128) v = g.mode == MODE_REF ? occupancy_mfma<128, MODE_REF>(nrt) : occupancy_mfma<128, MODE_AFFINE>(nrt);
-    else v = g.mode == MODE_REF ? occupancy_mfma<256, MODE_REF>(nrt) : occupancy_mfma<256, MODE_AFFINE>(nrt);
+    const int W = 1 << wsel;
+    int v;
+    if (g.D == 64) v = g.mode == MODE_REF ? occupancy_mfma_w<64, MODE_REF>(W) : occupancy_mfma_w<64, MODE_AFFINE>(W);
+    else if (g.D == 128) v = g.mode == MODE_REF ? occupancy_mfma_w<128, MODE_REF>(W) : occupancy_mfma_w<128, MODE_AFFINE>(W);
+    else v = g.mode == MODE_REF ? occupancy_mfma_w<256, MODE_REF>(W) : occupancy_mfma_w<256, MODE_AFFINE>(W);
     c = v;
   }
   return c;

@@ -1040,30 +1040,36 @@ int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq,
   const int64_t tmax = (int64_t)B * nb_max;
   const int64_t cus = g.num_cus > 0 ? g.num_cus : 256;
   if (p.use_mfma) {
-    // MFMA: at most 32 query rows per wave (16 for D = 256) keeps the score,
-    // output and operand tiles in registers; more rows form row groups.
-    const int32_t max_tiles = g.D >= 256 ? 1 : 2;
-    p.nrt = std::min(max_tiles, (p.NR + 15) / 16);
-    p.rows_per_group = 16 * p.nrt;
-    p.row_groups = (p.NR + p.rows_per_group - 1) / p.rows_per_group;
+    // MFMA: 16 query rows per wave (a row group); the row groups of a KV head
+    // go to workgroups of up to 4 waves that share one LDS ring, so a block
+    // is fetched once per 4 row groups and the smaller register file of a
+    // 16-row wave leaves room for two waves per SIMD.
+    p.nrt = 1;
+    p.rows_per_group = 16;
+    p.row_groups = (p.NR + 15) / 16;
+    p.group_waves = p.row_groups >= 3 ? 4 : p.row_groups;
   } else {
     p.nrt = 0;
     p.rows_per_group = p.NR;
     p.row_groups = 1;
+    p.group_waves = 1;
   }
   // Both kernels: per (KV head, row group) the blocks of all sequences in
-  // flat order, split evenly over a grid of waves.  Automatic: the GPU's
-  // resident wave capacity for the kernel instantiation (every SIMD gets the
-  // same load, one round); with split_blocks set: enough waves for that many
-  // blocks each when every sequence is max_seq_len long.  Never more than 64
-  // blocks per wave (one VGPR of block-table entries).
+  // flat order, split evenly over a grid of workgroups (one wave each on the
+  // VALU path).  Automatic: the GPU's resident capacity for the kernel
+  // instantiation (every SIMD gets the same load, one round); with
+  // split_blocks set: enough workgroups for that many blocks each when every
+  // sequence is max_seq_len long.  Never more than 64 blocks per workgroup
+  // (one VGPR of block-table entries).
   int64_t waves;
   if (split_blocks > 0) {
     const int64_t pw = std::min(split_blocks, 64);
     waves = (tmax + pw - 1) / pw;
+  } else if (p.use_mfma) {
+    const int64_t groups = (p.row_groups + p.group_waves - 1) / p.group_waves;
+    waves = std::max<int64_t>(1, cus * mfma_groups_per_cu(g, p.nrt, p.group_waves) / ((int64_t)g.Hkv * groups));
   } else {
-    const int64_t per_cu = p.use_mfma ? mfma_waves_per_cu(g, p.nrt) : valu_waves_per_cu(g, p.NR);
-    waves = std::max<int64_t>(1, cus * per_cu / ((int64_t)g.Hkv * p.row_groups));
+    waves = std::max<int64_t>(1, cus * valu_waves_per_cu(g, p.NR) / g.Hkv);
   }
   waves = std::max<int64_t>(waves, (tmax + 63) / 64);
   p.split_blocks = split_blocks > 0 ? std::min(split_blocks, 64) : 0;

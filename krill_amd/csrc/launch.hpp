@@ -55,12 +55,13 @@ struct AttnPlan {
   int32_t NR;             // query rows per KV head = (Hq/Hkv) * Lq
   int32_t use_mfma;       // 1 when the MFMA kernel runs
   int32_t split_blocks;   // option value: blocks per wave (<= 64), 0 automatic
-  int32_t waves;          // waves per (KV head, row group)
+  int32_t waves;          // workgroups per (KV head, row group): the flat block split
   int32_t nb_cap;         // blocks per sequence covered (from max_seq_len)
   int64_t slots;          // partial results the workspace holds
   int32_t row_groups;     // row groups per KV head (1 on the VALU path)
   int32_t rows_per_group; // query rows per wave: NR (VALU), 16 * nrt (MFMA)
   int32_t nrt;            // MFMA: 16-row tiles per wave (register budget bound)
+  int32_t group_waves;    // MFMA: waves per workgroup, one row group each, sharing one LDS ring (1 on the VALU path)
   size_t ws_bytes;
 };
 
@@ -104,9 +105,10 @@ hipError_t launch_attention_shared_prefix(const PoolGeometry &g, int32_t layer, 
 // mode), from the runtime's occupancy query on a device pool, else the
 // register-budget design point.
 int32_t valu_waves_per_cu(const PoolGeometry &g, int32_t NR);
-// Resident waves per compute unit of the MFMA kernel for (D, nrt, mode)
-// (bound by its LDS ring), from the occupancy query on a device pool.
-int32_t mfma_waves_per_cu(const PoolGeometry &g, int32_t nrt);
+// Resident workgroups per compute unit of the MFMA kernel for (D, nrt,
+// group_waves, mode) (bound by its LDS ring or its registers), from the
+// occupancy query on a device pool.
+int32_t mfma_groups_per_cu(const PoolGeometry &g, int32_t nrt, int32_t group_waves);
 
 // Per-configuration kernels, defined in the attention translation units.
 hipError_t launch_attn_valu(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
