@@ -83,6 +83,9 @@ def parse():
                     help="shared-prefix workload: one decode attention over the whole tables instead of the "
                          "prefix/suffix cascade")
     ap.add_argument("--kernel-reps", type=int, default=5, help="repetitions of the attention-only timing loop")
+    ap.add_argument("--graph", type=int, default=1,
+                    help="decode workloads: 1 = replay each step's table upload and per-layer calls from a HIP "
+                         "graph (captured once per pinned table buffer); 0 = issue them from Python every step")
     ap.add_argument("--cpu-baseline", type=int, default=1, help="1: time the CPU baseline sample on rank 0")
     ap.add_argument("--seed", type=int, default=20261203)
     ap.add_argument("--copy-calibration", type=int, default=0,
@@ -315,9 +318,44 @@ class StepTables:
         else:
             self.d_tables.copy_(pt, non_blocking=True)
             self.d_lens.copy_(pl, non_blocking=True)
+        self.mark(j)
+
+    def mark(self, j):
+        """Event after the work that reads ring buffer j (its next host() waits on it)."""
         ev = self.env.torch.cuda.Event()
         ev.record(self.env.stream)
         self.events[j] = ev
+
+
+class StepGraphs:
+    """A decode step replayed from HIP graphs: per pinned ring buffer j, the
+    copy of its tables (and slots) to the device and every layer's calls,
+    captured once on a side stream (default priority).  The calls are made
+    with max_seq_len = the run's final longest sequence, an upper bound for
+    every step (the kernels read the true lengths from the device), so one
+    capture serves all steps."""
+
+    def __init__(self, env, st, layers, step_layer, max_len_final, slots):
+        t = env.torch
+        self.graphs = []
+        cap = t.cuda.Stream()
+        scap = ctypes.c_void_p(cap.cuda_stream)
+        t.cuda.synchronize()
+        for j in range(3):
+            ps, pt, pl = st.ring[j][0], st.ring[j][1], st.ring[j][2]
+            g = t.cuda.CUDAGraph()
+            with t.cuda.graph(g, stream=cap):
+                if slots:
+                    st.d_slots.copy_(ps, non_blocking=True)
+                st.d_tables.copy_(pt, non_blocking=True)
+                st.d_lens.copy_(pl, non_blocking=True)
+                for layer in range(layers):
+                    step_layer(layer, max_len_final, scap)
+            self.graphs.append(g)
+        t.cuda.synchronize()
+
+    def replay(self, j):
+        self.graphs[j].replay()
 
 
 def _decode_calls(env, seqs, st, max_len_final, Hq):
@@ -336,27 +374,27 @@ def _decode_calls(env, seqs, st, max_len_final, Hq):
     scale = ctypes.c_float(1.0 / math.sqrt(D))
     keep = (q_all, k_new, v_new, out, ws)
 
-    def append(layer):
-        KL.check(lib.krill_quantize_append(h, layer, kp[layer], vp[layer], st.d_slots.data_ptr(), B, 1, sp))
+    def append(layer, s):
+        KL.check(lib.krill_quantize_append(h, layer, kp[layer], vp[layer], st.d_slots.data_ptr(), B, 1, s))
 
-    def attend(layer, mx):
+    def attend(layer, mx, s=sp):
         KL.check(lib.krill_decode_attention(h, layer, qp[layer], st.d_tables.data_ptr(), st.d_lens.data_ptr(), B,
                                             st.mb, mx, Hq, scale, out.data_ptr(), KL.DTYPE_BF16, ws.data_ptr(),
-                                            ws_bytes, sp))
+                                            ws_bytes, s))
 
-    def fused(layer, mx):
+    def fused(layer, mx, s=sp):
         # the token at position len - 1 (its slot reserved by the step) is written, then attended over
         KL.check(lib.krill_decode_append_attention(h, layer, qp[layer], kp[layer], vp[layer], Hkv * D, D,
                                                    st.d_tables.data_ptr(), st.d_lens.data_ptr(), B, st.mb, mx, Hq,
                                                    scale, out.data_ptr(), KL.DTYPE_BF16, ws.data_ptr(), ws_bytes,
-                                                   sp))
+                                                   s))
 
-    def step_layer(layer, mx):
+    def step_layer(layer, mx, s=sp):
         if args.unfused:
-            append(layer)
-            attend(layer, mx)
+            append(layer, s)
+            attend(layer, mx, s)
         else:
-            fused(layer, mx)
+            fused(layer, mx, s)
 
     def call_only(layer, mx):  # the dominant call alone; the fused one rewrites the same token
         if args.unfused:
@@ -414,7 +452,7 @@ def run_decode(args, w):
     layers, Hq, Hkv, D, B = w["layers"], w["Hq"], w["Hkv"], w["D"], w["B"]
     rng = np.random.default_rng(args.seed)
     lens0 = rng.integers(w["lo"], w["hi"] + 1, size=B).astype(np.int64)
-    total_steps = args.warmup + args.steps + 1
+    total_steps = args.warmup + args.steps + 1 + (3 if args.graph else 0)
     blocks_needed = int(sum((int(T) + total_steps + 63) // 64 for T in lens0))
     num_blocks = blocks_needed + max(16, blocks_needed // 8)
     max_len_final = int(lens0.max()) + total_steps
@@ -428,6 +466,7 @@ def run_decode(args, w):
     seqs_np = np.array(seqs, np.int32)
     one = np.empty(1, np.int32)
     cur_len = [int(x) for x in lens0]
+    graphs = None
 
     def step(i):
         j, ps, pt, pl = st.host(i)
@@ -436,6 +475,10 @@ def run_decode(args, w):
             ps[b, 0] = one[0]
             cur_len[b] += 1
         env.KL.check(env.lib.krill_batch_tables(env.h, env.i32p(seqs_np), B, max_blocks, env.i32p(pt), env.i32p(pl)))
+        if graphs is not None:
+            graphs.replay(j)
+            st.mark(j)
+            return
         st.upload(j, slots=args.unfused)
         mx = max(cur_len)
         for layer in range(layers):
@@ -443,6 +486,10 @@ def run_decode(args, w):
 
     for i in range(args.warmup):
         step(i)
+    if args.graph:
+        graphs = StepGraphs(env, st, layers, step_layer, max_len_final, args.unfused)
+        for i in range(3):  # one replay of each graph before the timed steps
+            step(args.warmup + i)
     lens_start = None
     # timed steps (lengths at their start recorded for the byte count)
     env.torch.cuda.synchronize()
@@ -473,7 +520,8 @@ def run_decode(args, w):
                     "bf16 N(0,1) inputs"
                     + (f" ({w['outlier_frac']:.0%} of channels x20)" if w.get("outlier_frac") else "")
                     + "; step = per layer quantize-append 1 token/seq + paged decode attention"
-                    + (" (two calls)" if args.unfused else " (one fused call)"),
+                    + (" (two calls)" if args.unfused else " (one fused call)")
+                    + ("; each step's table upload and calls replayed from a HIP graph" if args.graph else ""),
         "layers": layers, "Hq": Hq, "Hkv": Hkv, "head_dim": D, "batch": B, "quant": args.quant,
         "context_mean": float(np.mean(lens0)), "num_blocks": num_blocks,
     }
