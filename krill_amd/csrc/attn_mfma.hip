@@ -56,7 +56,12 @@ __host__ __device__ constexpr int mfma_stages(int D, int G, int W) {
 
 // VAR: 0 plain; 1 RoPE of the queries; 2 sliding window (keys below
 // max(win_start[b], position - window + 1) masked).
-template <int D, int MODE, int NRT, int VAR, int W>
+// TS: 1 -- the W waves of a workgroup hold W row groups and every wave
+// works on all 64 tokens of a block; 2 (W = 2) -- both waves hold the same
+// row group and split each block's tokens (wave w: tokens 32 w .. 32 w + 31,
+// its own softmax state), so no byte is converted twice; at each segment
+// end the two states are combined through the ring stage just consumed.
+template <int D, int MODE, int NRT, int VAR, int W, int TS>
 __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
   constexpr bool ROPE = VAR == 1, WIN = VAR == 2;
   constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
@@ -71,13 +76,20 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
   constexpr int NCH_W = NCH / W;
   static_assert((NST - 1) * NCH <= 63, "vmcnt immediate range");
   static_assert(W == 1 || W == 2 || W == 4, "waves per workgroup");
+  static_assert(TS == 1 || (TS == 2 && W == 2), "token split: two waves");
+  constexpr int WR = TS > 1 ? 1 : W;   // row groups per workgroup
+  constexpr int NTT = 4 / TS;          // 16-token score tiles per wave and block
+  constexpr int NTG = 2 / TS;          // 32-token P.V groups per wave and block
+  static_assert(TS == 1 || NRT * NDT * 64 * 16 + NRT * 64 * 8 <= STAGE, "combine buffer fits a stage");
   __shared__ __attribute__((aligned(1024))) uint8_t ring[NST * STAGE];
 
   const int lane = threadIdx.x & 63;
   const int wid = W > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;
   const int n = lane & 15, q4 = lane >> 4;
-  const int RGB = (a.row_groups + W - 1) / W;  // workgroups per KV head and block range
-  const int wv = blockIdx.x, hk = blockIdx.y / RGB, rg = (blockIdx.y % RGB) * W + wid;
+  const int RGB = (a.row_groups + WR - 1) / WR;  // workgroups per KV head and block range
+  const int wv = blockIdx.x, hk = blockIdx.y / RGB, rg = (blockIdx.y % RGB) * WR + (TS > 1 ? 0 : wid);
+  const int tt0 = TS > 1 ? wid * NTT : 0;  // first score tile / P.V group of this wave
+  const int tg0 = TS > 1 ? wid * NTG : 0;
   const int RG = a.row_groups;
   const int rbase = rg * RR;  // rg >= RG (a group's spare wave): no valid row
 
@@ -311,9 +323,10 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
       // ---- S^T = K . Q^T, four 16-token tiles.  Affine mode feeds the bytes
       // as exact fp16 u - 128 and folds the offset into the zero point:
       // q.k = s * (q.(u - 128)) + (z + 128 s) * sum q (per 64-d group).
-      float sc[4][NRT][4];
+      float sc[NTT][NRT][4];  // local tile t = score tile tt0 + t
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
+      for (int t = 0; t < NTT; ++t) {
+        const int tt = tt0 + t;
         const int tokA = 16 * tt + n;  // A-operand row
         half2_t ks2 = half2_t{(_Float16)0.0f, (_Float16)0.0f}, kz2 = ks2;
         if constexpr (MODE == MODE_REF) {
@@ -371,14 +384,14 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
               float sv = 0.0f;
 #pragma unroll
               for (int g = 0; g < G; ++g) sv = fmaf(kss[g], sacc[rt][g][e], fmaf(kzz[g], qsum[rt][g], sv));
-              sc[tt][rt][e] = sv * a.scale_log2;
+              sc[t][rt][e] = sv * a.scale_log2;
             }
           }
         } else {
 #pragma unroll
           for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sc[tt][rt][e] = sacc[rt][0][e] * a.scale_log2;
+            for (int e = 0; e < 4; ++e) sc[t][rt][e] = sacc[rt][0][e] * a.scale_log2;
         }
       }
       // the K bytes of this stage are consumed: refill them NST blocks ahead
@@ -388,13 +401,14 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
       }
       if (edge) {
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
+        for (int t = 0; t < NTT; ++t)
 #pragma unroll
           for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (tbase + 16 * tt + 4 * q4 + e >= lim[rt] || (WIN && tbase + 16 * tt + 4 * q4 + e < lo[rt]))
-                sc[tt][rt][e] = -INFINITY;
+            for (int e = 0; e < 4; ++e) {
+              const int tok = tbase + 16 * (tt0 + t) + 4 * q4 + e;
+              if (tok >= lim[rt] || (WIN && tok < lo[rt])) sc[t][rt][e] = -INFINITY;
+            }
       }
 
       // ---- online softmax with a lazily raised running max (row n of each
@@ -407,8 +421,8 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
       for (int rt = 0; rt < NRT; ++rt) {
         float v = -INFINITY;
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-          v = fmaxf(v, fmaxf(fmaxf(sc[tt][rt][0], sc[tt][rt][1]), fmaxf(sc[tt][rt][2], sc[tt][rt][3])));
+        for (int t = 0; t < NTT; ++t)
+          v = fmaxf(v, fmaxf(fmaxf(sc[t][rt][0], sc[t][rt][1]), fmaxf(sc[t][rt][2], sc[t][rt][3])));
         v = fmaxf(v, shfl_xor(v, 16));
         v = fmaxf(v, shfl_xor(v, 32));
         mb[rt] = v;
@@ -432,11 +446,11 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
         const float mu = m_run[rt] == -INFINITY ? 0.0f : m_run[rt];
         float ps = 0.0f;
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
+        for (int t = 0; t < NTT; ++t)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            sc[tt][rt][e] = fast_exp2(sc[tt][rt][e] - mu);
-            ps += sc[tt][rt][e];
+            sc[t][rt][e] = fast_exp2(sc[t][rt][e] - mu);
+            ps += sc[t][rt][e];
           }
         l_part[rt] += ps;
       }
@@ -445,7 +459,8 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
       // (below 2^8 * s_v) as fp16 high and low parts, V bytes as exact fp16
       // u - 128, the zero points (and 128 s_v) summed on the side
 #pragma unroll
-      for (int tg = 0; tg < 2; ++tg) {
+      for (int tgi = 0; tgi < NTG; ++tgi) {
+        const int tg = tg0 + tgi;
         // logical k = 8*q4 + i  <->  token 32*tg + (i < 4 ? 4*q4 + i : 16 + 4*q4 + i - 4)
         // the (scale, zero) words of the 8 k positions (zero past the data)
         uint32_t vmw[8][G];
@@ -482,7 +497,7 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
             float w8[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-              const float p = sc[2 * tg + (k >> 2)][rt][k & 3];
+              const float p = sc[2 * tgi + (k >> 2)][rt][k & 3];  // score tile 2 tg + k / 4
               const float vsf = f16_bits_to_f32((uint16_t)(vmw[k][g] & 0xffffu));
               w8[k] = MODE == MODE_AFFINE ? p * vsf : p;
               // the zero point and the 128 taken off the V bytes: p (z + 128 s)
@@ -519,9 +534,62 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
       }
     }
 
+    if constexpr (TS > 1) {
+      // ---- token split: wave 1's state of this segment (its half of every
+      // block's tokens) joins wave 0's through the ring stage of the block
+      // just consumed (no load targets it before the next block's barrier):
+      // O = a0 O0 + a1 O1, l = a0 l0 + a1 l1, a_w = 2^(m_w - max(m0, m1)).
+      // Each wave first folds its zero-point sums into O.
+      float *xo = reinterpret_cast<float *>(ring + ((i - 1 - i0) % NST) * STAGE);
+      float lw[NRT];
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt) {
+        float l = l_part[rt];
+        l += shfl_xor(l, 16);
+        l += shfl_xor(l, 32);
+        lw[rt] = l;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float c = c_part[rt][g];
+          c += shfl_xor(c, 16);
+          c += shfl_xor(c, 32);
+          c_part[rt][g] = 0.0f;
+#pragma unroll
+          for (int t2 = 0; t2 < NDT / G; ++t2) oacc[rt][g * (NDT / G) + t2] += c;
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // both waves are done with the stage
+      if (wid == 1) {
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) *reinterpret_cast<float4_t *>(xo + ((rt * NDT + dt) * 64 + lane) * 4) = oacc[rt][dt];
+          *reinterpret_cast<float2 *>(xo + NRT * NDT * 256 + (rt * 64 + lane) * 2) = float2{m_run[rt], lw[rt]};
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (wid == 0) {
+#pragma unroll
+        for (int rt = 0; rt < NRT; ++rt) {
+          const float2 ml1 = *reinterpret_cast<const float2 *>(xo + NRT * NDT * 256 + (rt * 64 + lane) * 2);
+          const float M = fmaxf(m_run[rt], ml1.x);
+          const float a0 = m_run[rt] == -INFINITY ? 0.0f : fast_exp2(m_run[rt] - M);
+          const float a1 = ml1.x == -INFINITY ? 0.0f : fast_exp2(ml1.x - M);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            const float4_t o1 = *reinterpret_cast<const float4_t *>(xo + ((rt * NDT + dt) * 64 + lane) * 4);
+            oacc[rt][dt] = oacc[rt][dt] * a0 + o1 * a1;
+          }
+          m_run[rt] = M;
+          l_part[rt] = q4 == 0 ? a0 * lw[rt] + a1 * ml1.y : 0.0f;  // the epilogue sums the four quarter lanes
+        }
+      }
+    }
+
     // ---- end of the segment: lane holds O^T[d = 16*dt + 4*q4 + e][row n].
     // The whole sequence in this wave -> output; otherwise a partial in slot
-    // (hk * row_groups + rg) * (waves + B) + wave + b.
+    // (hk * row_groups + rg) * (waves + B) + wave + b.  Token split: wave 0
+    // writes the combined state.
     const bool whole = !a.partial_only && s >= i0 && e <= iend;
     const int64_t slot = ((int64_t)hk * RG + rg) * (a.waves + a.B) + wv + b;
 #pragma unroll
@@ -537,7 +605,7 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
         c += shfl_xor(c, 32);
         cg[g] = c;
       }
-      if (!rvalid[rt]) continue;
+      if (!rvalid[rt] || (TS > 1 && wid != 0)) continue;
       const int r = rbase + 16 * rt + n;
       if (whole) {
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
@@ -579,24 +647,34 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template <int D, int MODE, int W>
+template <int D, int MODE, int NRT, int W, int TS>
 static hipError_t launch_mfma_w(const AttnArgs &args, dim3 grid, hipStream_t st) {
   const dim3 block(64 * W);
   if (args.rope_cs)
-    k_attn_mfma<D, MODE, 1, 1, W><<<grid, block, 0, st>>>(args);
+    k_attn_mfma<D, MODE, NRT, 1, W, TS><<<grid, block, 0, st>>>(args);
   else if (args.window > 0)
-    k_attn_mfma<D, MODE, 1, 2, W><<<grid, block, 0, st>>>(args);
+    k_attn_mfma<D, MODE, NRT, 2, W, TS><<<grid, block, 0, st>>>(args);
   else
-    k_attn_mfma<D, MODE, 1, 0, W><<<grid, block, 0, st>>>(args);
+    k_attn_mfma<D, MODE, NRT, 0, W, TS><<<grid, block, 0, st>>>(args);
   return hipGetLastError();
 }
 
+// (nrt, group_waves, token_split) shapes the plan may choose: 16-row waves
+// in workgroups of 1, 2 or 4 row groups, or (D <= 128) a 32-row group split
+// over two waves by tokens.
 template <int D, int MODE>
-static hipError_t launch_mfma_dm(const AttnArgs &args, int W, dim3 grid, hipStream_t st) {
-  switch (W) {
-    case 1: return launch_mfma_w<D, MODE, 1>(args, grid, st);
-    case 2: return launch_mfma_w<D, MODE, 2>(args, grid, st);
-    case 4: return launch_mfma_w<D, MODE, 4>(args, grid, st);
+static hipError_t launch_mfma_dm(const AttnArgs &args, const AttnPlan &p, dim3 grid, hipStream_t st) {
+  if (p.token_split == 2) {
+    if constexpr (D <= 128) {
+      if (p.nrt == 2 && p.group_waves == 1) return launch_mfma_w<D, MODE, 2, 2, 2>(args, grid, st);
+    }
+    return hipErrorInvalidValue;
+  }
+  if (p.token_split != 1 || p.nrt != 1) return hipErrorInvalidValue;
+  switch (p.group_waves) {
+    case 1: return launch_mfma_w<D, MODE, 1, 1, 1>(args, grid, st);
+    case 2: return launch_mfma_w<D, MODE, 1, 2, 1>(args, grid, st);
+    case 4: return launch_mfma_w<D, MODE, 1, 4, 1>(args, grid, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -605,32 +683,30 @@ hipError_t launch_attn_mfma(const PoolGeometry &g, int32_t layer, const AttnLaun
                             hipStream_t st) {
   // one VGPR of block-table entries per workgroup
   if (p.waves < 1 || (int64_t)p.waves * 64 < (int64_t)a.B * p.nb_cap) return hipErrorInvalidValue;
-  if (p.nrt != 1 || p.rows_per_group != 16 || p.row_groups * p.rows_per_group < p.NR ||
-      (p.group_waves != 1 && p.group_waves != 2 && p.group_waves != 4))
-    return hipErrorInvalidValue;
+  if (p.rows_per_group != 16 * p.nrt || p.row_groups * p.rows_per_group < p.NR) return hipErrorInvalidValue;
   const AttnArgs args = make_attn_args(g, layer, a, p);
   const int groups = (p.row_groups + p.group_waves - 1) / p.group_waves;
   const dim3 grid((unsigned)p.waves, (unsigned)(g.Hkv * groups));
   switch (g.D) {
     case 64:
-      return g.mode == MODE_REF ? launch_mfma_dm<64, MODE_REF>(args, p.group_waves, grid, st)
-                                : launch_mfma_dm<64, MODE_AFFINE>(args, p.group_waves, grid, st);
+      return g.mode == MODE_REF ? launch_mfma_dm<64, MODE_REF>(args, p, grid, st)
+                                : launch_mfma_dm<64, MODE_AFFINE>(args, p, grid, st);
     case 128:
-      return g.mode == MODE_REF ? launch_mfma_dm<128, MODE_REF>(args, p.group_waves, grid, st)
-                                : launch_mfma_dm<128, MODE_AFFINE>(args, p.group_waves, grid, st);
+      return g.mode == MODE_REF ? launch_mfma_dm<128, MODE_REF>(args, p, grid, st)
+                                : launch_mfma_dm<128, MODE_AFFINE>(args, p, grid, st);
     case 256:
-      return g.mode == MODE_REF ? launch_mfma_dm<256, MODE_REF>(args, p.group_waves, grid, st)
-                                : launch_mfma_dm<256, MODE_AFFINE>(args, p.group_waves, grid, st);
+      return g.mode == MODE_REF ? launch_mfma_dm<256, MODE_REF>(args, p, grid, st)
+                                : launch_mfma_dm<256, MODE_AFFINE>(args, p, grid, st);
     default:
       return hipErrorInvalidValue;
   }
 }
 
-template <int D, int MODE, int W>
+template <int D, int MODE, int NRT, int W, int TS>
 static int32_t occupancy_mfma() {
   int n = 0;
   const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-      &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, 1, 0, W>), 64 * W, 0);
+      &n, reinterpret_cast<const void *>(&k_attn_mfma<D, MODE, NRT, 0, W, TS>), 64 * W, 0);
   if (e != hipSuccess || n <= 0) {
     (void)hipGetLastError();
     constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
@@ -640,25 +716,31 @@ static int32_t occupancy_mfma() {
 }
 
 template <int D, int MODE>
-static int32_t occupancy_mfma_w(int W) {
-  return W == 1 ? occupancy_mfma<D, MODE, 1>() : W == 2 ? occupancy_mfma<D, MODE, 2>() : occupancy_mfma<D, MODE, 4>();
+static int32_t occupancy_mfma_sel(int sel) {
+  switch (sel) {
+    case 0: return occupancy_mfma<D, MODE, 1, 1, 1>();
+    case 1: return occupancy_mfma<D, MODE, 1, 2, 1>();
+    case 2: return occupancy_mfma<D, MODE, 1, 4, 1>();
+    default:
+      if constexpr (D <= 128) return occupancy_mfma<D, MODE, 2, 2, 2>();
+      return 1;
+  }
 }
 
-int32_t mfma_groups_per_cu(const PoolGeometry &g, int32_t nrt, int32_t group_waves) {
+int32_t mfma_groups_per_cu(const PoolGeometry &g, int32_t nrt, int32_t group_waves, int32_t token_split) {
   const int dsel = g.D == 64 ? 0 : g.D == 128 ? 1 : 2;
-  const int wsel = group_waves == 4 ? 2 : group_waves == 2 ? 1 : 0;
+  const int sel = token_split == 2 ? 3 : group_waves == 4 ? 2 : group_waves == 2 ? 1 : 0;
   if (g.num_cus <= 0) {  // host-only pool: the LDS bound (the ring per workgroup, 160 KB per CU)
-    static const int est[3][3] = {{5, 5, 3}, {3, 3, 2}, {1, 1, 1}};
-    return est[dsel][wsel];
+    static const int est[3][4] = {{5, 5, 3, 8}, {3, 3, 2, 4}, {1, 1, 1, 1}};
+    return est[dsel][sel];
   }
-  static int cache[2][3][3] = {};  // [mode][D][W], filled on first use per process
-  int &c = cache[g.mode == MODE_AFFINE][dsel][wsel];
+  static int cache[2][3][4] = {};  // [mode][D][shape], filled on first use per process
+  int &c = cache[g.mode == MODE_AFFINE][dsel][sel];
   if (c == 0) {
-    const int W = 1 << wsel;
     int v;
-    if (g.D == 64) v = g.mode == MODE_REF ? occupancy_mfma_w<64, MODE_REF>(W) : occupancy_mfma_w<64, MODE_AFFINE>(W);
-    else if (g.D == 128) v = g.mode == MODE_REF ? occupancy_mfma_w<128, MODE_REF>(W) : occupancy_mfma_w<128, MODE_AFFINE>(W);
-    else v = g.mode == MODE_REF ? occupancy_mfma_w<256, MODE_REF>(W) : occupancy_mfma_w<256, MODE_AFFINE>(W);
+    if (g.D == 64) v = g.mode == MODE_REF ? occupancy_mfma_sel<64, MODE_REF>(sel) : occupancy_mfma_sel<64, MODE_AFFINE>(sel);
+    else if (g.D == 128) v = g.mode == MODE_REF ? occupancy_mfma_sel<128, MODE_REF>(sel) : occupancy_mfma_sel<128, MODE_AFFINE>(sel);
+    else v = g.mode == MODE_REF ? occupancy_mfma_sel<256, MODE_REF>(sel) : occupancy_mfma_sel<256, MODE_AFFINE>(sel);
     c = v;
   }
   return c;

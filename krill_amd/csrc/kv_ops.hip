@@ -1044,15 +1044,28 @@ int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq,
     // go to workgroups of up to 4 waves that share one LDS ring, so a block
     // is fetched once per 4 row groups and the smaller register file of a
     // 16-row wave leaves room for two waves per SIMD.
-    p.nrt = 1;
-    p.rows_per_group = 16;
-    p.row_groups = (p.NR + 15) / 16;
-    p.group_waves = p.row_groups >= 3 ? 4 : p.row_groups;
+    // 17-32 rows (speculative verify) at D <= 128: one 32-row group per
+    // workgroup whose two waves split each block's tokens instead, so no
+    // byte is converted twice.
+    p.token_split = 1;
+    if (p.NR > 16 && p.NR <= 32 && g.D <= 128) {
+      p.nrt = 2;
+      p.rows_per_group = 32;
+      p.row_groups = 1;
+      p.group_waves = 1;
+      p.token_split = 2;
+    } else {
+      p.nrt = 1;
+      p.rows_per_group = 16;
+      p.row_groups = (p.NR + 15) / 16;
+      p.group_waves = p.row_groups >= 3 ? 4 : p.row_groups;
+    }
   } else {
     p.nrt = 0;
     p.rows_per_group = p.NR;
     p.row_groups = 1;
     p.group_waves = 1;
+    p.token_split = 1;
   }
   // Both kernels: per (KV head, row group) the blocks of all sequences in
   // flat order, split evenly over a grid of workgroups (one wave each on the
@@ -1067,7 +1080,8 @@ int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq,
     waves = (tmax + pw - 1) / pw;
   } else if (p.use_mfma) {
     const int64_t groups = (p.row_groups + p.group_waves - 1) / p.group_waves;
-    waves = std::max<int64_t>(1, cus * mfma_groups_per_cu(g, p.nrt, p.group_waves) / ((int64_t)g.Hkv * groups));
+    waves = std::max<int64_t>(1, cus * mfma_groups_per_cu(g, p.nrt, p.group_waves, p.token_split) /
+                                     ((int64_t)g.Hkv * groups));
   } else {
     waves = std::max<int64_t>(1, cus * valu_waves_per_cu(g, p.NR) / g.Hkv);
   }

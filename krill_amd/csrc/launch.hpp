@@ -61,7 +61,8 @@ struct AttnPlan {
   int32_t row_groups;     // row groups per KV head (1 on the VALU path)
   int32_t rows_per_group; // query rows per wave: NR (VALU), 16 * nrt (MFMA)
   int32_t nrt;            // MFMA: 16-row tiles per wave (register budget bound)
-  int32_t group_waves;    // MFMA: waves per workgroup, one row group each, sharing one LDS ring (1 on the VALU path)
+  int32_t group_waves;    // MFMA: row groups per workgroup, one wave each, sharing one LDS ring (1 on the VALU path)
+  int32_t token_split;    // MFMA: 2 = one row group per workgroup, its two waves split each block's tokens; else 1
   size_t ws_bytes;
 };
 
@@ -106,9 +107,9 @@ hipError_t launch_attention_shared_prefix(const PoolGeometry &g, int32_t layer, 
 // register-budget design point.
 int32_t valu_waves_per_cu(const PoolGeometry &g, int32_t NR);
 // Resident workgroups per compute unit of the MFMA kernel for (D, nrt,
-// group_waves, mode) (bound by its LDS ring or its registers), from the
+// group_waves, token_split, mode) (bound by its LDS ring or its registers), from the
 // occupancy query on a device pool.
-int32_t mfma_groups_per_cu(const PoolGeometry &g, int32_t nrt, int32_t group_waves);
+int32_t mfma_groups_per_cu(const PoolGeometry &g, int32_t nrt, int32_t group_waves, int32_t token_split);
 
 // Per-configuration kernels, defined in the attention translation units.
 hipError_t launch_attn_valu(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
