@@ -90,19 +90,18 @@ __global__ __launch_bounds__(256) void k_quantize_append(LayerView lv, const uin
   store_row<D, MODE>(head_region(lv, blk, h), kv, t, lane, qb, scale, zero);
 }
 
-// Token owning byte `o` of a head region (pool layout in kdev.hpp).
-template <int D, int G>
-__device__ __forceinline__ int region_byte_token(int o) {
-  if (o < 64 * D) return (o >> 4) & 63;  // K: ((d/16)*64 + t)*16 + d%16
-  if (o < 128 * D) {                     // V: tg*32*D + ((2*(d%DPL) + p/16)*64 + d/DPL)*16 + p%16
-    const int ov = o - 64 * D;
-    const int tg = ov / (32 * D);
-    const int piece = (ov % (32 * D)) >> 4;
-    const int p = ((piece >> 6) & 1) * 16 + (o & 15);
-    return 32 * tg + vtok(p);
-  }
-  if (o < 128 * D + 256 * G) return ((o - 128 * D) >> 2) / G;  // K (scale, zero): (t*G + g)*4
-  return ((o - 128 * D - 256 * G) >> 2) / G;                    // V (scale, zero)
+// Which of the 16 bytes of V piece `o` (byte offset inside the V region of
+// a block) belong to tokens in the 64-bit token set `tm`: the piece holds
+// positions p = 16 h .. 16 h + 15 of one d in token group tg, and position
+// p = 16 h + x is token 32 tg + 8 h + 4 (x / 8) + x % 4 + 16 ((x / 4) % 2)
+// (vtok, pool layout in kdev.hpp), so bytes 0-3, 4-7, 8-11 and 12-15 are
+// tokens 32 tg + 8 h + {0..3, 16..19, 4..7, 20..23}.
+template <int D>
+__device__ __forceinline__ unsigned v_piece_mask(int o, uint64_t tm) {
+  const int tg = o / (32 * D);
+  const int h = ((o % (32 * D)) >> 10) & 1;  // (piece index / 64) % 2
+  const uint64_t s = tm >> (32 * tg + 8 * h);
+  return (unsigned)((s & 0xfu) | (((s >> 16) & 0xfu) << 4) | (((s >> 4) & 0xfu) << 8) | (((s >> 20) & 0xfu) << 12));
 }
 
 // Bulk append (prefill, chunked appends): one workgroup (256 threads) per
@@ -273,17 +272,14 @@ __global__ __launch_bounds__(256) void k_quantize_append_blocks(LayerView lv, co
 #pragma unroll 1
   for (int ib = 0; ib < (blkB >= 0 ? 2 : 1); ++ib) {
     const int tlo = ib == 0 ? tA : 0, thi = ib == 0 ? tA + nA : nrows - nA;
+    // tokens [tlo, thi) as a bit set (thi <= 64)
+    const uint64_t tm = (thi >= 64 ? ~0ull : ((1ull << thi) - 1ull)) & ~((1ull << tlo) - 1ull);
     uint8_t *reg = head_region(lv, ib == 0 ? blkA : blkB, h) + v_offset(D);
     const uint8_t *im = img[ib];
 #pragma unroll 1
     for (int q = tid; q < VB / 16; q += 256) {
       const int o = q * 16;
-      unsigned mask = 0;
-#pragma unroll
-      for (int x = 0; x < 16; ++x) {
-        const int tk = region_byte_token<D, G>(v_offset(D) + o + x);
-        mask |= (unsigned)(tk >= tlo && tk < thi) << x;
-      }
+      const unsigned mask = v_piece_mask<D>(o, tm);
       if (mask == 0xffffu) {
         *reinterpret_cast<uint4 *>(reg + o) = *reinterpret_cast<const uint4 *>(im + o);
       } else if (mask) {
