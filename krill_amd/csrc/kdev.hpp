@@ -368,6 +368,34 @@ __device__ __forceinline__ uint8_t affine_q(float w, float s, float bias) {
   return (uint8_t)(uint32_t)n;
 }
 
+// The two quantizers' per-element division q = x / s done as x * r, with r
+// = v_rcp_f32(s) (within one ulp of 1/s), wherever that provably gives the
+// same byte: |fl(x r) - fl(x / s)| <= (2^-23 + 2^-24 + 2^-24) |x / s| =
+// 2^-22 |x / s| < 2^-13 for |x / s| < 512 (the quotients here stay within
+// about [-1, 256]), so when x r lies more than 2^-12 from every rounding
+// boundary of the step that follows (k + 1/2 for rint, k for truncation)
+// both round to the same integer; otherwise the exact division decides.
+// (About 2^-11 of uniformly spread quotients take the division.)
+__device__ __forceinline__ uint8_t affine_q_r(float w, float s, float bias, float r) {
+  const float a = w - bias;
+  const float y = a * r;
+  float n = rintf(y);
+  // y - n is exact (|y - n| <= 1/2 and n = rint(y))
+  if (!(fabsf(y) < 512.0f && fabsf(y - n) < 0.5f - 0x1p-12f)) n = rintf(a / s);
+  if (n > 255.0f) n = 255.0f;
+  if (n < 0.0f) n = 0.0f;
+  return (uint8_t)(uint32_t)n;
+}
+template <int DT>
+__device__ __forceinline__ uint8_t ref_q_r(float x, float mn, float safe, float r) {
+  const float a = round_dt<DT>(x - mn);
+  float n = a * r;
+  if (!(fabsf(n) < 512.0f && fabsf(n - rintf(n)) > 0x1p-12f)) n = a / safe;
+  if (n < 0.0f) n = 0.0f;
+  if (n > 255.0f) n = 255.0f;
+  return (uint8_t)(uint32_t)n;
+}
+
 template <int D, int MODE, int DT>
 __device__ __forceinline__ void quantize_row(const float (&x)[D / 64], uint8_t (&qb)[D / 64], float &scale,
                                              float &zero) {
@@ -385,7 +413,7 @@ __device__ __forceinline__ void quantize_row(const float (&x)[D / 64], uint8_t (
 #pragma unroll
     for (int e = 0; e < E; ++e) qb[e] = ref_q<DT>(x[e], mn, safe);
     scale = safe;
-    zero = mn;
+    zero = mn + 0.0f;  // a zero minimum is stored as +0 (min over +-0 depends on order)
   } else {
     constexpr int LPG = 64 / E;  // lanes per group of 64
     float w[E];

@@ -219,15 +219,16 @@ __global__ __launch_bounds__(256) void k_quantize_append_blocks(LayerView lv, co
         mx = fmaxf(mx, elem(e));
       }
       const float safe = ref_safe_scale<DT>(mn, mx);
+      const float rs = __builtin_amdgcn_rcpf(safe);
 #pragma unroll
       for (int c = 0; c < GE / 4; ++c) {
         uint32_t wv = 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) wv |= (uint32_t)ref_q<DT>(elem(4 * c + e), mn, safe) << (8 * e);
+        for (int e = 0; e < 4; ++e) wv |= (uint32_t)ref_q_r<DT>(elem(4 * c + e), mn, safe, rs) << (8 * e);
         qw[c] = wv;
       }
       scale = safe;
-      zero = mn;
+      zero = mn + 0.0f;  // a zero minimum is stored as +0 (min over +-0 depends on order)
     } else {
       float wmin = affine_w<DT>(elem(0)), wmax = wmin;
 #pragma unroll
@@ -237,11 +238,13 @@ __global__ __launch_bounds__(256) void k_quantize_append_blocks(LayerView lv, co
         wmax = fmaxf(wmax, w);
       }
       affine_params(wmin, wmax, scale, zero);
+      const float rs = __builtin_amdgcn_rcpf(scale);
 #pragma unroll
       for (int c = 0; c < GE / 4; ++c) {
         uint32_t wv = 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) wv |= (uint32_t)affine_q(affine_w<DT>(elem(4 * c + e)), scale, zero) << (8 * e);
+        for (int e = 0; e < 4; ++e)
+          wv |= (uint32_t)affine_q_r(affine_w<DT>(elem(4 * c + e)), scale, zero, rs) << (8 * e);
         qw[c] = wv;
       }
     }

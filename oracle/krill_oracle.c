@@ -107,6 +107,7 @@ static inline float dt_round(float f, int dt) {
  *   n = f32(round_dt(x - mn)) / safe                         (:192)
  *   q = uint8(trunc(clip(n, 0, 255)))                        (:193-194)
  *   returns (q, f16(safe), f16(mn))                          (:196)
+ *   (a zero mn is returned as +0: see below)
  */
 void oracle_quantize_ref_rows(const uint16_t *x, int dt, int64_t n_rows, int D,
                               uint8_t *q, uint16_t *scale_f16, uint16_t *zero_f16) {
@@ -127,7 +128,10 @@ void oracle_quantize_ref_rows(const uint16_t *x, int dt, int64_t n_rows, int D,
             q[r * D + d] = (uint8_t)n;
         }
         scale_f16[r] = oracle_f32_to_f16(safe);
-        zero_f16[r] = oracle_f32_to_f16(mn); /* identity for f16 input; RNE for bf16 */
+        /* identity for f16 input, RNE for bf16; a zero minimum is stored as +0:
+         * which of +0 / -0 a minimum over both returns depends on the order
+         * of the comparisons (the kernels reduce in a tree) */
+        zero_f16[r] = oracle_f32_to_f16(mn + 0.0f);
     }
 }
 
