@@ -147,7 +147,16 @@ class ContinuousBatcher:
 
     def step(self) -> int:
         """Retire, admit (prefill), then one decode step of every active row
-        that still has tokens to generate.  Returns the rows decoded."""
+        that still has tokens to generate.  Returns the rows decoded.  With a
+        `stream` (a torch stream) the whole step -- the model's inputs, the
+        table uploads, the workspace and the kernels -- runs on it."""
+        if self.stream is None:
+            return self._step()
+        torch = _torch()
+        with torch.cuda.stream(self.stream):
+            return self._step()
+
+    def _step(self) -> int:
         retired, admitted = self.sched.plan_step()
         for row in retired:
             self.pool.seq_free(row.seq)

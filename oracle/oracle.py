@@ -23,6 +23,8 @@ quantize_ref (a1)           (1) tiny-input brute force with exact rational
                             row -> scale 0 after fp16 rounding, q = 0, zero =
                             value; the row minimum always maps to q = 0);
                             (4) committed golden vectors (tests/golden/).
+                            A zero row minimum is returned as +0 (which of
+                            +-0 a minimum returns depends on comparison order).
 quantize_mlx (a1')          MLX's CPU affine quantize (third-party mlx 0.31
                             via mlx-swift 0.31.4, absent here) restated from
                             its published algorithm and pinned choice by

@@ -71,13 +71,13 @@ def _oracle(model, req, layer, scale):
     return out
 
 
-def _run(reqs, arrivals, max_rows, prefill_chunk, seed=0):
+def _run(reqs, arrivals, max_rows, prefill_chunk, seed=0, stream=None):
     model = SynthModel(reqs, seed)
     blocks = sum((r.prompt_len + r.max_new_tokens + 63) // 64 for r in reqs) + 4
     pool = krill_amd.KVPool(LAYERS, H, D, blocks, "affine_g64", DTS, free_list_seed=seed + 1)
     scale = 1.0 / np.sqrt(D)
     cb = ContinuousBatcher(pool, model, max_rows, H * R, scale, prefill_chunk=prefill_chunk,
-                           out_dtype=torch.float32)
+                           out_dtype=torch.float32, stream=stream)
     step = 0
     while step < 1000:
         for r in arrivals.get(step, []):
@@ -124,6 +124,21 @@ def test_batched_equals_alone():
     assert batched.out.keys() == alone.out.keys()
     dev = max(np.abs(batched.out[k] - alone.out[k]).max() for k in batched.out)
     assert dev <= 1e-5, dev
+
+
+def test_batcher_on_its_own_stream_matches_the_current_stream():
+    # the whole step (inputs, table uploads, workspace, kernels) on a side
+    # stream (default priority): the same outputs as on torch's current stream
+    print("\ncase batcher_stream", flush=True)
+    arrivals = lambda rq: {0: rq[:3], 2: rq[3:]}  # noqa: E731
+    reqs = _requests()
+    cur, _, _ = _run(reqs, arrivals(reqs), max_rows=3, prefill_chunk=48)
+    reqs2 = _requests()
+    side, stats, _ = _run(reqs2, arrivals(reqs2), max_rows=3, prefill_chunk=48, stream=torch.cuda.Stream())
+    assert stats["blocks_used"] == 0
+    assert cur.out.keys() == side.out.keys()
+    for k in cur.out:
+        assert np.array_equal(cur.out[k], side.out[k]), k
 
 
 def test_cancel_frees_blocks():
