@@ -1021,7 +1021,10 @@ def run_verify(args, w):
     seqs_np = np.array(seqs, np.int32)
     slots_h = np.empty(k, np.int32)
     cur_len = [int(x) for x in lens0]
-    acc_rng = Philox(args.seed, S_ACCEPT)
+    # accepted drafts per (step, sequence), drawn before the steps (no
+    # generator work inside the timed loop)
+    acc_draws = Philox(args.seed, S_ACCEPT).integers(0, k + 1, size=(args.warmup + args.steps + 1) * B)
+    acc_pos = [0]
     accepted_total = [0]
 
     def verify(layer, mx):
@@ -1047,7 +1050,8 @@ def run_verify(args, w):
             if not rollback:  # chunked prefill keeps every row
                 accepted_total[0] += k
                 continue
-            a = int(acc_rng.integers(0, k + 1))
+            a = int(acc_draws[acc_pos[0]])
+            acc_pos[0] += 1
             keep_rows = a + 1 if a < k else k
             cur_len[b] += keep_rows - k
             accepted_total[0] += keep_rows
