@@ -220,6 +220,18 @@ def test_verify_attention_mfma_causal(mode, D):
     assert err <= ATOL, f"max abs error {err:.3e}"
 
 
+@pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
+@pytest.mark.parametrize("D,R,Lq", [(128, 5, 5), (64, 3, 6), (128, 2, 16), (64, 17, 1)])
+def test_verify_attention_token_split_partial_rows(mode, D, R, Lq):
+    # 17-32 rows per KV head: one 32-row group whose two waves split the
+    # tokens; here with 18-32 valid rows, edge and split blocks, ragged lengths
+    print(f"\ncase verify_token_split mode={mode} D={D} R={R} Lq={Lq}", flush=True)
+    got, ref = _attn_case(mode, D, 2, R, [Lq, 40, 64, 65, 129, 700], Lq=Lq, split_blocks=2 if R == 2 else 0,
+                          seed=3 * R + Lq)
+    err = np.abs(got - ref).max()
+    assert err <= ATOL, f"max abs error {err:.3e}"
+
+
 def test_verify_attention_mfma_splits_and_row_groups():
     print("\ncase verify_mfma_rowgroups", flush=True)
     # 16 draft rows x 5 heads = 80 rows -> several row groups; small splits
