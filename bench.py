@@ -1150,7 +1150,8 @@ def traffic_source(args, call):
 
 def cpu_baseline(args, w, lens0, per_tok):
     """Time the oracle's restatement of the reference step (quantize row ->
-    concat -> full-cache fp16 dequant -> fp32 SDPA) on a bounded sample."""
+    concat -> full-cache fp16 dequant -> SDPA as MLX's composed ops, float32 for
+    bf16 queries) on a bounded sample."""
     from oracle import oracle as O
 
     Hq, Hkv, D = w["Hq"], w["Hkv"], w["D"]
@@ -1201,7 +1202,7 @@ def cpu_baseline(args, w, lens0, per_tok):
         "kind": "port",
         "sample": f"{reps} decode steps x {sample_layers} layers of the same batch ({B} seqs, same lengths) "
                   f"through the CPU restatement of the reference step (row quantize, concat, full fp16 dequant, "
-                  f"fp32 SDPA); {el:.1f} s; GB/s on the row layout's {per_tok} B per token and layer; "
+                  f"SDPA as MLX's composed ops, float32 for bf16 queries); {el:.1f} s; GB/s on the row layout's {per_tok} B per token and layer; "
                   f"tokens/s extrapolated to {layers} layers",
         "single_thread": {"value": round(ctx * per_tok / one_s / 1e9, 3), "unit": "GB/s",
                           "tokens_per_s": round(B / (one_s * layers), 4),

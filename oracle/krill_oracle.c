@@ -339,9 +339,12 @@ int64_t oracle_common_prefix_length(const int64_t *a, int64_t na, const int64_t 
 /*   2. concatenated(...) the six tensors along the sequence axis -- a fresh */
 /*      allocation and an O(T) copy per tensor (:55-61)                      */
 /*   3. dequantize the WHOLE cache to fp16 (:72-73, :200-204)                */
-/*   4. SDPA with GQA.  The queries are bf16 and the dequantized K/V fp16, so */
-/*      MLX promotes the products to float32: scores, softmax and P.V are    */
-/*      computed in float32 here.                                            */
+/*   4. SDPA with GQA as MLX's composed ops run it (attention_mlx_composed  */
+/*      in oracle.py): the query scaled in its own dtype (the scale a scalar */
+/*      of that dtype), scores = q . K^T, a precise softmax, out = P . V,    */
+/*      float32 accumulation; with fp16 queries the scores, the weights and  */
+/*      the output are each rounded to fp16, with bf16 queries the products  */
+/*      promote to float32 (bf16 x fp16) and stay there.                     */
 /* Parallel over (sequence, kv-head) with OpenMP.                            */
 /* ------------------------------------------------------------------------ */
 typedef struct {
@@ -476,17 +479,19 @@ void oracle_baseline_step(void *h, const uint16_t *q, const uint16_t *k_new, con
                 kf[i] = oracle_f16_to_f32(dk[i]);
                 vf[i] = oracle_f16_to_f32(dv[i]);
             }
+            const int half = dt == DT_F16;  /* fp16 queries: fp16 products */
+            const float sdt = dt_round(scale, dt);
             for (int j = 0; j < R; ++j) {
                 int hq = hk * R + j;
                 const uint16_t *qr = q + (((int64_t)l * B + b) * Hq + hq) * D;
                 float qf[512];
-                for (int d = 0; d < D; ++d) qf[d] = dt_to_f32(qr[d], dt);
+                for (int d = 0; d < D; ++d) qf[d] = dt_round(dt_to_f32(qr[d], dt) * sdt, dt);
                 float mx = -INFINITY;
                 for (int t = 0; t < T; ++t) {
                     float acc = 0.0f;
                     const float *kr = kf + (int64_t)t * D;
                     for (int d = 0; d < D; ++d) acc += qf[d] * kr[d];
-                    sc[t] = acc * scale;
+                    sc[t] = half ? dt_round(acc, DT_F16) : acc;
                     if (sc[t] > mx) mx = sc[t];
                 }
                 float lsum = 0.0f;
@@ -495,9 +500,12 @@ void oracle_baseline_step(void *h, const uint16_t *q, const uint16_t *k_new, con
                 for (int d = 0; d < D; ++d) o[d] = 0.0f;
                 for (int t = 0; t < T; ++t) {
                     float p = sc[t] / lsum;
+                    if (half) p = dt_round(p, DT_F16);
                     const float *vr = vf + (int64_t)t * D;
                     for (int d = 0; d < D; ++d) o[d] += p * vr[d];
                 }
+                if (half)
+                    for (int d = 0; d < D; ++d) o[d] = dt_round(o[d], DT_F16);
             }
             free(dk); free(dv); free(sc); free(kf); free(vf);
         }

@@ -659,3 +659,42 @@ def test_rotating_retained_start_reference_vectors(oracle):
     # append is min(retained, window - 1)
     total, start = oracle.rotating_retained_start([("append", L) for L in (5, 3, 12, 1, 9, 6)], 8)
     assert (total, total - start) == (36, 7 + 6)
+
+
+# -------------------------------------------------------------- CPU baseline
+
+@pytest.mark.parametrize("dtname", ["bf16", "f16"])
+def test_cpu_baseline_step_is_the_composed_sdpa(oracle, dtname):
+    """The timed CPU baseline (the reference's step restated in C: row
+    quantize, concat, full fp16 dequant, SDPA as MLX's composed ops) against
+    the row quantizer, the dequantizer and attention_mlx_composed, over two
+    steps from an empty cache (one key, then two)."""
+    B, Hkv, Hq, D = 2, 2, 4, 64
+    R = Hq // Hkv
+    dt = oracle.DT_BF16 if dtname == "bf16" else oracle.DT_F16
+    rng = np.random.default_rng(40 + dt)
+    base = oracle.Baseline(1, B, Hkv, Hq, D, np.zeros(B, np.int32), seed=1)
+    mk = oracle.f32_to_bf16_bits if dt == oracle.DT_BF16 else oracle.f32_to_f16_bits
+    ks, vs = [], []
+    scale = 1.0 / np.sqrt(D)
+    for step in range(2):
+        q = mk(rng.standard_normal((1, B, Hq, D)).astype(np.float32))
+        k = mk(rng.standard_normal((1, B, Hkv, D)).astype(np.float32))
+        v = mk(rng.standard_normal((1, B, Hkv, D)).astype(np.float32))
+        ks.append(k[0])
+        vs.append(v[0])
+        out = np.empty((1, B, Hq, D), np.float32)
+        base.step(q, k, v, dt, scale, out)
+        for b in range(B):
+            for hk in range(Hkv):
+                kr = np.stack([x[b, hk] for x in ks])  # [T, D] bits
+                vr = np.stack([x[b, hk] for x in vs])
+                kf16 = oracle.dequant_ref_f16(*oracle.quantize(kr, dt, 0))
+                vf16 = oracle.dequant_ref_f16(*oracle.quantize(vr, dt, 0))
+                qr = q[0, b, hk * R:(hk + 1) * R]
+                want = oracle.attention_mlx_composed(qr, dt, kf16, vf16, [step + 1] * R, scale)
+                got = out[0, b, hk * R:(hk + 1) * R].astype(np.float64)
+                if step == 0:  # one key: the value row exactly
+                    np.testing.assert_array_equal(got, want)
+                np.testing.assert_allclose(got, want, rtol=2e-3 if dt == oracle.DT_F16 else 1e-5, atol=1e-6)
+    base.close()
