@@ -670,7 +670,14 @@ static hipError_t launch_mfma_dm(const AttnArgs &args, const AttnPlan &p, dim3 g
     }
     return hipErrorInvalidValue;
   }
-  if (p.token_split != 1 || p.nrt != 1) return hipErrorInvalidValue;
+  if (p.token_split != 1) return hipErrorInvalidValue;
+  if (p.nrt == 2) {
+    if constexpr (D <= 128) {
+      if (p.group_waves == 4) return launch_mfma_w<D, MODE, 2, 4, 1>(args, grid, st);
+    }
+    return hipErrorInvalidValue;
+  }
+  if (p.nrt != 1) return hipErrorInvalidValue;
   switch (p.group_waves) {
     case 1: return launch_mfma_w<D, MODE, 1, 1, 1>(args, grid, st);
     case 2: return launch_mfma_w<D, MODE, 1, 2, 1>(args, grid, st);
@@ -721,20 +728,23 @@ static int32_t occupancy_mfma_sel(int sel) {
     case 0: return occupancy_mfma<D, MODE, 1, 1, 1>();
     case 1: return occupancy_mfma<D, MODE, 1, 2, 1>();
     case 2: return occupancy_mfma<D, MODE, 1, 4, 1>();
-    default:
+    case 3:
       if constexpr (D <= 128) return occupancy_mfma<D, MODE, 2, 2, 2>();
+      return 1;
+    default:
+      if constexpr (D <= 128) return occupancy_mfma<D, MODE, 2, 4, 1>();
       return 1;
   }
 }
 
 int32_t mfma_groups_per_cu(const PoolGeometry &g, int32_t nrt, int32_t group_waves, int32_t token_split) {
   const int dsel = g.D == 64 ? 0 : g.D == 128 ? 1 : 2;
-  const int sel = token_split == 2 ? 3 : group_waves == 4 ? 2 : group_waves == 2 ? 1 : 0;
+  const int sel = token_split == 2 ? 3 : nrt == 2 ? 4 : group_waves == 4 ? 2 : group_waves == 2 ? 1 : 0;
   if (g.num_cus <= 0) {  // host-only pool: the LDS bound (the ring per workgroup, 160 KB per CU)
-    static const int est[3][4] = {{5, 5, 3, 8}, {3, 3, 2, 4}, {1, 1, 1, 1}};
+    static const int est[3][5] = {{5, 5, 3, 8, 3}, {3, 3, 2, 4, 2}, {1, 1, 1, 1, 1}};
     return est[dsel][sel];
   }
-  static int cache[2][3][4] = {};  // [mode][D][shape], filled on first use per process
+  static int cache[2][3][5] = {};  // [mode][D][shape], filled on first use per process
   int &c = cache[g.mode == MODE_AFFINE][dsel][sel];
   if (c == 0) {
     int v;

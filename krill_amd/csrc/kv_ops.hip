@@ -1045,14 +1045,27 @@ int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq,
     // 16-row wave leaves room for two waves per SIMD.
     // 17-32 rows (speculative verify) at D <= 128: one 32-row group per
     // workgroup whose two waves split each block's tokens instead, so no
-    // byte is converted twice.
+    // byte is converted twice.  More than 64 rows at D <= 128 (chunked
+    // prefill): 32-row waves in groups of four, each converted byte feeding
+    // two row tiles, when a batch of max_seq_len sequences gives every
+    // workgroup of that grid at least 16 blocks to stream (the cascade's
+    // shared prefix of 65 blocks does not: its 16-row grid keeps more
+    // workgroups busy).
     p.token_split = 1;
+    const int64_t grp32 = ((p.NR + 31) / 32 + 3) / 4;
+    const bool rows32 = p.NR > 64 && g.D <= 128 &&
+                        tmax >= 16 * (cus * mfma_groups_per_cu(g, 2, 4, 1) / ((int64_t)g.Hkv * grp32));
     if (p.NR > 16 && p.NR <= 32 && g.D <= 128) {
       p.nrt = 2;
       p.rows_per_group = 32;
       p.row_groups = 1;
       p.group_waves = 1;
       p.token_split = 2;
+    } else if (rows32) {
+      p.nrt = 2;
+      p.rows_per_group = 32;
+      p.row_groups = (p.NR + 31) / 32;
+      p.group_waves = 4;
     } else {
       p.nrt = 1;
       p.rows_per_group = 16;

@@ -200,6 +200,46 @@ def test_decode_attention_many_partials(mode):
     assert err <= ATOL, f"max abs error {err:.3e}"
 
 
+@pytest.mark.parametrize("R", [5, 1])
+def test_decode_attention_any_workspace_contents(R):
+    """Callers reuse one workspace across calls without clearing it: whatever
+    it holds before the call (zeros, all ones, 0x7F bytes, random bytes, the
+    previous call's partials) the output is the same, bit for bit, and within
+    the bound of the float64 oracle.  The automatic split over many ragged
+    and empty sequences puts wave and sequence boundaries at many offsets."""
+    print(f"\ncase decode_any_workspace R={R}", flush=True)
+    rng = np.random.default_rng(77 + R)
+    H, D, dt = 2, 128, "bf16"
+    lens = [int(x) for x in rng.integers(1, 1500, size=40)] + [0, 64, 65, 1]
+    pool = make_pool(H, D, "affine_g64", dt, blocks=sum((T + 63) // 64 for T in lens) + 8)
+    f = Filled(pool, lens, rng, dt)
+    tables, tl, _ = f.tables()
+    qb = rand_bits(rng, (len(lens), H * R, 1, D), dt)
+    q = to_dev(qb, dt)
+    need = pool.workspace_size(len(lens), H * R, 1, max(lens))
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    outs = []
+    for fill in ("zeros", "ones", "0x7f", "random", "previous"):
+        if fill == "zeros":
+            ws.zero_()
+        elif fill == "ones":
+            ws.fill_(0xFF)
+        elif fill == "0x7f":
+            ws.fill_(0x7F)
+        elif fill == "random":
+            ws.copy_(torch.from_numpy(rng.integers(0, 256, size=need, dtype=np.uint8)).cuda())
+        out = pool.attention(0, q, tables, tl, max(lens), 1.0 / np.sqrt(D), ws=ws)
+        torch.cuda.synchronize()
+        outs.append(out.float().cpu().numpy())
+        print(f"workspace {fill}: done", flush=True)
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+    ref = oracle_attention(pool, f, 0, qb, dt, 1.0 / np.sqrt(D))
+    err = np.abs(outs[0] - ref).max()
+    pool.close()
+    assert err <= ATOL, f"max abs error {err:.3e}"
+
+
 @pytest.mark.parametrize("out_dtype", ["bf16", "f16"])
 def test_decode_attention_low_precision_output(out_dtype):
     print(f"\ncase decode_out {out_dtype}", flush=True)
@@ -236,6 +276,21 @@ def test_verify_attention_mfma_splits_and_row_groups():
     print("\ncase verify_mfma_rowgroups", flush=True)
     # 16 draft rows x 5 heads = 80 rows -> several row groups; small splits
     got, ref = _attn_case("affine_g64", 128, 2, 5, [40, 300, 777], Lq=16, split_blocks=2, seed=5)
+    err = np.abs(got - ref).max()
+    assert err <= ATOL, f"max abs error {err:.3e}"
+
+
+@pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
+@pytest.mark.parametrize("D", [128, 64])
+def test_prefill_chunk_32_row_waves(mode, D):
+    """A prefill chunk of 32 positions x 5 query heads per KV head (160 rows)
+    over a batch long enough (8 x 129 blocks of max_seq_len) that every
+    workgroup of the 32-row grid streams at least 16 blocks: 32-row waves
+    (two MFMA row tiles per converted byte) in groups of four, five row
+    groups, so the second group holds one row group and three spare waves;
+    causal rows, ragged lengths, edge blocks."""
+    print(f"\ncase prefill_rows32 mode={mode} D={D}", flush=True)
+    got, ref = _attn_case(mode, D, 8, 5, [8200, 2500, 900, 65, 4000, 7000, 130, 3000], Lq=32, seed=61 + D)
     err = np.abs(got - ref).max()
     assert err <= ATOL, f"max abs error {err:.3e}"
 
