@@ -661,7 +661,7 @@ static hipError_t launch_mfma_w(const AttnArgs &args, dim3 grid, hipStream_t st)
 
 // (nrt, group_waves, token_split) shapes the plan may choose: 16-row waves
 // in workgroups of 1, 2 or 4 row groups, or (D <= 128) a 32-row group split
-// over two waves by tokens.
+// over two waves by tokens, or (D <= 128) 32-row waves in workgroups of 4.
 template <int D, int MODE>
 static hipError_t launch_mfma_dm(const AttnArgs &args, const AttnPlan &p, dim3 grid, hipStream_t st) {
   if (p.token_split == 2) {
