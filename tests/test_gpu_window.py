@@ -198,3 +198,26 @@ def test_window_f16_inputs(Lq):
     _check(pools, sl, W, Lq, "affine_g64", rng, R, tol_pair=1e-3)
     for p in pools:
         p.close()
+
+
+@pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
+def test_window_prefill_chunk_32_row_waves(mode):
+    """A 32-position chunk x 5 query heads per KV head (160 rows) over four
+    long sequences with an 8192-token window (windowed calls are planned on
+    min(max_seq_len, window + Lq + 62) tokens: here long enough for 32-row
+    waves in groups of four), each chunk appended after its prefix; the
+    longest sequence's first retained token (9) and its rows' window starts
+    fall inside its first block."""
+    print(f"\ncase window_prefill_rows32 mode={mode}", flush=True)
+    W, H, D, R, Lq = 8192, 8, 128, 5, 32
+    rng = np.random.default_rng(71)
+    lens = [8200, 3000, 6100, 900]
+    pools = _pools(mode, H, D, sum((n + Lq + 63) // 64 for n in lens) + 8, W, seed=21)
+    sl = [Seqs(p, len(lens), max(lens) + Lq, np.random.default_rng(73)) for p in pools]
+    for ss in sl:
+        for b, n in enumerate(lens):
+            ss.append(b, n)
+            ss.append(b, Lq)
+    _check(pools, sl, W, Lq, mode, rng, R, tol_pair=1e-3)
+    for p in pools:
+        p.close()
