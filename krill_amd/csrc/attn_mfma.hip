@@ -87,7 +87,11 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
   const int wid = W > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;
   const int n = lane & 15, q4 = lane >> 4;
   const int RGB = (a.row_groups + WR - 1) / WR;  // workgroups per KV head and block range
-  const int wv = blockIdx.x, hk = blockIdx.y / RGB, rg = (blockIdx.y % RGB) * WR + (TS > 1 ? 0 : wid);
+  // range index rotated by the KV head, as in the decode kernel: range w of
+  // the heads on different XCDs, while the row groups of one head, which
+  // read the same bytes, keep range w on one XCD and share its L2
+  const int hk = blockIdx.y / RGB, rg = (blockIdx.y % RGB) * WR + (TS > 1 ? 0 : wid);
+  const int wv = (int)((blockIdx.x + (unsigned)hk) % gridDim.x);
   const int tt0 = TS > 1 ? wid * NTT : 0;  // first score tile / P.V group of this wave
   const int tg0 = TS > 1 ? wid * NTG : 0;
   const int RG = a.row_groups;

@@ -229,7 +229,14 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   __shared__ __attribute__((aligned(16))) uint16_t sz_lds[2 * 64];
 
   const int lane = threadIdx.x;
-  const int wv = blockIdx.x, hk = blockIdx.y;
+  // Every KV head splits its blocks into the same ranges, and workgroups go
+  // to the 8 XCDs round-robin by linear id, so with the range index equal to
+  // blockIdx.x (the wave count a multiple of 8) range w of every head would
+  // land on the same XCD.  Rotating the range by the head sends range w of
+  // the 8 heads to 8 different XCDs: the ranges that cost more (sequence
+  // ends inside them) no longer pile up on one XCD.
+  const int hk = blockIdx.y;
+  const int wv = (int)((blockIdx.x + (unsigned)hk) % gridDim.x);
   // This wave's blocks: flat indices [i0, iend) of the concatenated block
   // lists of all sequences.  The T blocks are split evenly over the grid's
   // waves (sized to the resident wave capacity of the GPU; min(W, T) of them
