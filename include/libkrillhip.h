@@ -126,7 +126,11 @@ int32_t krill_pool_get_stats(krill_pool_t pool, krill_pool_stats *out);
 int32_t krill_pool_set_stream(krill_pool_t pool, krill_stream_t stream);
 int32_t krill_pool_set_option(krill_pool_t pool, int32_t option, int64_t value);
 /* Issue queued copy-on-write block copies on `stream` (kernels do this
- * themselves before they touch the pool). */
+ * themselves before they touch the pool).  Copies are never issued into a
+ * stream that is capturing a HIP graph: there this call, and any kernel
+ * entry point while copies are queued, fails with KRILL_E_STATE and leaves
+ * the copies queued.  Callers that replay graphs flush eagerly after each
+ * step's krill_seq_reserve_append calls. */
 int32_t krill_pool_flush(krill_pool_t pool, krill_stream_t stream);
 
 /* Introspection (tests, debugging): copy the per-block reference counts of
@@ -294,7 +298,8 @@ int32_t krill_decode_append_attention(krill_pool_t pool, int32_t layer, const vo
  * shares that GPU's array and leaves its partials there (nothing in it
  * needs to start at zero): calls that overlap on one GPU -- on different
  * streams, or from several pools or threads -- race, so keep them on one
- * stream or ordered by events. */
+ * stream or ordered by events.  Under graph capture, queued copy-on-write
+ * copies must be flushed eagerly first (krill_pool_flush). */
 #define KRILL_NOALLOC_SCRATCH_BYTES (32u << 20)
 int32_t krill_decode_append_attention_noalloc(krill_pool_t pool, int32_t layer, const void *dev_q,
                                               const void *dev_k_new, const void *dev_v_new, int64_t stride_b,

@@ -533,6 +533,11 @@ std::vector<CopyPair> BlockManager::take_pending() {
   return out;
 }
 
+bool BlockManager::has_pending() {
+  std::lock_guard<std::mutex> g(mu_);
+  return !pending_.empty();
+}
+
 int32_t BlockManager::refcounts(int32_t *out, int32_t cap) {
   std::lock_guard<std::mutex> g(mu_);
   if (cap < 0 || (cap > 0 && !out)) return fail(KRILL_E_INVAL, "bad output buffer");

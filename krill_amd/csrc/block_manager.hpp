@@ -82,6 +82,7 @@ class BlockManager {
 
   // Queued copy-on-write copies, removed from the queue.
   std::vector<CopyPair> take_pending();
+  bool has_pending();
   BlockManagerStats stats();
   int32_t refcounts(int32_t *out, int32_t cap);
 

@@ -75,12 +75,30 @@ int32_t check_device_pool(krill_pool_t p, int32_t layer) {
 hipStream_t pick_stream(krill_pool_t p, krill_stream_t s) { return s ? static_cast<hipStream_t>(s) : p->stream; }
 
 // Issue queued copy-on-write copies before anything touches the pool.
+// Copies are never issued into a stream that is capturing a HIP graph: the
+// graph would carry this step's (source, destination) pairs by value and
+// repeat them on every replay, copying the shared block over the tokens
+// appended to the private copy since, while copies queued between replays
+// would never run.  Such a call fails with KRILL_E_STATE and leaves the
+// copies queued; the caller flushes eagerly (krill_pool_flush) before it
+// captures or replays.
 int32_t flush_pending(krill_pool_t p, hipStream_t st) {
   if (p->host_only) {
     (void)p->bm->take_pending();
     return KRILL_OK;
   }
   std::lock_guard<std::mutex> g(p->flush_mu);
+  if (!p->bm->has_pending()) return KRILL_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  const hipError_t ce = hipStreamIsCapturing(st, &cs);
+  if (ce != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(KRILL_E_STATE, "copy-on-write block copies are queued and the stream's capture state is unknown "
+                "(%s): call krill_pool_flush on an idle stream first", hipGetErrorString(ce));
+  }
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(KRILL_E_STATE, "copy-on-write block copies are queued while the stream captures a graph: call "
+                "krill_pool_flush eagerly after krill_seq_reserve_append, before capturing and before each replay");
   std::vector<krill::CopyPair> pairs = p->bm->take_pending();
   if (pairs.empty()) return KRILL_OK;
   hipError_t e = krill::launch_copy_pairs(p->geom, pairs.data(), static_cast<int32_t>(pairs.size()), st);

@@ -40,11 +40,14 @@ def _batch(caches):
     return pool, layer
 
 
-def _tables(pool, caches, device):
-    """Block tables [B, max_blocks] and this layer's lengths [B] on `device`."""
+def _tables(pool, caches, device, extra: int = 0):
+    """Block tables [B, max_blocks] and this layer's lengths (+ `extra`) [B]
+    on `device`.  The table width covers every block the sequences hold: a
+    layer may be behind its sequence (restored or appended one layer at a
+    time), and the tables carry the whole sequence."""
     torch = _torch()
-    lens = np.array([c.sequence_length for c in caches], np.int32)
-    mb = max(1, int(max((int(n) + 63) // 64 for n in lens)))
+    lens = np.array([c.sequence_length + extra for c in caches], np.int32)
+    mb = max(1, int(max((int(c.s.length) + 63) // 64 for c in caches)), int(max((int(n) + 63) // 64 for n in lens)))
     t, _ = pool.batch_tables([c.s.seq for c in caches], mb)
     return (torch.as_tensor(np.ascontiguousarray(t), device=device),
             torch.as_tensor(lens, device=device), int(lens.max()) if lens.size else 0)
@@ -81,9 +84,15 @@ class KrillKernels:
         B, L_ = int(keys.shape[0]), int(keys.shape[2])
         if B != len(caches) or tuple(values.shape) != tuple(keys.shape):
             raise ValueError("keys/values must be [len(caches), Hkv, L, D]")
-        slots = np.stack([c.s.slots_for(layer, L_) for c in caches]).astype(np.int32)
-        pool.quantize_append(layer, keys.contiguous(), values.contiguous(),
-                             torch.as_tensor(slots, device=keys.device))
+        try:
+            slots = np.stack([c.s.slots_for(layer, L_) for c in caches]).astype(np.int32)
+            pool.quantize_append(layer, keys.contiguous(), values.contiguous(),
+                                 torch.as_tensor(slots, device=keys.device))
+        except BaseException:
+            # nothing was appended: release what the reservation added
+            for c in caches:
+                c.s.shrink_to_layers()
+            raise
         for c in caches:
             c.s.layer_len[layer] += L_
 
@@ -98,14 +107,28 @@ class KrillKernels:
             raise ValueError("queries must be [len(caches), Hq, 1, D]")
         if (keys is None) != (values is None):
             raise ValueError("keys and values come together")
-        if keys is not None:
+        if keys is None:
+            tables, lens, max_len = _tables(pool, caches, queries.device)
+            return pool.attention(layer, queries, tables, lens, max_len, scale, out_dtype)
+        want = (len(caches), pool.num_kv_heads, 1, pool.head_dim)
+        if tuple(keys.shape) != want or tuple(values.shape) != want:
+            raise ValueError(f"keys/values must be {list(want)}")
+        # The caches change only once the launch is accepted: the slots are
+        # reserved first (the kernel writes position len - 1 of each table),
+        # and released again if the call fails.
+        try:
             for c in caches:
                 c.s.slots_for(layer, 1)
-                c.s.layer_len[layer] += 1
-        tables, lens, max_len = _tables(pool, caches, queries.device)
-        if keys is None:
-            return pool.attention(layer, queries, tables, lens, max_len, scale, out_dtype)
-        return pool.decode_append_attention(layer, queries, keys, values, tables, lens, max_len, scale, out_dtype)
+            tables, lens, max_len = _tables(pool, caches, queries.device, extra=1)
+            out = pool.decode_append_attention(layer, queries, keys, values, tables, lens, max_len, scale,
+                                               out_dtype)
+        except BaseException:
+            for c in caches:
+                c.s.shrink_to_layers()
+            raise
+        for c in caches:
+            c.s.layer_len[layer] += 1
+        return out
 
     @staticmethod
     def paged_verify_attention(queries, caches, scale: float, out_dtype=None):

@@ -700,3 +700,54 @@ def test_krill_kernels_validate_the_batch_on_the_host():
         KrillKernels.paged_decode_attention(q, [a[0], object()], 0.1)
     assert isinstance(KrillKernels.status(), str)
     p.close()
+
+
+def test_krill_kernels_change_no_state_when_the_call_fails():
+    """A decode step whose launch is refused leaves every cache as it was:
+    no layer length advances and no reserved position stays behind (here the
+    call fails because the tensors are not on a HIP device)."""
+    import torch
+
+    from krill_amd import KrillKernels
+    from krill_amd.cache import make_quantized_kv_caches
+
+    p = host_pool()
+    a = make_quantized_kv_caches(p)
+    b = make_quantized_kv_caches(p)
+    for c in (a[0], b[0], a[1], b[1]):
+        c.s.slots_for(c.layer, 70)
+        c.s.layer_len[c.layer] += 70
+    q = torch.zeros((2, 4, 1, 128), dtype=torch.bfloat16)
+    kv = torch.zeros((2, 2, 1, 128), dtype=torch.bfloat16)
+    before = [(p.seq_length(c.s.seq), list(c.s.layer_len)) for c in (a[0], b[0])]
+    with pytest.raises(Exception):
+        KrillKernels.paged_decode_attention(q, [a[0], b[0]], 0.1, keys=kv, values=kv)
+    assert [(p.seq_length(c.s.seq), list(c.s.layer_len)) for c in (a[0], b[0])] == before
+    with pytest.raises(ValueError, match="keys/values"):
+        KrillKernels.paged_decode_attention(q, [a[0], b[0]], 0.1, keys=kv[:, :1], values=kv[:, :1])
+    assert [(p.seq_length(c.s.seq), list(c.s.layer_len)) for c in (a[0], b[0])] == before
+    with pytest.raises(Exception):
+        KrillKernels.quantize_append([a[0], b[0]], torch.zeros((2, 2, 3, 128), dtype=torch.bfloat16),
+                                     torch.zeros((2, 2, 3, 128), dtype=torch.bfloat16))
+    assert [(p.seq_length(c.s.seq), list(c.s.layer_len)) for c in (a[0], b[0])] == before
+    p.close()
+
+
+def test_krill_kernels_tables_cover_a_layer_behind_its_sequence():
+    """The table width follows the blocks each sequence holds, not the layer's
+    length: layer 1 two blocks behind layer 0 still gets whole tables."""
+    from krill_amd.cache import make_quantized_kv_caches
+    from krill_amd.kernels import _tables
+
+    torch = pytest.importorskip("torch")
+    p = host_pool()
+    c0, c1 = make_quantized_kv_caches(p)
+    c0.s.slots_for(0, 200)
+    c0.s.layer_len[0] += 200
+    c1.s.layer_len[1] = 60  # as a restore of a 60-token snapshot into layer 1 leaves it
+    t, lens, mx = _tables(p, [c1], "cpu")
+    assert t.shape == (1, 4) and int(lens[0]) == 60 and mx == 60
+    np.testing.assert_array_equal(t.numpy()[0], p.block_table(c0.s.seq))
+    t, lens, mx = _tables(p, [c1], "cpu", extra=1)
+    assert t.shape == (1, 4) and int(lens[0]) == 61
+    p.close()

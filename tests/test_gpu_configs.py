@@ -6,7 +6,8 @@ float64 oracle (2e-3 max-abs) and the cache bytes against the oracle's
 quantization (bit-exact):
 - Llama-3.2-1B, one sequence of 2048 tokens, a decode step with the append
   fused on the first and the last of 16 layers;
-- Qwen3-14B, 32 sequences of U[512, 8192] tokens, the fused decode step;
+- Qwen3-14B, 32 sequences of U[512, 8192] tokens, the fused decode step, in
+  affine group-64 and in the reference's row mode;
 - Llama-3-8B, 64 sequences forked from one 4120-token prefix, each with
   U[0, 1024] tokens of its own (copy-on-write of the shared partial block),
   the shared-prefix decode step with the append fused; the prefix sequence
@@ -16,9 +17,16 @@ quantization (bit-exact):
   SpeculativeDecoder.swift:309-318 (keep the accepted rows, truncate the
   rest), then one more fused decode step: the rows truncated away are
   neither attended nor left in the cache;
+- Llama-3-8B shared prefix with the pool crossing its 90 % watermark: an
+  unreferenced prefix entry is evicted while the forks append, its blocks
+  are reissued to them (stale bytes beyond each fork's length), then the
+  cascade step, against the oracle;
 - Qwen3-30B-A3B long context: 2 of the 8 sequences at 131072 tokens with
-  x20 outlier channels, the fused decode step.
-Inputs are seeded N(0,1) bf16, affine int8 in groups of 64."""
+  x20 outlier channels, the fused decode step; and all 8 sequences at
+  131072 tokens (the benchmark's grid) with keys equal inside each 64-token
+  block, where the output has a closed form over per-block sums.
+Inputs are seeded N(0,1) bf16, affine int8 in groups of 64 unless a case
+names the row mode."""
 import numpy as np
 import pytest
 
@@ -83,12 +91,13 @@ def test_llama32_1b_b1_decode_step():
     pool.close()
 
 
-def test_qwen3_14b_b32_decode_step():
-    print("\ncase config qwen3-14b b32 U[512,8192]", flush=True)
+@pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
+def test_qwen3_14b_b32_decode_step(mode):
+    print(f"\ncase config qwen3-14b b32 U[512,8192] {mode}", flush=True)
     rng = np.random.default_rng(20261202)
     H, R, D = 8, 5, 128
     ctx = [int(x) for x in rng.integers(512, 8193, 32)]
-    pool = krill_amd.KVPool(1, H, D, _blocks(ctx), "affine_g64", DT, free_list_seed=2)
+    pool = krill_amd.KVPool(1, H, D, _blocks(ctx), mode, DT, free_list_seed=2)
     f = Filled(pool, ctx, rng, DT, max_chunk=512)
     err, tables, lens = _fused_steps(pool, f, rng, R)
     print(f"max abs error {err:.3e}", flush=True)
@@ -209,4 +218,127 @@ def test_qwen3_30b_a3b_128k_decode_step():
     err, tables, lens = _fused_steps(pool, f, rng, R, outlier_frac=0.01)
     print(f"max abs error {err:.3e}", flush=True)
     assert err <= ATOL, f"max abs error {err:.3e}"
+    pool.close()
+
+
+def test_llama3_8b_shared_prefix_after_watermark_eviction():
+    """Config 3 with LRU eviction on the GPU: a 1000-token prefix entry that
+    no sequence holds any more is the pool's oldest; while 64 forks of a
+    4120-token prefix append their own tokens the pool crosses 90 % of its
+    blocks, the entry is evicted (PrefixCache.swift:535-551 at block level)
+    and its blocks are handed to the forks.  The cascade step with the
+    append fused must then match the oracle, and the forks' bytes too."""
+    print("\ncase config llama-3-8b shared prefix b64 + watermark eviction", flush=True)
+    rng = np.random.default_rng(20261213)
+    H, R, D, B, PT, VT = 8, 4, 128, 64, 4120, 1000
+    extra = [int(x) for x in rng.integers(0, 1025, B)]
+    P = PT // 64
+    used_final = (PT + 63) // 64 + sum((PT % 64 + T + 1 + 63) // 64 for T in extra)
+    nb = used_final + 12  # 90 % of it is below used_final + the entry's 16 blocks
+    pool = krill_amd.KVPool(1, H, D, nb, "affine_g64", DT, free_list_seed=13, max_prefix_entries=8,
+                            min_prefix_len=8)
+    victim = Filled(pool, [VT], rng, DT, max_chunk=512)
+    vblocks = set(pool.block_table(victim.seqs[0]).tolist())
+    assert pool.prefix_store(victim.seqs[0], np.arange(VT), "m")
+    pool.seq_free(victim.seqs[0])  # only the entry holds its 16 blocks now
+    pre = Filled(pool, [PT], rng, DT, max_chunk=512)
+    forks = [pool.seq_fork(pre.seqs[0], PT) for _ in range(B)]
+    suf = Filled(pool, extra, rng, DT, seqs=forks, max_chunk=512)
+    f = _Joined(pre, suf)
+    for s in f.seqs:
+        pool.reserve_append(s, 1)
+    st = pool.stats()
+    assert st["evicted_entries"] == 1 and st["evicted_blocks"] == len(vblocks), st
+    assert pool.prefix_lookup(np.arange(VT), "m") == (0, None)
+    f.lens = [T + 1 for T in f.lens]
+    t, n = pool.batch_tables(f.seqs, max((T + 63) // 64 for T in f.lens))
+    held = set(t[:, P:][t[:, P:] >= 0].tolist())
+    assert len(held & vblocks) > 0, "the evicted entry's blocks were not reissued"
+    kn = rand_bits(rng, (B, H, 1, D), DT)
+    vn = rand_bits(rng, (B, H, 1, D), DT)
+    q = rand_bits(rng, (B, H * R, 1, D), DT)
+    scale = 1.0 / np.sqrt(D)
+    out = pool.attention_shared_prefix(0, to_dev(q, DT), i32(t[0, :P]), i32(np.ascontiguousarray(t[:, P:])),
+                                       i32(n - 64 * P), int(n.max()) - 64 * P, scale, k_new=to_dev(kn, DT),
+                                       v_new=to_dev(vn, DT))
+    torch.cuda.synchronize()
+    for b in range(B):
+        f.k[0][b] = np.concatenate([f.k[0][b], kn[b]], axis=1)
+        f.v[0][b] = np.concatenate([f.v[0][b], vn[b]], axis=1)
+    ref = oracle_attention(pool, f, 0, q, DT, scale)
+    err = float(np.abs(out.float().cpu().numpy() - ref).max())
+    print(f"max abs error {err:.3e} ({len(held & vblocks)} reissued blocks)", flush=True)
+    assert err <= ATOL, f"max abs error {err:.3e}"
+    check_snapshot(pool.gather(0, i32(t), i32(n), max(f.lens)), f, 0)
+    pool.close()
+
+
+def test_qwen3_30b_a3b_b8_128k_blockwise_equal_keys():
+    """Config 5 at its own batch: 8 sequences of 131072 tokens (the grid and
+    split the benchmark times), x20 outlier channels in V.  Every token of a
+    64-token block has the same K row (its own per (sequence, head, block)),
+    so each block's keys score alike and the output of query row r is
+        sum_j exp(s_rj) Vsum_j / sum_j n_j exp(s_rj)
+    over blocks j (n_j tokens, Vsum_j the sum of its dequantized V rows,
+    s_rj = scale q_r . k_j on the dequantized key), computed in float64 from
+    the oracle's quantization, block sums accumulated while the pool fills.
+    Then one fused decode step (the new token in a block of its own)."""
+    from kvutil import DT as ODT, MODE
+    from oracle import oracle as O
+
+    print("\ncase config qwen3-30b-a3b b8 128k blockwise-equal keys", flush=True)
+    rng = np.random.default_rng(20261215)
+    H, R, D, B, T, C = 4, 8, 128, 8, 131072, 8192
+    NBK = T // 64
+    mode = MODE["affine_g64"]
+    pool = krill_amd.KVPool(1, H, D, B * (NBK + 1) + 8, "affine_g64", DT, free_list_seed=15)
+    seqs = [pool.seq_create() for _ in range(B)]
+    kblk = rand_bits(rng, (B, H, NBK + 1, D), DT)  # the last: the new token's row
+    ch = rng.choice(D, size=max(1, int(round(0.01 * D))), replace=False)  # outlier channels of V
+    vsum = np.zeros((B, H, NBK + 1, D), np.float64)
+    for c0 in range(0, T, C):
+        slots = np.stack([pool.reserve_append(s, C) for s in seqs])
+        kb = np.repeat(kblk[:, :, c0 // 64:(c0 + C) // 64], 64, axis=2)
+        x = rng.standard_normal((B, H, C, D)).astype(np.float32)
+        x[..., ch] *= 20.0
+        vb = O.f32_to_bf16_bits(x)
+        pool.quantize_append(0, to_dev(kb, DT), to_dev(vb, DT), i32(slots))
+        for b in range(B):
+            vq, vs, vz = O.quantize(vb[b], ODT[DT], mode)
+            vd = O.dequant_f64(vq, vs, vz, mode)  # [H, C, D]
+            vsum[b, :, c0 // 64:(c0 + C) // 64] = vd.reshape(H, C // 64, 64, D).sum(axis=2)
+    torch.cuda.synchronize()
+    # the decode step: one more token per sequence, in block NBK
+    for s in seqs:
+        pool.reserve_append(s, 1)
+    kn = np.ascontiguousarray(kblk[:, :, NBK:NBK + 1])
+    x = rng.standard_normal((B, H, 1, D)).astype(np.float32)
+    x[..., ch] *= 20.0
+    vn = O.f32_to_bf16_bits(x)
+    for b in range(B):
+        vq, vs, vz = O.quantize(vn[b], ODT[DT], mode)
+        vsum[b, :, NBK] = O.dequant_f64(vq, vs, vz, mode)[:, 0]
+    q = rand_bits(rng, (B, H * R, 1, D), DT)
+    t, n = pool.batch_tables(seqs, NBK + 1)
+    assert (n == T + 1).all()
+    scale = 1.0 / np.sqrt(D)
+    out = pool.decode_append_attention(0, to_dev(q, DT), to_dev(kn, DT), to_dev(vn, DT), i32(t), i32(n), T + 1,
+                                       scale).float().cpu().numpy()
+    torch.cuda.synchronize()
+    cnt = np.full(NBK + 1, 64.0)
+    cnt[NBK] = 1.0
+    qf = O.bits_to_f32(q, ODT[DT]).astype(np.float64)
+    worst = 0.0
+    for b in range(B):
+        kq, ks, kz = O.quantize(kblk[b], ODT[DT], mode)
+        kd = O.dequant_f64(kq, ks, kz, mode)  # [H, NBK + 1, D]
+        for hk in range(H):
+            for r in range(R):
+                hq = hk * R + r
+                sc = scale * (kd[hk] @ qf[b, hq, 0])
+                w = np.exp(sc - sc.max())
+                ref = (w[:, None] * vsum[b, hk]).sum(axis=0) / (w * cnt).sum()
+                worst = max(worst, float(np.abs(out[b, hq, 0] - ref).max()))
+    print(f"max abs error {worst:.3e}", flush=True)
+    assert worst <= ATOL, f"max abs error {worst:.3e}"
     pool.close()

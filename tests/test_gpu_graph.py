@@ -111,3 +111,87 @@ def test_decode_step_graph_replays_match_eager(R):
         print(f"layer {layer} max abs error {err:.3e}", flush=True)
         assert err <= 2e-3
     pool.close()
+
+
+def test_capture_refuses_queued_copy_on_write_and_replays_after_an_eager_flush():
+    """A sequence forked from another inside a partly filled block: its first
+    append queues a copy-on-write copy of that block.  Capturing a decode step
+    while the copy is queued is refused (the graph would repeat the copy on
+    every replay) and leaves the copy queued; after an eager flush the
+    captured step replays bit for bit like the eager one, the sharer keeps its
+    bytes and the fork holds the sharer's first 70 tokens plus its own."""
+    from krill_amd import _lib as L
+    from kvutil import MODE, check_snapshot, i32
+    from oracle import oracle as O
+
+    print("\ncase graph_cow_refused_then_flushed", flush=True)
+    rng = np.random.default_rng(77)
+    H, D, R, layers = 2, 128, 4, 2
+    pool = krill_amd.KVPool(layers, H, D, 16, "affine_g64", DT, free_list_seed=5)
+    f = Filled(pool, [100], rng, DT, layers=tuple(range(layers)))
+    a = f.seqs[0]
+    fork = pool.seq_fork(a, 70)  # block 1 (tokens 64..99 of a) shared, partly filled for the fork
+    pool.reserve_append(fork, 1)  # position 70: copy-on-write of block 1 queued
+    assert pool.stats()["cow_copies"] == 1 and pool.stats()["pending_copies"] == 1
+    t, n = pool.batch_tables([fork], 2)
+    tab, lens = i32(t), i32(n)
+    q = [to_dev(rand_bits(rng, (1, H * R, 1, D), DT), DT) for _ in range(layers)]
+    kn = [rand_bits(rng, (1, H, 1, D), DT) for _ in range(layers)]
+    vn = [rand_bits(rng, (1, H, 1, D), DT) for _ in range(layers)]
+    k_d = [to_dev(x, DT) for x in kn]
+    v_d = [to_dev(x, DT) for x in vn]
+    scale = 1.0 / np.sqrt(D)
+    ws = torch.empty(max(pool.workspace_size(1, H * R, 1, 71), 1), dtype=torch.uint8, device="cuda")
+    out_g = [torch.empty((1, H * R, 1, D), dtype=torch.float32, device="cuda") for _ in range(layers)]
+    marker = torch.zeros(1, device="cuda")
+    torch.cuda.synchronize()
+
+    cap = torch.cuda.Stream()
+    g0 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g0, stream=cap):
+        marker.add_(1.0)  # the refused capture still records a node
+        with pytest.raises(L.KrillError) as ei:
+            pool.decode_append_attention(0, q[0], k_d[0], v_d[0], tab, lens, 71, scale, ws=ws, out=out_g[0])
+    assert ei.value.code == L.KRILL_E_STATE, str(ei.value)
+    assert pool.stats()["pending_copies"] == 1  # still queued, nothing captured
+    del g0
+
+    pool.flush()  # eager: the copy runs now, outside any graph
+    assert pool.stats()["pending_copies"] == 0
+
+    def step(out):
+        for layer in range(layers):
+            pool.decode_append_attention(layer, q[layer], k_d[layer], v_d[layer], tab, lens, 71, scale, ws=ws,
+                                         out=out[layer])
+
+    out_e = [torch.empty_like(o) for o in out_g]
+    step(out_e)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        step(out_g)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        torch.randn(1 << 16, device="cuda").sum().item()  # eager work between replays
+        for o in out_g:
+            o.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for layer in range(layers):
+            assert torch.equal(out_g[layer], out_e[layer]), (rep, layer)
+
+    mode = MODE["affine_g64"]
+    for layer in range(layers):
+        ta, na = pool.batch_tables([a], 2)
+        check_snapshot(pool.gather(layer, i32(ta), i32(na), 100), f, layer)  # the sharer is unchanged
+        snap = pool.gather(layer, tab, lens, 71)
+        kq, ks, kz, vq, vs, vz = f.expected(layer, 0)
+        nk = O.quantize(kn[layer][0], O.DT_BF16, mode)
+        nv = O.quantize(vn[layer][0], O.DT_BF16, mode)
+        keys = snap["keys"].cpu().numpy()
+        vals = snap["values"].cpu().numpy()
+        np.testing.assert_array_equal(keys[0, :, :70], kq[:, :70])
+        np.testing.assert_array_equal(vals[0, :, :70], vq[:, :70])
+        np.testing.assert_array_equal(keys[0, :, 70:], nk[0])
+        np.testing.assert_array_equal(vals[0, :, 70:], nv[0])
+    pool.close()

@@ -1,8 +1,9 @@
 """GPU: the quantizers' pinned cases through the append kernels.
 
 The groups that pin the affine quantizer in the oracle's own tests (exact
-ties, the sign of the scale and its edge, constant groups, the binary32 scale
-and the division where a reciprocal multiply gives another byte) and ladders
+ties, the sign of the scale and its edge, constant groups, the binary32
+range and scale, and the division where a reciprocal multiply gives another
+byte) and ladders
 of exact half-integer quotients, as the K and V rows of a 64-row launch (the
 block kernel, whose per-element division takes a reciprocal wherever that
 cannot change the byte) and of one-row launches (the row kernel), in both
@@ -42,6 +43,8 @@ def _pinned_groups():
         _group([0.0, 255.0] + [k + 0.5 for k in range(62)], 0.0),
         # (w - 127.5) / -0.5 = 254.5 - k: ties again, with another scale
         _group([0.0, 127.5] + [k / 2 + 0.25 for k in range(62)], 0.0),
+        # the range max - min in binary32 (an fp16 rounding of it changes q0)
+        _group([-3.38671875, 1.591796875, 0.0], 0.0),
     ]
     return np.stack(g)
 

@@ -377,6 +377,38 @@ def test_affine_quantizes_with_the_binary32_scale_and_divides(oracle):
     assert _alt_reciprocal(w)[0][3] == 245
 
 
+def _affine_range16(w):
+    """_affine_exact with the range max - min rounded to fp16 (the input
+    dtype) before the / 255, as an op-by-op fp16 restatement computes it."""
+    mn, mx = min(w), max(w)
+    s = max(_fl32(_fl16(mx - mn) / 255), _EPS32)
+    side = abs(mn) > abs(mx)
+    s = s if side else -s
+    edge = mn if side else mx
+    q0 = _rint(_fl32(edge / s))
+    bias = _Fr(0)
+    if q0 != 0:
+        s = _fl32(edge / q0)
+        bias = edge
+    return [min(max(_rint(_fl32(_fl32(x - bias) / s)), 0), 255) for x in w], s, bias
+
+
+def test_affine_range_is_binary32_not_rounded_to_fp16(oracle):
+    # min -3.38671875, max 1.591796875: max - min = 4.978515625 exactly in
+    # binary32; in fp16 (spacing 2^-8 there) it is the tie 1274.5 ulps and
+    # rounds to even, 4.9765625.  |min| > |max|, so edge = min and
+    # q0 = rint(min / (range / 255)): -173.468.. -> -173 with the binary32
+    # range, -173.536.. -> -174 with the fp16 one.  scale = min / q0 then
+    # differs (0.0195764.. against 0.0194639..), and so do q(max) (254
+    # against 255) and q(0) (173 against 174).
+    bits, w = _group([-3.38671875, 1.591796875, 0.0], 0.0)
+    q, s, b = _check_group(oracle, bits, w)
+    assert (q[0], q[1], q[2]) == (0, 254, 173)
+    assert b == 0xC2C6  # fp16 -3.38671875
+    alt = _affine_range16(w)[0]
+    assert (alt[0], alt[1], alt[2]) == (0, 255, 174)
+
+
 def test_affine_matches_the_exact_restatement_on_random_groups(oracle):
     rng = np.random.default_rng(21)
     x = rng.standard_normal((240, 64)).astype(np.float32) * rng.choice([1e-4, 0.02, 1, 30], (240, 1)).astype(np.float32)
