@@ -114,15 +114,32 @@ __device__ __forceinline__ void ld_stream_words(__amdgpu_buffer_rsrc_t r, int of
 // registers 68.4 us per call; 3 waves with K staged in LDS 75.0 us (the
 // compiler orders every LDS access after the outstanding direct-to-LDS
 // loads, which drains the K prefetch); 2 waves with K in LDS 70.0 us.
+// head_dim 512: each block is split over d_slices = 4 waves of one
+// workgroup, 128 dims each (a 512-byte K row per lane and 32 V tiles would not
+// fit one wave's registers).  Every wave holds its slice's query pairs, K
+// pieces, V tiles and output tiles, exactly the register set of the D = 128
+// kernel; the partial scores of the four slices meet in LDS (one barrier per
+// block), and every wave then runs the same softmax on the same sums.
+template <int D>
+constexpr int d_slices() {
+  return D > 256 ? D / 128 : 1;
+}
 template <int D, int NR>
 constexpr bool pv_on_mfma() {
-  return D <= 128 && NR >= 3;
+  return (D <= 128 && NR >= 3) || D > 256;
 }
 template <int D, int NR>
 constexpr int valu_waves_per_simd() {
+  if constexpr (D > 256) return 2;
   if constexpr (pv_on_mfma<D, NR>()) return D <= 64 ? 3 : 2;
   return D <= 64 || (D == 128 && NR <= 5) ? 3 : 2;
 }
+
+// LDS written and read by the lanes of one wave only: a wave's LDS
+// operations complete in order, so waiting for its outstanding ones (and
+// keeping the compiler from moving memory operations across) orders the
+// writes before the other lanes' reads without a workgroup barrier.
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // The step's new K/V rows of sequence b, head hk: lane l loads the raw
 // elements d = l*E .. l*E+E-1 (E = D/64), the quantizer's lane ownership.
@@ -193,8 +210,10 @@ __device__ __forceinline__ void store_newest(const AttnArgs &a, int hk, int phys
     kd[0] = newrow[d0];
   } else if constexpr (E == 2) {
     *reinterpret_cast<uint16_t *>(kd) = *reinterpret_cast<const uint16_t *>(newrow + d0);
-  } else {
+  } else if constexpr (E == 4) {
     *reinterpret_cast<uint32_t *>(kd) = *reinterpret_cast<const uint32_t *>(newrow + d0);
+  } else {
+    *reinterpret_cast<uint2 *>(kd) = *reinterpret_cast<const uint2 *>(newrow + d0);
   }
 #pragma unroll
   for (int e = 0; e < E; ++e) reg[v_byte(D, t, d0 + e)] = newrow[D + d0 + e];
@@ -212,23 +231,41 @@ __device__ __forceinline__ void store_newest(const AttnArgs &a, int hk, int phys
 
 // VAR: 0 plain; 1 RoPE of the queries (and the fused new K row); 2 sliding
 // window (keys below max(win_start[b], position - window + 1) masked).
+// head_dim 512 (d_slices > 1): workgroups of d_slices waves, wave w the dims
+// [DW w, DW w + DW); the query rows of a KV head in row groups of NR rows
+// (blockIdx.z), each its own flat block order and partial slots.
 template <int D, int NR, int MODE, int VAR>
-__global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_valu(AttnArgs a) {
+__global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>())) void k_attn_valu(AttnArgs a) {
   constexpr bool ROPE = VAR == 1, WIN = VAR == 2;
-  constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
-  constexpr int NP = D / 16;   // 16-byte K pieces per token row
-  constexpr int PPG = NP / G;  // pieces per scale group
-  constexpr int DPL = D / 64;  // V^T rows (d values) per lane
+  constexpr int DS = d_slices<D>();  // waves per workgroup, one per d-slice
+  constexpr int DW = D / DS;         // dims of one wave
+  constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;    // scale groups per token (pool layout)
+  constexpr int GW = MODE == MODE_AFFINE ? DW / 64 : 1;  // the wave's scale groups
+  constexpr int NP = DW / 16;  // the wave's 16-byte K pieces per token row
+  constexpr int PPG = NP / GW; // pieces per scale group
+  constexpr int DPL = D / 64;  // V^T rows (d values) per lane (pool layout)
   // P.V on the matrix cores (16 query rows per MFMA tile, so worth it from 3
   // rows on and while its 2 D / 16 accumulator registers per lane fit) or on
   // the VALU (lane owns D / 64 rows of V^T, fp32 FMAs)
   constexpr bool PVM = pv_on_mfma<D, NR>();
   constexpr bool LOAD_TOGETHER = !PVM && valu_waves_per_simd<D, NR>() >= 3;  // next block's loads in one pass
 
-  __shared__ __attribute__((aligned(16))) float w_lds[NR * G * 64];
-  __shared__ __attribute__((aligned(16))) uint16_t sz_lds[2 * 64];
+  __shared__ __attribute__((aligned(16))) float w_lds_all[DS][NR * GW * 64];
+  __shared__ __attribute__((aligned(16))) uint16_t sz_lds_all[DS][2 * 64];
+  // the slices' partial scores, two buffers (block parity)
+  __shared__ __attribute__((aligned(16))) float sc_lds[DS > 1 ? 2 : 1][DS][DS > 1 ? NR * 64 : 1];
 
-  const int lane = threadIdx.x;
+  const int lane = DS > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
+  const int wsl = DS > 1 ? (int)(threadIdx.x >> 6) : 0;  // this wave's d-slice
+  float *const w_lds = w_lds_all[wsl];
+  uint16_t *const sz_lds = sz_lds_all[wsl];
+  const int p0 = wsl * NP;                             // first K piece of the slice
+  const int g0 = MODE == MODE_AFFINE ? wsl * GW : 0;   // first scale group of the slice
+  const int rg = DS > 1 ? (int)blockIdx.z : 0;         // row group
+  const int r0 = rg * NR;                              // its first query row
+  int sbuf = 0;                                        // partial-score buffer of the block
+  // blocks of a sequence of (view) length len that this row group reads
+  auto nblk = [&](int len) -> int { return DS > 1 ? seq_blocks_rg(a, len, rg) : seq_blocks(a, len); };
   // Every KV head splits its blocks into the same ranges, and workgroups go
   // to the 8 XCDs round-robin by linear id, so with the range index equal to
   // blockIdx.x (the wave count a multiple of 8) range w of every head would
@@ -247,12 +284,12 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   // sequence c0 + j, c0 = the chunk holding the wave's first sequence).
   const int W = a.waves;
   int c0 = 0, lenv = lane < a.B ? seq_len_view<WIN>(a, lane) : 0;
-  int nbv = seq_blocks(a, lenv);
+  int nbv = nblk(lenv);
   int incl = wave_incl_scan(nbv);
   int T = __builtin_amdgcn_readlane(incl, 63);
   for (int cc = 64; cc < a.B; cc += 64) {
     const int bb = cc + lane;
-    T += __builtin_amdgcn_readfirstlane(wave_allsum_int(bb < a.B ? seq_blocks(a, seq_len_view<WIN>(a, bb)) : 0));
+    T += __builtin_amdgcn_readfirstlane(wave_allsum_int(bb < a.B ? nblk(seq_len_view<WIN>(a, bb)) : 0));
   }
   // At most T waves take part, so every participating wave holds at least
   // one block (the merge relies on it: each wave between a sequence's first
@@ -268,7 +305,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       if (c0 > 0) {
         const int bb = c0 + lane;
         lenv = bb < a.B ? seq_len_view<WIN>(a, bb) : 0;
-        nbv = seq_blocks(a, lenv);
+        nbv = nblk(lenv);
         incl = wave_incl_scan(nbv) + carry;
       }
       const unsigned long long m = __ballot(c0 + lane < a.B && incl > i0);
@@ -293,8 +330,8 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   constexpr int E = D / 64;
   uint16_t rk[E], rv[E];
   bool own = false;
-  if (a.k_new) {
-    const int len0 = seq_len(b), nb0 = seq_blocks(a, len0);
+  if (a.k_new) {  // (every row group patches the token in; row group 0 stores it)
+    const int len0 = seq_len(b), nb0 = nblk(len0);
     own = nb0 > 0 && s + nb0 <= iend && ((len0 - 1) >> 6) == nb0 - 1;
     if (own) load_new_rows<D>(a, b, hk, rk, rv);
   }
@@ -309,7 +346,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     const int f = i0 + lane;
     int bs = b, ss = s;
     while (bs < a.B && ss < iend) {
-      const int nbs = seq_blocks(a, seq_len(bs));
+      const int nbs = nblk(seq_len(bs));
       if (f < iend && f >= ss && f < ss + nbs) {
         const int phys = a.tables[(int64_t)bs * a.max_blocks + table_offset<WIN>(a, bs) + (f - ss)];
         tab_ok = (unsigned)phys < (unsigned)a.lv.num_blocks;
@@ -321,7 +358,8 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     if (ss < iend) iend_eff = ss;  // the last sequence ends inside this range
   }
   const uint64_t tab_okm = __ballot(tab_ok);
-  __shared__ __attribute__((aligned(16))) uint8_t newrow[2 * D];
+  __shared__ __attribute__((aligned(16))) uint8_t newrow_all[DS][2 * D];
+  uint8_t *const newrow = newrow_all[wsl];  // the whole quantized row, per wave
   int patch_i = -1, patch_t = 0;  // flat block holding the segment's newest token, its position
   uint32_t pkm[G], pvm[G];
 #pragma unroll
@@ -354,22 +392,26 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   // d = tile_d(dt, m); lane l loads the 16 storage positions 16 (l >> 4) ..
   // +15 of that row (group l >> 5, half (l >> 4) & 1): for a fixed tile the
   // 16 lanes of a quarter read 16 consecutive 16-byte pieces.
-  constexpr int ND = D / 16;
+  constexpr int ND = DW / 16;  // the wave's V^T tiles (matrix-core P.V): tiles dt0 .. dt0 + ND - 1 of the row
+  const int dt0 = wsl * ND;
   auto tile_d = [](int dt, int m) { return DPL * (16 * (dt / DPL) + m) + dt % DPL; };
+  // byte offset of tile gd's 16-byte piece for lane quarter (tg, h), row m
+  auto v_tile_off = [](int gd, int tg, int h, int m) {
+    return v_offset(D) + tg * 32 * D + (((2 * (gd % DPL) + h) * 64 + 16 * (gd / DPL) + m) << 4);
+  };
   const int gl = MODE == MODE_AFFINE ? (DPL * lane) / 64 : 0;  // VALU P.V: scale group of this lane's V rows
   constexpr int NV = PVM ? ND : 4 * DPL;  // 16-byte V pieces per lane
   uint4 kr[NP];
   uint4 vr[NV];
   auto load_k = [&](__amdgpu_buffer_rsrc_t r) {
 #pragma unroll
-    for (int p = 0; p < NP; ++p) kr[p] = ld_stream16(r, k_byte(lane, 16 * p));
+    for (int p = 0; p < NP; ++p) kr[p] = ld_stream16(r, k_byte(lane, 16 * (p0 + p)));
   };
   auto load_v = [&](__amdgpu_buffer_rsrc_t r) {
     if constexpr (PVM) {
       const int tg = lane >> 5, h = (lane >> 4) & 1, m = lane & 15;
 #pragma unroll
-      for (int dt = 0; dt < ND; ++dt)
-        vr[dt] = ld_stream16(r, v_offset(D) + tg * 32 * D + (((2 * (dt % DPL) + h) * 64 + 16 * (dt / DPL) + m) << 4));
+      for (int dt = 0; dt < ND; ++dt) vr[dt] = ld_stream16(r, v_tile_off(dt0 + dt, tg, h, m));
     } else {
       // vr[tg 2 DPL + i]: d = DPL lane + i / 2, half i % 2 of token group tg
 #pragma unroll
@@ -379,33 +421,35 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
           vr[tg * 2 * DPL + i2] = ld_stream16(r, v_offset(D) + tg * 32 * D + ((i2 * 64 + lane) << 4));
     }
   };
-  // this lane's token's (scale, zero) pairs, K and V
-  uint32_t km[G], vm[G];
-  auto load_meta = [&](__amdgpu_buffer_rsrc_t r, uint32_t (&kmo)[G], uint32_t (&vmo)[G]) {
-    ld_stream_words<G>(r, km_offset(D) + lane * 4 * G, kmo);
-    ld_stream_words<G>(r, vm_offset(D, G) + lane * 4 * G, vmo);
+  // this lane's token's (scale, zero) pairs of the slice's groups, K and V
+  uint32_t km[GW], vm[GW];
+  auto load_meta = [&](__amdgpu_buffer_rsrc_t r, uint32_t (&kmo)[GW], uint32_t (&vmo)[GW]) {
+    ld_stream_words<GW>(r, km_offset(D) + (lane * G + g0) * 4, kmo);
+    ld_stream_words<GW>(r, vm_offset(D, G) + (lane * G + g0) * 4, vmo);
   };
 
   // fp16 query pairs: qv[r][c] holds pair 16*c + (lane & 15) of row r, so
   // every 16-lane row carries the whole query (one VGPR per 32 d).  Affine
   // mode also needs the sum of each 64-d group of the fp16 query (pairs
   // 32g .. 32g+31 = columns 2g and 2g+1), reduced inside each 16-lane row.
-  uint32_t qv[NR][D / 32];
-  float qs[NR][G];
+  uint32_t qv[NR][DW / 32];
+  float qs[NR][GW];
   const bool q_bf16 = a.q_dtype == DT_BF16;
   int qlen = 0;  // length of the sequence whose queries are loaded (RoPE positions)
-  auto load_q = [&](int bq) {  // raw pairs of sequence bq
+  int qseq = 0;  // that sequence
+  auto load_q = [&](int bq) {  // raw pairs of sequence bq (the slice's dims)
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      const int hq = hk * a.R + r % a.R, j = r / a.R;
-      const uint32_t *qp = reinterpret_cast<const uint32_t *>(q_row(a, bq, hq, j));
+      const int hq = hk * a.R + (r0 + r) % a.R, j = (r0 + r) / a.R;
+      const uint32_t *qp = reinterpret_cast<const uint32_t *>(q_row(a, bq, hq, j)) + wsl * (DW / 2);
 #pragma unroll
-      for (int c = 0; c < D / 32; ++c) qv[r][c] = qp[16 * c + (lane & 15)];
+      for (int c = 0; c < DW / 32; ++c) qv[r][c] = qp[16 * c + (lane & 15)];
     }
     if constexpr (ROPE) qlen = seq_len(bq);
+    qseq = bq;
   };
   auto finish_q = [&]() {
-    if constexpr (ROPE) {
+    if constexpr (ROPE && DS == 1) {
       // row r (query position j = r / R, token qlen - Lq + j): pair words
       // 16 c + (lane & 15) of the first half turn with their partners
       // D/64 columns on
@@ -423,11 +467,35 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
             rope_pair_words<DT_F16>(qv[r][c], qv[r][c + D / 64], c2, s2);
         }
       }
+    } else if constexpr (ROPE) {
+      // d-slices: the partner of dim e is e +- D/2, in slice wsl ^ (DS/2);
+      // its raw pair words are read here (once per segment) and the pair
+      // turns by cos/sin index e mod D/2
+      const bool low = wsl < DS / 2;
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const int hq = hk * a.R + (r0 + r) % a.R, j = (r0 + r) / a.R;
+        const uint32_t *pp = reinterpret_cast<const uint32_t *>(q_row(a, qseq, hq, j)) + (wsl ^ (DS / 2)) * (DW / 2);
+        const float *crow = rope_row(a, qlen - a.Lq + (r0 + r) / a.R, D);
+#pragma unroll
+        for (int c = 0; c < DW / 32; ++c) {
+          const int i = (wsl % (DS / 2)) * DW + 2 * (16 * c + (lane & 15));
+          const float2 c2 = *reinterpret_cast<const float2 *>(crow + i);
+          const float2 s2 = *reinterpret_cast<const float2 *>(crow + D / 2 + i);
+          const uint32_t part = pp[16 * c + (lane & 15)];
+          uint32_t lo = low ? qv[r][c] : part, hi = low ? part : qv[r][c];
+          if (q_bf16)
+            rope_pair_words<DT_BF16>(lo, hi, c2, s2);
+          else
+            rope_pair_words<DT_F16>(lo, hi, c2, s2);
+          qv[r][c] = low ? lo : hi;
+        }
+      }
     }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
 #pragma unroll
-      for (int c = 0; c < D / 32; ++c) {
+      for (int c = 0; c < DW / 32; ++c) {
         // bf16 pairs are widened to fp32 and rounded to fp16; fp16 pairs pass through
         const uint32_t w = qv[r][c];
         const half2_t hb = half2_t{(_Float16)__builtin_bit_cast(float, w << 16),
@@ -436,13 +504,13 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       }
       if constexpr (MODE == MODE_AFFINE) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const half2_t p0 = u32_as_h2(qv[r][2 * g]), p1 = u32_as_h2(qv[r][2 * g + 1]);
-          qs[r][g] = uniform_f32(row_allsum(((float)p0.x + (float)p0.y) + ((float)p1.x + (float)p1.y)));
+        for (int g = 0; g < GW; ++g) {
+          const half2_t h0 = u32_as_h2(qv[r][2 * g]), h1 = u32_as_h2(qv[r][2 * g + 1]);
+          qs[r][g] = uniform_f32(row_allsum(((float)h0.x + (float)h0.y) + ((float)h1.x + (float)h1.y)));
         }
       } else {
 #pragma unroll
-        for (int g = 0; g < G; ++g) qs[r][g] = 0.0f;
+        for (int g = 0; g < GW; ++g) qs[r][g] = 0.0f;
       }
     }
   };
@@ -460,13 +528,13 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     load_meta(r0, km, vm);
     load_v(r0);
   }
-  if (own) prepare(b, s + seq_blocks(a, seq_len(b)) - 1);
+  if (own) prepare(b, s + nblk(seq_len(b)) - 1);
 #pragma unroll
   for (int p = 0; p < NP; ++p) settle(kr[p]);
 #pragma unroll
   for (int k = 0; k < NV; ++k) settle(vr[k]);
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
+  for (int g = 0; g < GW; ++g) {
     settle(km[g]);
     settle(vm[g]);
   }
@@ -476,28 +544,28 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
   // Issue priority falls as the wave works through its range (3 in its
   // first quarter .. 0 in its last), so a wave that is ahead yields to the
   // other waves of its SIMD and the SIMD's waves finish together.
-  const int nblk = iend_eff - i0;
-  const int pq1 = i0 + (nblk + 3) / 4, pq2 = i0 + (nblk + 1) / 2, pq3 = i0 + (3 * nblk + 3) / 4;
+  const int nrange = iend_eff - i0;
+  const int pq1 = i0 + (nrange + 3) / 4, pq2 = i0 + (nrange + 1) / 2, pq3 = i0 + (3 * nrange + 3) / 4;
   __builtin_amdgcn_s_setprio(3);
   // one pass per sequence segment [max(s, i0), min(s + nb, iend)); the
   // queries of sequence b are ready on entry
   while (true) {
     const int len = seq_len(b);
-    const int e = s + seq_blocks(a, len);
+    const int e = s + nblk(len);
     const int seg_start = i, seg_end = min(e, iend_eff);
 
     int lim[NR];
 #pragma unroll
-    for (int r = 0; r < NR; ++r) lim[r] = key_limit(a, len, r / a.R);
+    for (int r = 0; r < NR; ++r) lim[r] = key_limit(a, len, (r0 + r) / a.R);
     int lo[NR], wst = 0;  // sliding window: first key each row sees, first retained key
     if constexpr (WIN) {
       wst = win_view_start(a, b);
 #pragma unroll
-      for (int r = 0; r < NR; ++r) lo[r] = max(wst, len - a.Lq + r / a.R - a.window + 1);
+      for (int r = 0; r < NR; ++r) lo[r] = max(wst, len - a.Lq + (r0 + r) / a.R - a.window + 1);
     }
 
     // acc[dt]: O^T tile dt, lane l: query row l & 15, d = tile_d(dt, 4 (l >> 4) + j)
-    float m_run[NR], l_part[NR], c_part[NR][G];
+    float m_run[NR], l_part[NR], c_part[NR][GW];
     float4_t acc[PVM ? ND : 1];          // matrix-core P.V
     float accv[PVM ? 1 : NR][DPL];       // VALU P.V: row r, d = DPL lane + e
 #pragma unroll
@@ -505,7 +573,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       m_run[r] = -INFINITY;
       l_part[r] = 0.0f;
 #pragma unroll
-      for (int g = 0; g < G; ++g) c_part[r][g] = 0.0f;
+      for (int g = 0; g < GW; ++g) c_part[r][g] = 0.0f;
     }
 #pragma unroll
     for (int dt = 0; dt < (PVM ? ND : 1); ++dt) acc[dt] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -525,14 +593,14 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       // (scale, zero) words go to lane patch_t
 #pragma unroll
       for (int p = 0; p < NP; ++p) {
-        const uint4 x = *reinterpret_cast<const uint4 *>(newrow + 16 * p);
+        const uint4 x = *reinterpret_cast<const uint4 *>(newrow + 16 * (p0 + p));
         if (lane == patch_t) kr[p] = x;
       }
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
+      for (int g = 0; g < GW; ++g) {
         if (lane == patch_t) {
-          km[g] = pkm[g];
-          vm[g] = pvm[g];
+          km[g] = pkm[g0 + g];
+          vm[g] = pvm[g0 + g];
         }
       }
     }
@@ -540,11 +608,11 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     // ---- scores: this lane's token against every query row; the query
     // pair of each dot comes from lane (pair & 15) of the lane's 16-lane row
     // through the DPP broadcast of v_dot2c.
-    float accg[NR][G];
+    float accg[NR][GW];
 #pragma unroll
     for (int r = 0; r < NR; ++r)
 #pragma unroll
-      for (int g = 0; g < G; ++g) accg[r][g] = 0.0f;
+      for (int g = 0; g < GW; ++g) accg[r][g] = 0.0f;
     half2_t ks2 = m1024, kz2 = m1024;
     if constexpr (MODE == MODE_REF) {
       const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)(km[0] & 0xffffu));
@@ -570,7 +638,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
         for (int i = 0; i < 8; ++i) kp[i] = kp[i] + m1152;  // u - 128, exact
       }
       // the piece is converted: its register takes the next block's piece
-      if constexpr (!LOAD_TOGETHER) kr[p] = ld_stream16(nrs, k_byte(lane, 16 * p));
+      if constexpr (!LOAD_TOGETHER) kr[p] = ld_stream16(nrs, k_byte(lane, 16 * (p0 + p)));
       const int g = MODE == MODE_AFFINE ? p / PPG : 0;
       // the last piece of a scale group finishes accg[.][g]
       const bool tail = MODE == MODE_AFFINE ? (p + 1) % PPG == 0 : p == NP - 1;
@@ -591,7 +659,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     }
     // The K registers are consumed: the next block's K bytes and metadata
     // are fetched now, in flight through the softmax and P.V.
-    uint32_t km_next[G], vm_next[G];
+    uint32_t km_next[GW], vm_next[GW];
     if constexpr (!LOAD_TOGETHER) load_meta(nrs, km_next, vm_next);
 
     float s[NR];
@@ -601,7 +669,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       if constexpr (MODE == MODE_AFFINE) {
         v = 0.0f;
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
+        for (int g = 0; g < GW; ++g) {
           const float kss = f16_bits_to_f32((uint16_t)(km[g] & 0xffffu));
           const float kzz = f16_bits_to_f32((uint16_t)(km[g] >> 16));
           v += kss * accg[r][g] + (kzz + 128.0f * kss) * qs[r][g];
@@ -609,9 +677,28 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       } else {
         v = accg[r][0];
       }
-      bool seen = tbase + lane < lim[r];
-      if constexpr (WIN) seen = seen && tbase + lane >= lo[r];
-      s[r] = seen ? v * a.scale_log2 : -INFINITY;
+      if constexpr (DS > 1) {
+        sc_lds[sbuf][wsl][r * 64 + lane] = v;  // this slice's part of the score
+      } else {
+        bool seen = tbase + lane < lim[r];
+        if constexpr (WIN) seen = seen && tbase + lane >= lo[r];
+        s[r] = seen ? v * a.scale_log2 : -INFINITY;
+      }
+    }
+    if constexpr (DS > 1) {
+      // every slice's part in: the whole score, summed in slice order (the
+      // same sum in every wave)
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        float v = sc_lds[sbuf][0][r * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < DS; ++w) v += sc_lds[sbuf][w][r * 64 + lane];
+        bool seen = tbase + lane < lim[r];
+        if constexpr (WIN) seen = seen && tbase + lane >= lo[r];
+        s[r] = seen ? v * a.scale_log2 : -INFINITY;
+      }
+      sbuf ^= 1;
     }
 
     // ---- online softmax with a lazily raised running max
@@ -632,7 +719,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
         m_run[r] = uniform_f32(mn);
         l_part[r] *= al;
 #pragma unroll
-        for (int g = 0; g < G; ++g) c_part[r][g] *= al;
+        for (int g = 0; g < GW; ++g) c_part[r][g] *= al;
         aln = (lane & 15) == r ? al : aln;
         if constexpr (!PVM) {
 #pragma unroll
@@ -659,12 +746,12 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     // the group's value range in the output when a few keys hold the weight.
     if constexpr (MODE == MODE_AFFINE) {
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
+      for (int g = 0; g < GW; ++g) {
         const float vsf = valid ? f16_bits_to_f32((uint16_t)(vm[g] & 0xffffu)) : 0.0f;
         const float vzf = valid ? f16_bits_to_f32((uint16_t)(vm[g] >> 16)) : 0.0f;
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-          w_lds[(r * G + g) * 64 + pos] = pr[r] * vsf;
+          w_lds[(r * GW + g) * 64 + pos] = pr[r] * vsf;
           // the zero point, plus on the matrix cores the 128 taken off the V
           // bytes: p (z + 128 s); the VALU takes the bytes as they are: p z
           c_part[r][g] = fmaf(pr[r], PVM ? fmaf(128.0f, vsf, vzf) : vzf, c_part[r][g]);
@@ -676,7 +763,10 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       sz_lds[pos] = valid ? (uint16_t)(vm[0] & 0xffffu) : (uint16_t)0;
       sz_lds[64 + pos] = valid ? (uint16_t)(vm[0] >> 16) : (uint16_t)0;
     }
-    __syncthreads();
+    if constexpr (DS > 1)
+      wave_lds_sync();  // each wave has its own weights
+    else
+      __syncthreads();
     if constexpr (PVM) {
     if (i == patch_i) {
       // the newest token's V bytes: storage position p of group tg is byte
@@ -687,7 +777,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       const bool mine = (lane >> 4) == 2 * tg + (p >> 4);
 #pragma unroll
       for (int dt = 0; dt < ND; ++dt) {
-        const uint32_t nv = (uint32_t)newrow[D + tile_d(dt, lane & 15)] << sh;
+        const uint32_t nv = (uint32_t)newrow[D + tile_d(dt0 + dt, lane & 15)] << sh;
         uint4 &x = vr[dt];
         if (mine) {
           if ((bp >> 2) == 0) x.x = (x.x & keep) | nv;
@@ -732,13 +822,44 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     // row l & 15 (rows beyond NR repeat the last one; their outputs are never
     // read), each binary32 weight as an fp16 high part and the fp16 rounding
     // of its remainder (about 2^-22 relative left), two MFMAs per tile.
-    {
+    if constexpr (DS > 1 && MODE == MODE_AFFINE) {
+      // head_dim 512: a tile's 16 rows d = 8 (16 k + m) + dt % 8 span two
+      // scale groups of the slice (rows m < 8 the first, m >= 8 the
+      // second), so each tile runs once per group with the other group's
+      // rows zeroed in A and that group's weights in B
+      const int nb = (lane & 15) < NR ? (lane & 15) : NR - 1, q = lane >> 4;
+      const bool upper = (lane & 15) >= 8;
+      const half8_t zero8 = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int sh = 0; sh < 2; ++sh) {
+        half8_t bh[2], bl[2];
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          const float *wp = w_lds + (nb * GW + g) * 64 + 16 * q + 8 * sh;
+          split_hi_lo(*reinterpret_cast<const float4 *>(wp), *reinterpret_cast<const float4 *>(wp + 4), bh[g], bl[g]);
+        }
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt) {
+          const uint4 v = vr[dt];
+          const half8_t av = bytes8_centred(sh ? uint2{v.z, v.w} : uint2{v.x, v.y});
+          const half8_t a0 = upper ? zero8 : av, a1 = upper ? av : zero8;
+          acc[dt] = mfma16x16x32(a0, bh[0], acc[dt]);
+          acc[dt] = mfma16x16x32(a0, bl[0], acc[dt]);
+          acc[dt] = mfma16x16x32(a1, bh[1], acc[dt]);
+          acc[dt] = mfma16x16x32(a1, bl[1], acc[dt]);
+        }
+      }
+      // the tiles are consumed: their registers take the next block's
+      const int tg = lane >> 5, h = (lane >> 4) & 1, m = lane & 15;
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) vr[dt] = ld_stream16(nrs, v_tile_off(dt0 + dt, tg, h, m));
+    } else {
       const int nb = (lane & 15) < NR ? (lane & 15) : NR - 1, q = lane >> 4;
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
+      for (int g = 0; g < GW; ++g) {
 #pragma unroll
         for (int sh = 0; sh < 2; ++sh) {
-          const float *wp = w_lds + (nb * G + g) * 64 + 16 * q + 8 * sh;
+          const float *wp = w_lds + (nb * GW + g) * 64 + 16 * q + 8 * sh;
           half8_t bh, bl;
           split_hi_lo(*reinterpret_cast<const float4 *>(wp), *reinterpret_cast<const float4 *>(wp + 4), bh, bl);
           uint4 sc = {0u, 0u, 0u, 0u}, zc = {0u, 0u, 0u, 0u};
@@ -747,8 +868,8 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
             zc = *reinterpret_cast<const uint4 *>(sz_lds + 64 + 16 * q + 8 * sh);
           }
 #pragma unroll
-          for (int t = 0; t < ND / G; ++t) {
-            const int dt = g * (ND / G) + t;
+          for (int t = 0; t < ND / GW; ++t) {
+            const int dt = g * (ND / GW) + t;
             const uint4 v = vr[dt];
             const uint2 w8 = sh ? uint2{v.z, v.w} : uint2{v.x, v.y};
             half8_t av;
@@ -764,9 +885,9 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
         {
           const int tg = lane >> 5, h = (lane >> 4) & 1, m = lane & 15;
 #pragma unroll
-          for (int t = 0; t < ND / G; ++t) {
-            const int dt = g * (ND / G) + t;
-            vr[dt] = ld_stream16(nrs, v_offset(D) + tg * 32 * D + (((2 * (dt % DPL) + h) * 64 + 16 * (dt / DPL) + m) << 4));
+          for (int t = 0; t < ND / GW; ++t) {
+            const int dt = g * (ND / GW) + t;
+            vr[dt] = ld_stream16(nrs, v_tile_off(dt0 + dt, tg, h, m));
           }
         }
       }
@@ -835,24 +956,30 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     if constexpr (!PVM) load_v(nrs);
     if constexpr (LOAD_TOGETHER) load_meta(nrs, km_next, vm_next);
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+    for (int g = 0; g < GW; ++g) {
       km[g] = km_next[g];
       vm[g] = vm_next[g];
     }
-    __syncthreads();
+    if constexpr (DS > 1)
+      wave_lds_sync();
+    else
+      __syncthreads();
   }
 
     // the segment's newest token goes to the pool with the segment's output
-    if (patch_i >= 0) store_newest<D, MODE>(a, hk, __builtin_amdgcn_readlane(tab, patch_i - i0), patch_t, newrow, pkm, pvm);
+    // (the whole row, by the first slice's wave of row group 0; the other
+    // row groups read the token from their registers, never from memory)
+    if (patch_i >= 0 && wsl == 0 && rg == 0)
+      store_newest<D, MODE>(a, hk, __builtin_amdgcn_readlane(tab, patch_i - i0), patch_t, newrow, pkm, pvm);
 
     if constexpr (PVM) {
     // ---- end of the segment: the whole sequence in this wave -> output;
     // otherwise a partial in slot hk * (waves + B) + wave + b.  Lane l holds
     // query row n = l & 15 (rows n >= NR are padding).
     const int n = lane & 15, q4 = 4 * (lane >> 4);
-    float lsum_n = 0.0f, m_n = 0.0f, cg[G];
+    float lsum_n = 0.0f, m_n = 0.0f, cg[GW];
 #pragma unroll
-    for (int g = 0; g < G; ++g) cg[g] = 0.0f;
+    for (int g = 0; g < GW; ++g) cg[g] = 0.0f;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       const float ls = uniform_f32(wave_allsum(l_part[r]));
@@ -860,21 +987,30 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       m_n = n == r ? m_run[r] : m_n;
       if constexpr (MODE == MODE_AFFINE) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
+        for (int g = 0; g < GW; ++g) {
           const float c = wave_allsum(c_part[r][g]);
           cg[g] = n == r ? c : cg[g];
         }
       }
     }
+    if constexpr (DS > 1 && MODE == MODE_AFFINE) {
+      // head_dim 512: output rows m = q4 + j < 8 are the slice's first group
+      const float cgl = lane >= 32 ? cg[1] : cg[0];
 #pragma unroll
-    for (int dt = 0; dt < ND; ++dt) acc[dt] += cg[dt / (ND / G)];
+      for (int dt = 0; dt < ND; ++dt) acc[dt] += cgl;
+    } else {
+#pragma unroll
+      for (int dt = 0; dt < ND; ++dt) acc[dt] += cg[dt / (ND / GW)];
+    }
     // The lane's values of tiles DPL k .. DPL k + DPL - 1 form one run of
-    // 4 DPL consecutive d: d = DPL (16 k + q4 + j) + e for j < 4, e < DPL.
+    // 4 DPL consecutive d: d = DPL (16 k + q4 + j) + e for j < 4, e < DPL
+    // (k counted over the whole row: the slice's tiles start at dt0).
     if (n < NR) {
       const bool whole = !a.partial_only && s >= i0 && e <= iend;
       const float mul = !whole ? 1.0f : lsum_n > 0.0f ? 1.0f / lsum_n : 0.0f;
-      const int64_t pi = ((int64_t)hk * (a.waves + a.B) + wv + b) * NR + n;
-      const int64_t ob = whole ? out_row_base(a, b, hk, n, D) : pi * D;
+      const int64_t hslot = DS > 1 ? (int64_t)hk * a.row_groups + rg : (int64_t)hk;
+      const int64_t pi = (hslot * (a.waves + a.B) + wv + b) * NR + n;
+      const int64_t ob = whole ? out_row_base(a, b, hk, r0 + n, D) : pi * D;
 #pragma unroll
       for (int k = 0; k < ND / DPL; ++k) {
         float run[4 * DPL];
@@ -882,9 +1018,10 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
         for (int j2 = 0; j2 < 4; ++j2)
 #pragma unroll
           for (int e2 = 0; e2 < DPL; ++e2) run[DPL * j2 + e2] = acc[DPL * k + e2][j2] * mul;
-        store_run<4 * DPL>(whole ? a.out : (void *)a.ws_o, ob + DPL * (16 * k + q4), run, whole ? a.out_dtype : DT_F32);
+        store_run<4 * DPL>(whole ? a.out : (void *)a.ws_o, ob + DPL * (16 * (dt0 / DPL + k) + q4), run,
+                           whole ? a.out_dtype : DT_F32);
       }
-      if (!whole && lane < 16) reinterpret_cast<float2 *>(a.ws_ml)[pi] = float2{m_n, lsum_n};
+      if (!whole && lane < 16 && wsl == 0) reinterpret_cast<float2 *>(a.ws_ml)[pi] = float2{m_n, lsum_n};
     }
     } else {
     // ---- end of the segment: the whole sequence in this wave -> output;
@@ -896,7 +1033,7 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
       float cg = 0.0f;
       if constexpr (MODE == MODE_AFFINE) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
+        for (int g = 0; g < GW; ++g) {
           const float c = wave_allsum(c_part[r][g]);
           cg = g == gl ? c : cg;
         }
@@ -927,12 +1064,12 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
     // next sequence with blocks (empty ones get zeros from the merge)
     ++b;
     s = e;
-    while (b < a.B && seq_blocks(a, seq_len(b)) == 0) ++b;
+    while (b < a.B && nblk(seq_len(b)) == 0) ++b;
     if (b >= a.B) break;
     load_q(b);
     patch_i = -1;
     if (a.k_new) {
-      const int len2 = seq_len(b), nb2 = seq_blocks(a, len2);
+      const int len2 = seq_len(b), nb2 = nblk(len2);
       if (s + nb2 <= iend && ((len2 - 1) >> 6) == nb2 - 1) {
         load_new_rows<D>(a, b, hk, rk, rv);
         prepare(b, s + nb2 - 1);
@@ -944,12 +1081,13 @@ __global__ __launch_bounds__(64, (valu_waves_per_simd<D, NR>())) void k_attn_val
 
 template <int D, int MODE, int NR>
 static void launch_one(const AttnArgs &args, int B, dim3 grid, hipStream_t st) {
+  const dim3 block(64 * d_slices<D>());
   if (args.rope_cs)
-    k_attn_valu<D, NR, MODE, 1><<<grid, dim3(64), 0, st>>>(args);
+    k_attn_valu<D, NR, MODE, 1><<<grid, block, 0, st>>>(args);
   else if (args.window > 0)
-    k_attn_valu<D, NR, MODE, 2><<<grid, dim3(64), 0, st>>>(args);
+    k_attn_valu<D, NR, MODE, 2><<<grid, block, 0, st>>>(args);
   else
-    k_attn_valu<D, NR, MODE, 0><<<grid, dim3(64), 0, st>>>(args);
+    k_attn_valu<D, NR, MODE, 0><<<grid, block, 0, st>>>(args);
 }
 
 template <int D, int MODE>
@@ -976,8 +1114,11 @@ static int32_t occupancy_nr(int NR) {
 #define KRILL_OCC(N)                                                                                        \
   case N:                                                                                                   \
     e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(&k_attn_valu<D, N, MODE, 0>), \
-                                                     64, 0);                                                \
-    if (e != hipSuccess || n <= 0) n = 4 * valu_waves_per_simd<D, N>();                                    \
+                                                     64 * d_slices<D>(), 0);                                \
+    if (e != hipSuccess || n <= 0)                                                                          \
+      n = 4 * valu_waves_per_simd<D, N>();                                                                  \
+    else                                                                                                    \
+      n *= d_slices<D>();                                                                                   \
     break;
     KRILL_OCC(1) KRILL_OCC(2) KRILL_OCC(3) KRILL_OCC(4) KRILL_OCC(5) KRILL_OCC(6) KRILL_OCC(7) KRILL_OCC(8)
 #undef KRILL_OCC
@@ -987,22 +1128,25 @@ static int32_t occupancy_nr(int NR) {
   return n;
 }
 
+// Resident waves per CU (for head_dim 512: workgroups x 4 waves).
 int32_t valu_waves_per_cu(const PoolGeometry &g, int32_t NR) {
-  const int dsel = g.D == 64 ? 0 : g.D == 128 ? 1 : 2;
+  const int dsel = g.D == 64 ? 0 : g.D == 128 ? 1 : g.D == 256 ? 2 : 3;
   if (NR < 1 || NR > 8) return 8;
   if (g.num_cus <= 0) {  // host-only pool: the design point
-    static const int est[3][9] = {{0, 12, 12, 12, 12, 12, 12, 12, 12},
+    static const int est[4][9] = {{0, 12, 12, 12, 12, 12, 12, 12, 12},
                                   {0, 12, 12, 12, 12, 12, 8, 8, 8},
+                                  {0, 8, 8, 8, 8, 8, 8, 8, 8},
                                   {0, 8, 8, 8, 8, 8, 8, 8, 8}};
     return est[dsel][NR];
   }
-  static int cache[2][3][9] = {};  // [mode][D][NR], filled on first use per process
+  static int cache[2][4][9] = {};  // [mode][D][NR], filled on first use per process
   int &c = cache[g.mode == MODE_AFFINE][dsel][NR];
   if (c == 0) {
     int n = 8;
     if (g.D == 64) n = g.mode == MODE_REF ? occupancy_nr<64, MODE_REF>(NR) : occupancy_nr<64, MODE_AFFINE>(NR);
     else if (g.D == 128) n = g.mode == MODE_REF ? occupancy_nr<128, MODE_REF>(NR) : occupancy_nr<128, MODE_AFFINE>(NR);
-    else n = g.mode == MODE_REF ? occupancy_nr<256, MODE_REF>(NR) : occupancy_nr<256, MODE_AFFINE>(NR);
+    else if (g.D == 256) n = g.mode == MODE_REF ? occupancy_nr<256, MODE_REF>(NR) : occupancy_nr<256, MODE_AFFINE>(NR);
+    else n = g.mode == MODE_REF ? occupancy_nr<512, MODE_REF>(NR) : occupancy_nr<512, MODE_AFFINE>(NR);
     c = n;
   }
   return c;
@@ -1012,8 +1156,11 @@ hipError_t launch_attn_valu(const PoolGeometry &g, int32_t layer, const AttnLaun
                             hipStream_t st) {
   // one VGPR of block-table entries per wave
   if (p.waves < 1 || (int64_t)p.waves * 64 < (int64_t)a.B * p.nb_cap) return hipErrorInvalidValue;
+  // rows beyond 8 per KV head run in row groups on head_dim 512 only
+  if (p.row_groups < 1 || p.row_groups * p.rows_per_group != p.NR || (g.D <= 256 && p.row_groups != 1))
+    return hipErrorInvalidValue;
   const AttnArgs args = make_attn_args(g, layer, a, p);
-  const dim3 grid((unsigned)p.waves, (unsigned)g.Hkv);
+  const dim3 grid((unsigned)p.waves, (unsigned)g.Hkv, (unsigned)p.row_groups);
   switch (g.D) {
     case 64:
       return g.mode == MODE_REF ? launch_valu_nr<64, MODE_REF>(args, p.NR, a.B, grid, st)
@@ -1024,6 +1171,9 @@ hipError_t launch_attn_valu(const PoolGeometry &g, int32_t layer, const AttnLaun
     case 256:
       return g.mode == MODE_REF ? launch_valu_nr<256, MODE_REF>(args, p.NR, a.B, grid, st)
                                 : launch_valu_nr<256, MODE_AFFINE>(args, p.NR, a.B, grid, st);
+    case 512:
+      return g.mode == MODE_REF ? launch_valu_nr<512, MODE_REF>(args, p.rows_per_group, a.B, grid, st)
+                                : launch_valu_nr<512, MODE_AFFINE>(args, p.rows_per_group, a.B, grid, st);
     default:
       return hipErrorInvalidValue;
   }

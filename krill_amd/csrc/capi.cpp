@@ -36,7 +36,7 @@ hipError_t launch_copy_pairs(const PoolGeometry &g, const CopyPair *pairs, int32
 
 namespace {
 
-constexpr int32_t kMaxHeadDim = 256;
+constexpr int32_t kMaxHeadDim = 512;
 
 int32_t hip_fail(hipError_t e, const char *what) {
   return fail(KRILL_E_HIP, "%s: %s (%d)", what, hipGetErrorString(e), static_cast<int>(e));
@@ -122,8 +122,8 @@ int32_t krill_pool_create(const krill_pool_desc *desc, krill_stream_t stream, kr
     const krill_pool_desc &d = *desc;
     if (d.num_layers < 1 || d.num_kv_heads < 1 || d.num_blocks < 1)
       return fail(KRILL_E_INVAL, "num_layers, num_kv_heads and num_blocks must be >= 1");
-    if (d.head_dim != 64 && d.head_dim != 128 && d.head_dim != kMaxHeadDim)
-      return fail(KRILL_E_UNSUPPORTED, "head_dim %d (supported: 64, 128, 256)", d.head_dim);
+    if (d.head_dim != 64 && d.head_dim != 128 && d.head_dim != 256 && d.head_dim != kMaxHeadDim)
+      return fail(KRILL_E_UNSUPPORTED, "head_dim %d (supported: 64, 128, 256, 512)", d.head_dim);
     if (d.block_tokens != 64) return fail(KRILL_E_UNSUPPORTED, "block_tokens %d (supported: 64)", d.block_tokens);
     if (d.quant_mode != KRILL_QUANT_REF_ROW && d.quant_mode != KRILL_QUANT_AFFINE_G64)
       return fail(KRILL_E_INVAL, "quant_mode %d", d.quant_mode);

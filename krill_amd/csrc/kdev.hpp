@@ -447,9 +447,15 @@ __device__ __forceinline__ void store_row(uint8_t *reg, int kv, int t, int lane,
       dst[0] = qb[0];
     } else if constexpr (E == 2) {
       *reinterpret_cast<uint16_t *>(dst) = (uint16_t)(qb[0] | (qb[1] << 8));
-    } else {
+    } else if constexpr (E == 4) {
       *reinterpret_cast<uint32_t *>(dst) =
           (uint32_t)qb[0] | ((uint32_t)qb[1] << 8) | ((uint32_t)qb[2] << 16) | ((uint32_t)qb[3] << 24);
+    } else {
+      static_assert(E == 8, "head_dim 64, 128, 256 or 512");
+      // d0 = 8 lane: the 8 bytes sit in one 16-byte K chunk
+      *reinterpret_cast<uint2 *>(dst) =
+          uint2{(uint32_t)qb[0] | ((uint32_t)qb[1] << 8) | ((uint32_t)qb[2] << 16) | ((uint32_t)qb[3] << 24),
+                (uint32_t)qb[4] | ((uint32_t)qb[5] << 8) | ((uint32_t)qb[6] << 16) | ((uint32_t)qb[7] << 24)};
     }
   } else {
 #pragma unroll

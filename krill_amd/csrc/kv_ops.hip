@@ -881,6 +881,10 @@ __global__ __launch_bounds__(64) void k_attn_merge_cascade(AttnArgs ap, AttnArgs
       constexpr int D = 256;                      \
       __VA_ARGS__;                                \
     } break;                                      \
+    case 512: {                                   \
+      constexpr int D = 512;                      \
+      __VA_ARGS__;                                \
+    } break;                                      \
     default:                                      \
       return hipErrorInvalidValue;                \
   }
@@ -895,12 +899,15 @@ static hipError_t launch_append_rope(const PoolGeometry &g, int32_t layer, const
   if (waves == 0) return hipSuccess;
   const LayerView lv = layer_view(g, layer);
   const uint16_t *kk = static_cast<const uint16_t *>(k), *vv = static_cast<const uint16_t *>(v);
-  if (L >= 32 && B <= 65535 && g.Hkv <= 65535 && !(g.mode == MODE_REF && g.D > 128)) {
+  if (L >= 32 && B <= 65535 && g.Hkv <= 65535 && !(g.mode == MODE_REF && g.D > 128) && g.D <= 256) {
     // chunks of 64 rows staged per block in LDS (the row mode at D = 256 --
-    // a 256-element group per thread -- stays on the per-row kernel)
+    // a 256-element group per thread -- stays on the per-row kernel, and so
+    // does D = 512, whose two V block images alone would take 64 KB of LDS)
     const dim3 grid((unsigned)((L + 63) / 64), (unsigned)g.Hkv, (unsigned)B), block(256);
     KRILL_DISPATCH_D(g.D, {
-      if (g.mode == MODE_REF) {
+      if constexpr (D > 256) {
+        return hipErrorInvalidValue;
+      } else if (g.mode == MODE_REF) {
         if (g.in_dtype == DT_BF16)
           k_quantize_append_blocks<D, MODE_REF, DT_BF16, ROPE><<<grid, block, 0, st>>>(lv, kk, vv, sb, sh, sl, slots, L, rope);
         else
@@ -1033,8 +1040,14 @@ int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq,
   const int32_t R = Hq / g.Hkv;
   AttnPlan p{};
   p.NR = R * Lq;
-  p.use_mfma = path == 2 || (path == 0 && p.NR > 8);
-  if (!p.use_mfma && p.NR > 8) return -2;
+  // head_dim 512: the VALU kernel with each block split over four waves of
+  // 128 dims (the MFMA kernel's LDS ring would hold 70 KB per stage), the
+  // query rows in groups of at most 8 (the largest divisor of NR up to 8),
+  // one grid row group each
+  const bool dsplit = g.D > 256;
+  if (dsplit && path == 2) return -2;
+  p.use_mfma = !dsplit && (path == 2 || (path == 0 && p.NR > 8));
+  if (!p.use_mfma && !dsplit && p.NR > 8) return -2;
   const int32_t nb_max = std::max(1, (max_seq_len + 63) / 64);
   const int64_t tmax = (int64_t)B * nb_max;
   const int64_t cus = g.num_cus > 0 ? g.num_cus : 256;
@@ -1072,6 +1085,14 @@ int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq,
       p.row_groups = (p.NR + 15) / 16;
       p.group_waves = p.row_groups >= 3 ? 4 : p.row_groups;
     }
+  } else if (dsplit) {
+    int32_t rpg = std::min<int32_t>(8, p.NR);
+    while (p.NR % rpg != 0) --rpg;
+    p.nrt = 0;
+    p.rows_per_group = rpg;
+    p.row_groups = p.NR / rpg;
+    p.group_waves = 1;
+    p.token_split = 1;
   } else {
     p.nrt = 0;
     p.rows_per_group = p.NR;
@@ -1094,6 +1115,10 @@ int32_t plan_attention(const PoolGeometry &g, int32_t B, int32_t Hq, int32_t Lq,
     const int64_t groups = (p.row_groups + p.group_waves - 1) / p.group_waves;
     waves = std::max<int64_t>(1, cus * mfma_groups_per_cu(g, p.nrt, p.group_waves, p.token_split) /
                                      ((int64_t)g.Hkv * groups));
+  } else if (dsplit) {
+    // workgroups of 4 waves (one per 128-dim slice)
+    const int64_t wg_per_cu = std::max<int32_t>(1, valu_waves_per_cu(g, p.rows_per_group) / (g.D / 128));
+    waves = std::max<int64_t>(1, cus * wg_per_cu / ((int64_t)g.Hkv * p.row_groups));
   } else {
     waves = std::max<int64_t>(1, cus * valu_waves_per_cu(g, p.NR) / g.Hkv);
   }

@@ -84,7 +84,7 @@ def _close(ctx):
 
 @pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-@pytest.mark.parametrize("D,R", [(128, 5), (64, 4), (256, 2)])
+@pytest.mark.parametrize("D,R", [(128, 5), (64, 4), (256, 2), (512, 8)])
 def test_fused_step_matches_two_calls(mode, dt, D, R):
     # new tokens at the last slot of a block (63, 127), the first slot of a
     # new block (64, 200 -> 201 stays inside), a sequence's first token (0)
@@ -139,11 +139,13 @@ def test_fused_step_qwen3_14b_shape_against_oracle():
     _close(ctx)
 
 
-@pytest.mark.parametrize("D,R,dt", [(128, 5, "bf16"), (64, 4, "f16"), (256, 2, "bf16"), (128, 16, "bf16")])
+@pytest.mark.parametrize("D,R,dt", [(128, 5, "bf16"), (64, 4, "f16"), (256, 2, "bf16"), (128, 16, "bf16"),
+                                    (512, 8, "bf16"), (512, 16, "f16")])
 def test_fused_rope_step_matches_rope_append_and_rotated_queries(D, R, dt):
     """krill_decode_append_attention_rope against krill_quantize_append_rope at
     the reserved slots + decode attention on queries rotated by the oracle
-    (R = 16: more than 8 rows per KV head, the MFMA path)."""
+    (R = 16: more than 8 rows per KV head, the MFMA path; at D = 512 two
+    row groups of 8 on the d-sliced kernel, the first writing the token)."""
     from krill_amd.pool import rope_table
     from oracle import oracle as O
 

@@ -29,7 +29,7 @@ def gpu(t):
 
 @pytest.mark.parametrize("mode", ["ref_row", "affine_g64"])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("D", [64, 128, 256, 512])
 def test_quantize_append_bit_exact(mode, dt, D):
     print(f"\ncase quantize_append mode={mode} dt={dt} D={D}", flush=True)
     rng = np.random.default_rng(100 + D)
@@ -42,7 +42,7 @@ def test_quantize_append_bit_exact(mode, dt, D):
 
 
 @pytest.mark.parametrize("mode", ["ref_row", "affine_g64"])
-@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("D", [64, 128, 256, 512])
 def test_bulk_append_block_staging_bit_exact(mode, D):
     # appends of up to 200 rows (the 64-row chunks staged per block in LDS):
     # sequences starting at block edges and inside blocks, chunks straddling
@@ -173,7 +173,7 @@ def _attn_case(mode, D, H, R, lens, Lq=1, dt="bf16", split_blocks=0, path=0, out
 
 
 @pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
-@pytest.mark.parametrize("D,R", [(128, 5), (64, 4), (128, 8), (256, 2), (128, 1)])
+@pytest.mark.parametrize("D,R", [(128, 5), (64, 4), (128, 8), (256, 2), (128, 1), (512, 8), (512, 1)])
 def test_decode_attention_valu(mode, D, R):
     print(f"\ncase decode_valu mode={mode} D={D} R={R}", flush=True)
     got, ref = _attn_case(mode, D, 2, R, [1, 63, 64, 65, 300, 700], seed=D + R)

@@ -45,7 +45,7 @@ def _case(mode, dt, D, L, seed, H=2, B=3, max_pos=5000, bad_row=None):
 
 
 @pytest.mark.parametrize("mode", ["ref_row", "affine_g64"])
-@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("D", [64, 128, 256, 512])
 @pytest.mark.parametrize("L", [1, 5, 70])
 def test_rope_append_bit_exact(mode, D, L):
     dt = "bf16"

@@ -114,7 +114,7 @@ def _pools(mode, H, D, blocks, window, seed, dt=DTS):
 
 
 @pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
-@pytest.mark.parametrize("D,R", [(128, 4), (64, 2), (256, 2)])
+@pytest.mark.parametrize("D,R", [(128, 4), (64, 2), (256, 2), (512, 8)])
 def test_window_decode_parity(mode, D, R):
     print(f"\ncase window_decode mode={mode} D={D} R={R}", flush=True)
     W, H, steps = 100, 2, 24
