@@ -117,7 +117,7 @@ class Philox:
 # five are the reference's benchmark configurations in their order
 CONFIG_INDEX = {"llama-3.2-1b-b1": 0, "qwen3-14b-b32": 1, "llama-3-8b-shared-prefix-b64": 2,
                 "llama-3-8b-verify-b16": 3, "qwen3-30b-a3b-b8-128k": 4, "qwen3-14b-prefill-b8-c512": 5,
-                "qwen3-14b-b32-continuous": 6, "gemma3-12b-sliding-b32": 7}
+                "qwen3-14b-b32-continuous": 6, "gemma3-12b-sliding-b32": 7, "gemma4-26b-full-b32": 8}
 # streams of one run
 S_LENGTHS, S_FILL, S_STEP, S_ACCEPT, S_OUTLIERS, S_CPU = range(6)
 
@@ -146,6 +146,10 @@ WORKLOADS = {
     # the sliding-window layers of a Gemma-3-12B-shaped model (window 1024), contexts as the headline
     "gemma3-12b-sliding-b32": dict(kind="window", layers=40, Hq=16, Hkv=8, D=256, B=32, lo=512, hi=8192,
                                    window=1024),
+    # the full-attention layers of a Gemma-4-26B-A4B-shaped model (head_dim 512, 2 KV heads for 16
+    # query heads, SDPA scale 1.0; six of them), contexts as the headline
+    "gemma4-26b-full-b32": dict(kind="decode", layers=6, Hq=16, Hkv=2, D=512, B=32, lo=512, hi=8192,
+                                scale=1.0),
 }
 
 
@@ -456,7 +460,7 @@ def _decode_calls(env, seqs, st, max_len_final, Hq):
     qp = [q_all[l].data_ptr() for l in range(layers)]
     kp = [k_new[l].data_ptr() for l in range(layers)]
     vp = [v_new[l].data_ptr() for l in range(layers)]
-    scale = ctypes.c_float(1.0 / math.sqrt(D))
+    scale = ctypes.c_float(w.get("scale", 1.0 / math.sqrt(D)))
     keep = (q_all, k_new, v_new, out, ws)
 
     def append(layer, s):
@@ -604,6 +608,7 @@ def run_decode(args, w):
                     f"context U[{w['lo']},{w['hi']}], 64-token blocks (permuted pool), {args.quant} int8, "
                     "bf16 N(0,1) inputs"
                     + (f" ({w['outlier_frac']:.0%} of channels x20)" if w.get("outlier_frac") else "")
+                    + (f", softmax scale {w['scale']}" if "scale" in w else "")
                     + "; step = per layer quantize-append 1 token/seq + paged decode attention"
                     + (" (two calls)" if args.unfused else " (one fused call)")
                     + ("; each step's table upload and calls replayed from a HIP graph" if args.graph else ""),
@@ -1166,11 +1171,12 @@ def cpu_baseline(args, w, lens0, per_tok):
     k = O.f32_to_bf16_bits(rng.normal((sample_layers, B, Hkv, D)).numpy())
     v = O.f32_to_bf16_bits(rng.normal((sample_layers, B, Hkv, D)).numpy())
     out = np.empty((sample_layers, B, Hq, D), np.float32)
-    base.step(q, k, v, O.DT_BF16, 1.0 / math.sqrt(D), out)  # warm (allocations)
+    sc = w.get("scale", 1.0 / math.sqrt(D))
+    base.step(q, k, v, O.DT_BF16, sc, out)  # warm (allocations)
     reps = 0
     t0 = time.perf_counter()
     while True:
-        base.step(q, k, v, O.DT_BF16, 1.0 / math.sqrt(D), out)
+        base.step(q, k, v, O.DT_BF16, sc, out)
         reps += 1
         el = time.perf_counter() - t0
         if el > 12.0 or reps >= 100000:
@@ -1181,7 +1187,7 @@ def cpu_baseline(args, w, lens0, per_tok):
     one_reps = 0
     t1 = time.perf_counter()
     while True:
-        base.step(q, k, v, O.DT_BF16, 1.0 / math.sqrt(D), out, layers_to_run=1)
+        base.step(q, k, v, O.DT_BF16, sc, out, layers_to_run=1)
         one_reps += 1
         one_el = time.perf_counter() - t1
         if one_el > 2.0 or one_reps >= 100000:

@@ -72,7 +72,7 @@ typedef void *krill_stream_t; /* hipStream_t */
 typedef struct krill_pool_desc {
   int32_t num_layers;
   int32_t num_kv_heads;
-  int32_t head_dim;      /* 64, 128 or 256 */
+  int32_t head_dim;      /* 64, 128, 256 or 512 (Gemma 4 full-attention layers) */
   int32_t block_tokens;  /* must be 64 */
   int32_t num_blocks;    /* physical blocks per layer */
   int32_t quant_mode;    /* KRILL_QUANT_* */
