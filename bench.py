@@ -161,8 +161,13 @@ def parse():
     ap.add_argument("--workload", default="qwen3-14b-b32", choices=sorted(WORKLOADS))
     ap.add_argument("--quant", default="affine_g64", choices=["affine_g64", "ref_row"])
     ap.add_argument("--split-blocks", type=int, default=0)
+    ap.add_argument("--wave-stamps", action="store_true",
+                    help="add the last decode launch's wave timeline (needs KRILL_LIBRARY=libkrillhip_stamps.so)")
     ap.add_argument("--rope-fill", action="store_true",
                     help="prefill K with RoPE fused into the append (krill_quantize_append_rope)")
+    ap.add_argument("--window-rope", type=int, default=1,
+                    help="sliding-window workload, fused step: 1 = RoPE of the queries and new K rows in the call, "
+                         "0 = without")
     ap.add_argument("--unfused", action="store_true",
                     help="decode step as two calls per layer (quantize-append, then decode attention) instead of "
                          "the fused krill_decode_append_attention")
@@ -318,7 +323,54 @@ def _record(args, w, env, value, ms_step, config, roofline, extra, cpu=None):
     rec["cpu_baseline"] = cpu
     rec["pool"] = {k: stats[k] for k in ("cow_copies", "blocks_used", "blocks_shared", "evicted_entries",
                                          "evicted_blocks", "num_blocks")}
+    if args.wave_stamps:
+        rec["wave_stamps"] = wave_stamp_summary(env)
     return rec
+
+
+def wave_stamp_summary(env):
+    """Timeline of the last decode-attention launch from a library built with
+    `make stamps` (KRILL_LIBRARY=libkrillhip_stamps.so): per-wave start, first
+    block ready, static part done and end (realtime clock, 100 MHz), with the
+    XCD / CU / SIMD of each wave; and the launch's end time if the waves' work
+    were balanced within each CU, within each XCD, or over the whole GPU (the
+    mean end time of the group: total work kept, end times evened out)."""
+    env.torch.cuda.synchronize()
+    buf = np.zeros((65536, 6), np.uint64)
+    n = env.lib.krill_diag_wave_stamps(buf.ctypes.data_as(ctypes.c_void_p), buf.shape[0])
+    if n < 0:
+        return {"error": env.KL.last_error()}
+    a = buf[:n].astype(np.int64)
+    a = a[a[:, 2] > 0]
+    a = a[a[:, 0] >= a[:, 0].max() - 5000]  # the last launch: its waves start within 50 us
+    t0 = a[:, 0].min()
+    us = lambda t: (t - t0) / 100.0  # noqa: E731
+    st, fr, en = us(a[:, 0]), us(a[:, 1]), us(a[:, 2])
+    hw, xcc = a[:, 4] & 0xFFFFFFFF, (a[:, 4] >> 32) & 0xF
+    simd, cu, sh, se = (hw >> 4) & 3, (hw >> 8) & 15, (hw >> 12) & 1, (hw >> 13) & 7
+    cuid = xcc * 1000 + se * 100 + sh * 20 + cu
+    cus = np.unique(cuid)
+    cu_spread = np.array([np.ptp(en[cuid == c]) for c in cus])
+    cu_mean = np.array([en[cuid == c].mean() for c in cus])
+    xcds = np.unique(xcc)
+    xcd_mean = np.array([en[xcc == x].mean() for x in xcds])
+    grid = np.linspace(0.0, en.max(), 13)
+    r2 = lambda x: round(float(x), 2)  # noqa: E731
+    return {
+        "waves": int(len(a)),
+        "span_us": r2(en.max()),
+        "start_spread_us": r2(np.ptp(st)),
+        "first_ready_us": {"median": r2(np.median(fr - st)), "p90": r2(np.percentile(fr - st, 90))},
+        "end_us": {"min": r2(en.min()), "p10": r2(np.percentile(en, 10)), "median": r2(np.median(en)),
+                   "p90": r2(np.percentile(en, 90)), "max": r2(en.max())},
+        "mean_wave_life_frac": r2((en - st).mean() / en.max()),
+        "xcd_mean_end_us": [r2(x) for x in xcd_mean],
+        "within_cu_end_spread_us_median": r2(np.median(cu_spread)),
+        "balanced_end_us": {"within_cu": r2(cu_mean.max()), "within_xcd": r2(xcd_mean.max()),
+                            "whole_gpu": r2(en.mean())},
+        "alive_waves": [int(((st <= t) & (en > t)).sum()) for t in grid],
+        "alive_at_us": [r2(t) for t in grid],
+    }
 
 
 def _timed(env, step, warmup, steps):
@@ -782,8 +834,9 @@ def run_continuous(args, w):
 def run_window(args, w):
     """Decode steps of sliding-window layers: a pool with the window option
     (each append first drops the blocks below the sequence's last window - 1
-    tokens), per layer the new token's quantize-append and windowed decode
-    attention over the retained window."""
+    tokens), per layer one launch that turns the queries and the new K row by
+    the token's position (RoPE), appends the token and attends the retained
+    window (--unfused: quantize-append, then windowed attention, no RoPE)."""
     layers, Hq, Hkv, D, B, W = w["layers"], w["Hq"], w["Hkv"], w["D"], w["B"], w["window"]
     t = None
     rng = Philox(args.seed, S_LENGTHS)
@@ -813,11 +866,21 @@ def run_window(args, w):
     one = np.empty(1, np.int32)
     cur_len = [int(x) for x in lens0]
     KL, lib, h, sp = env.KL, env.lib, env.h, env.sp
+    from krill_amd.pool import rope_table
+
+    cs = t.from_numpy(rope_table(max_len_final + 1, D, 1.0e4)).to(env.dev)
 
     def attend(layer, mx):
         KL.check(lib.krill_attention_windowed(h, layer, q_all[layer].data_ptr(), 1, st.d_tables.data_ptr(),
                                               st.d_lens.data_ptr(), d_starts.data_ptr(), W, B, max_blocks, mx, Hq,
                                               scale, out.data_ptr(), KL.DTYPE_BF16, ws.data_ptr(), need.value, sp))
+
+    def fused(layer, mx):  # RoPE + append + windowed attention, one launch
+        KL.check(lib.krill_decode_append_attention_windowed(
+            h, layer, q_all[layer].data_ptr(), k_new[layer].data_ptr(), v_new[layer].data_ptr(), Hkv * D, D,
+            st.d_tables.data_ptr(), st.d_lens.data_ptr(), d_starts.data_ptr(), W, B, max_blocks, mx, Hq, scale,
+            cs.data_ptr() if args.window_rope else None, cs.shape[0], out.data_ptr(), KL.DTYPE_BF16, ws.data_ptr(),
+            need.value, sp))
 
     def step(i):
         j, ps, pt, pl = st.host(i)
@@ -831,9 +894,12 @@ def run_window(args, w):
         st.upload(j, slots=True)
         mx = max(cur_len)
         for layer in range(layers):
-            KL.check(lib.krill_quantize_append(h, layer, k_new[layer].data_ptr(), v_new[layer].data_ptr(),
-                                               st.d_slots.data_ptr(), B, 1, sp))
-            attend(layer, mx)
+            if args.unfused:
+                KL.check(lib.krill_quantize_append(h, layer, k_new[layer].data_ptr(), v_new[layer].data_ptr(),
+                                                   st.d_slots.data_ptr(), B, 1, sp))
+                attend(layer, mx)
+            else:
+                fused(layer, mx)
 
     for i in range(args.warmup):
         step(i)
@@ -846,20 +912,26 @@ def run_window(args, w):
     step_bytes = layers * (vis * per_tok + qo_layer + app_layer)
     gbs_step = step_bytes / (ms_step * 1e-3) / 1e9
     mx = max(cur_len)
-    attn_ms = _time_calls(env, lambda layer: attend(layer, mx), args.kernel_reps)
-    launch_bytes = vis * per_tok + qo_layer
+    call = attend if args.unfused else fused  # the fused call rewrites the same newest token
+    attn_ms = _time_calls(env, lambda layer: call(layer, mx), args.kernel_reps)
+    launch_bytes = vis * per_tok + qo_layer + (0 if args.unfused else app_layer)
     stats = env.pool.stats()
     config = {
         "workload": f"{args.workload}: {layers} sliding-window layers, window {W}, Hq {Hq}, Hkv {Hkv}, D {D}, B {B}, "
                     f"context U[{w['lo']},{w['hi']}], {args.quant} int8, pool with the window option (blocks below "
-                    "each window freed); step = per layer quantize-append 1 token/seq + windowed decode attention",
+                    "each window freed); step = per layer "
+                    + ("quantize-append 1 token/seq + windowed decode attention (two calls)" if args.unfused else
+                       ("RoPE of the queries and new K rows + " if args.window_rope else "")
+                       + "append 1 token/seq + windowed decode attention (one fused call)"),
         "layers": layers, "Hq": Hq, "Hkv": Hkv, "head_dim": D, "batch": B, "quant": args.quant, "window": W,
         "context_mean": float(np.mean(lens0)), "num_blocks": num_blocks,
     }
     roofline = {
         "bound": "hbm",
-        "kernel": "windowed decode attention call (k_attn_valu window variant + k_attn_merge_flat), one layer; "
-                  "bytes of the keys the rows see",
+        "kernel": ("windowed decode attention call" if args.unfused else
+                   "fused " + ("RoPE + " if args.window_rope else "") + "append + windowed decode attention call")
+                  + " (k_attn_valu window variant + k_attn_merge_flat), one layer; bytes of the keys the rows see"
+                  + ("" if args.unfused else ", q/o and the new token"),
         "achieved": round(launch_bytes / (attn_ms * 1e-3) / 1e9, 2),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",

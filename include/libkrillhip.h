@@ -20,6 +20,13 @@
  *     [B][H][L][D] (QuantizedKVCache.update input, QuantizedKVCache.swift:46),
  *     snapshots are [B][H][S][D] u8 + [B][H][S][G] f16 (QuantizedKVSnapshot,
  *     QuantizedKVCache.swift:150-157; G = 1 in the reference's row mode).
+ *   - Attention takes queries as fp16 (relative rounding 2^-11; scores and
+ *     softmax in fp32).  bf16 queries keep their whole range: a query row
+ *     whose largest |q| is 65504 or more is scaled by an exact power of two
+ *     before the fp16 rounding and its scores by the inverse, so it neither
+ *     overflows nor changes the rows beside it; elements of such a row below
+ *     2^-40 of its largest |q| round to zero.  A row holding inf or NaN
+ *     gives NaN output.
  */
 #ifndef LIBKRILLHIP_H
 #define LIBKRILLHIP_H
@@ -115,6 +122,13 @@ typedef struct krill_snapshot {
 /* Last error message of the calling thread ("" if none). */
 const char *krill_last_error(void);
 int32_t krill_abi_version(void);
+/* Diagnostics, no counterpart in the reference: per-wave timestamps of the
+ * last decode-attention launch, from a library built with `make stamps`
+ * (libkrillhip_stamps.so; the product build returns KRILL_E_UNSUPPORTED).
+ * Copies up to max_waves rows of 6 words: realtime clock (100 MHz) at the
+ * wave's start, first block ready, end, static part done; HW_ID | XCC_ID << 32;
+ * static blocks | segments << 32.  Returns the rows copied. */
+int32_t krill_diag_wave_stamps(uint64_t *out, int32_t max_waves);
 
 /* ---------------------------------------------------------------- pool */
 
@@ -377,6 +391,27 @@ int32_t krill_attention_windowed(krill_pool_t pool, int32_t layer, const void *d
                                  const int32_t *dev_starts, int32_t window, int32_t B, int32_t max_blocks,
                                  int32_t max_seq_len, int32_t Hq, float scale, void *dev_out, int32_t out_dtype,
                                  void *dev_ws, size_t ws_bytes, krill_stream_t stream);
+/* The sliding layers' decode step in one launch: each sequence's newest
+ * token (K/V rows [b][h][D] at element strides stride_b, stride_h) is
+ * written at position seq_lens[b] - 1 (the slot krill_seq_reserve_append
+ * handed out, after its window trim) and every query attends its window, as
+ * krill_quantize_append at that slot followed by krill_attention_windowed
+ * with Lq = 1 -- the update() of RotatingKVCache (RotatingKVCache.swift:40-173)
+ * and SDPA of a decode step.  With dev_cos_sin (fp32 [max_pos][D], max_pos >=
+ * max_seq_len) the queries and new K rows are first turned by the token's
+ * absolute position, as krill_decode_append_attention_rope does (the
+ * rotating model's applyRoPEPerRow, Attention.swift:13-20); NULL: no RoPE.
+ * The decode kernel only: at most 8 query rows per KV head, head_dim <= 256
+ * with RoPE (KRILL_E_UNSUPPORTED otherwise).  Workspace:
+ * krill_window_workspace_size with Lq = 1. */
+int32_t krill_decode_append_attention_windowed(krill_pool_t pool, int32_t layer, const void *dev_q,
+                                               const void *dev_k_new, const void *dev_v_new, int64_t stride_b,
+                                               int64_t stride_h, const int32_t *dev_block_tables,
+                                               const int32_t *dev_seq_lens, const int32_t *dev_starts,
+                                               int32_t window, int32_t B, int32_t max_blocks, int32_t max_seq_len,
+                                               int32_t Hq, float scale, const float *dev_cos_sin, int32_t max_pos,
+                                               void *dev_out, int32_t out_dtype, void *dev_ws, size_t ws_bytes,
+                                               krill_stream_t stream);
 /* Speculative-verify / chunked-prefill attention: Lq new query rows per
  * sequence, already appended, causal inside the window (row j sees tokens
  * [0, len - Lq + j]; BatchedDecode.swift:299-312, LlamaModel.swift:186-202).

@@ -10,7 +10,12 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libkrillhip.so")
+# KRILL_LIBRARY names another build in this directory (the diagnostic
+# libkrillhip_stamps.so of `make stamps`); a bare file name only.
+_LIB_NAME = os.environ.get("KRILL_LIBRARY", "libkrillhip.so")
+if os.path.basename(_LIB_NAME) != _LIB_NAME or not _LIB_NAME.endswith(".so"):
+    raise ValueError(f"KRILL_LIBRARY must name a .so file in {HERE}")
+LIB_PATH = os.path.join(HERE, _LIB_NAME)
 HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "libkrillhip.h")
 
 KRILL_OK = 0
@@ -119,6 +124,7 @@ STR = ctypes.c_char_p
 SIGNATURES = {
     "krill_last_error": [],
     "krill_abi_version": [],
+    "krill_diag_wave_stamps": [P, I32],
     "krill_pool_create": [ctypes.POINTER(PoolDesc), P, ctypes.POINTER(P)],
     "krill_pool_destroy": [P],
     "krill_pool_get_stats": [P, ctypes.POINTER(PoolStats)],
@@ -162,6 +168,8 @@ SIGNATURES = {
     "krill_window_workspace_size": [P, I32, I32, I32, I32, I32, I32, ctypes.POINTER(ctypes.c_size_t)],
     "krill_attention_windowed": [P, I32, P, I32, P, P, P, I32, I32, I32, I32, I32, ctypes.c_float, P, I32, P,
                                  ctypes.c_size_t, P],
+    "krill_decode_append_attention_windowed": [P, I32, P, P, P, I64, I64, P, P, P, I32, I32, I32, I32, I32,
+                                               ctypes.c_float, P, I32, P, I32, P, ctypes.c_size_t, P],
     "krill_shared_prefix_workspace_size": [P, I32, I32, I32, I32, ctypes.POINTER(ctypes.c_size_t)],
     "krill_decode_attention_shared_prefix": [P, I32, P, P, I32, P, P, I32, I32, I32, I32, ctypes.c_float, P, I32,
                                              P, ctypes.c_size_t, P],

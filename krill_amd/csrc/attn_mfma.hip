@@ -180,6 +180,7 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
   // ---- Q^T operands of sequence bq: lane holds q[row n][32 ks + 8 q4 .. +8]
   half8_t qB[NRT][KS];
   float qsum[NRT][G];
+  float q_up[NRT];  // the lane's row: softmax scale in log2 units times the query's 2^k
   bool rvalid[NRT];
 #pragma unroll
   for (int rt = 0; rt < NRT; ++rt) rvalid[rt] = rbase + 16 * rt + n < a.NR;
@@ -228,6 +229,25 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
     for (int rt = 0; rt < NRT; ++rt) {
 #pragma unroll
       for (int g = 0; g < G; ++g) qsum[rt][g] = 0.0f;
+      // bf16 rows at the fp16 range limit are scaled by 2^-k before the
+      // rounding, their scores by 2^k (q_range_scale); the row's elements
+      // sit in lanes n, n + 16, n + 32, n + 48
+      float down = 1.0f, up = 1.0f;
+      if (a.q_dtype == DT_BF16) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const uint32_t w4[4] = {qraw[rt][ks].x, qraw[rt][ks].y, qraw[rt][ks].z, qraw[rt][ks].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            mx = fmaxf(mx, fmaxf(fabsf(__builtin_bit_cast(float, w4[e] << 16)),
+                                 fabsf(__builtin_bit_cast(float, w4[e] & 0xffff0000u))));
+        }
+        mx = fmaxf(mx, shfl_xor(mx, 16));
+        mx = fmaxf(mx, shfl_xor(mx, 32));
+        down = q_range_scale(mx, up);
+      }
+      q_up[rt] = a.scale_log2 * up;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const uint32_t w4[4] = {qraw[rt][ks].x, qraw[rt][ks].y, qraw[rt][ks].z, qraw[rt][ks].w};
@@ -236,8 +256,8 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
         for (int e = 0; e < 4; ++e) {
           _Float16 lo, hi;
           if (a.q_dtype == DT_BF16) {
-            lo = (_Float16)__builtin_bit_cast(float, w4[e] << 16);
-            hi = (_Float16)__builtin_bit_cast(float, w4[e] & 0xffff0000u);
+            lo = (_Float16)(__builtin_bit_cast(float, w4[e] << 16) * down);
+            hi = (_Float16)(__builtin_bit_cast(float, w4[e] & 0xffff0000u) * down);
           } else {
             lo = __builtin_bit_cast(_Float16, (uint16_t)(w4[e] & 0xffffu));
             hi = __builtin_bit_cast(_Float16, (uint16_t)(w4[e] >> 16));
@@ -388,14 +408,14 @@ __global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
               float sv = 0.0f;
 #pragma unroll
               for (int g = 0; g < G; ++g) sv = fmaf(kss[g], sacc[rt][g][e], fmaf(kzz[g], qsum[rt][g], sv));
-              sc[t][rt][e] = sv * a.scale_log2;
+              sc[t][rt][e] = sv * q_up[rt];
             }
           }
         } else {
 #pragma unroll
           for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sc[t][rt][e] = sacc[rt][0][e] * a.scale_log2;
+            for (int e = 0; e < 4; ++e) sc[t][rt][e] = sacc[rt][0][e] * q_up[rt];
         }
       }
       // the K bytes of this stage are consumed: refill them NST blocks ahead

@@ -52,6 +52,15 @@
 
 namespace krill {
 
+#ifdef KRILL_WAVE_STAMPS
+// Diagnostic build only (make stamps): per wave of the last launch, the
+// realtime clock (100 MHz) at its start, when its first block and queries
+// are in registers and at its end, its hardware ids, its blocks and
+// sequence segments.
+constexpr int kStampWaves = 65536;
+__device__ unsigned long long g_wave_stamps[kStampWaves * 6];
+#endif
+
 // acc += sum_i k[i] . q_(OFF + i), i < 8, where q_n is lane n of this lane's
 // 16-lane row of `q` (v_dot2c_f32_f16 with a DPP row_newbcast source).  The
 // leading s_nop covers the VALU-write -> DPP-read hazard of the operands.
@@ -124,9 +133,16 @@ template <int D>
 constexpr int d_slices() {
   return D > 256 ? D / 128 : 1;
 }
+// KRILL_PV_ON_VALU (the libkrillhip_pvvalu.so diagnostic build) keeps P.V
+// on the VALU with binary32 weights wherever one wave holds the whole head,
+// for timing the two forms against each other on one build.
 template <int D, int NR>
 constexpr bool pv_on_mfma() {
+#ifdef KRILL_PV_ON_VALU
+  return D > 256;
+#else
   return (D <= 128 && NR >= 3) || D > 256;
+#endif
 }
 template <int D, int NR>
 constexpr int valu_waves_per_simd() {
@@ -230,13 +246,14 @@ __device__ __forceinline__ void store_newest(const AttnArgs &a, int hk, int phys
 }
 
 // VAR: 0 plain; 1 RoPE of the queries (and the fused new K row); 2 sliding
-// window (keys below max(win_start[b], position - window + 1) masked).
+// window (keys below max(win_start[b], position - window + 1) masked); 3
+// both (the sliding layers of a rotating model's decode step).
 // head_dim 512 (d_slices > 1): workgroups of d_slices waves, wave w the dims
 // [DW w, DW w + DW); the query rows of a KV head in row groups of NR rows
 // (blockIdx.z), each its own flat block order and partial slots.
 template <int D, int NR, int MODE, int VAR>
 __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>())) void k_attn_valu(AttnArgs a) {
-  constexpr bool ROPE = VAR == 1, WIN = VAR == 2;
+  constexpr bool ROPE = VAR == 1 || VAR == 3, WIN = VAR == 2 || VAR == 3;
   constexpr int DS = d_slices<D>();  // waves per workgroup, one per d-slice
   constexpr int DW = D / DS;         // dims of one wave
   constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;    // scale groups per token (pool layout)
@@ -274,6 +291,11 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
   // ends inside them) no longer pile up on one XCD.
   const int hk = blockIdx.y;
   const int wv = (int)((blockIdx.x + (unsigned)hk) % gridDim.x);
+#ifdef KRILL_WAVE_STAMPS
+  const unsigned long long st_t0 = __builtin_amdgcn_s_memrealtime();
+  unsigned long long st_t1 = 0;
+  int st_seg = 0;
+#endif
   // This wave's blocks: flat indices [i0, iend) of the concatenated block
   // lists of all sequences.  The T blocks are split evenly over the grid's
   // waves (sized to the resident wave capacity of the GPU; min(W, T) of them
@@ -368,11 +390,14 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
   auto prepare = [&](int bs, int f) {
     const int len2 = seq_len(bs);
     if (!((tab_okm >> (f - i0)) & 1)) return;
+    // RoPE turns the row by its absolute position (the window's view of a
+    // sequence starts some whole blocks in)
+    const int rpos = WIN ? len_of(a, bs) - 1 : len2 - 1;
     if (a.q_dtype == DT_BF16) {
-      if constexpr (ROPE) rope_row_lanes<D, DT_BF16>(rk, rope_row(a, len2 - 1, D));
+      if constexpr (ROPE) rope_row_lanes<D, DT_BF16>(rk, rope_row(a, rpos, D));
       prepare_newest<D, MODE, DT_BF16>(rk, rv, newrow, pkm, pvm);
     } else {
-      if constexpr (ROPE) rope_row_lanes<D, DT_F16>(rk, rope_row(a, len2 - 1, D));
+      if constexpr (ROPE) rope_row_lanes<D, DT_F16>(rk, rope_row(a, rpos, D));
       prepare_newest<D, MODE, DT_F16>(rk, rv, newrow, pkm, pvm);
     }
     patch_i = f;
@@ -434,6 +459,9 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
   // 32g .. 32g+31 = columns 2g and 2g+1), reduced inside each 16-lane row.
   uint32_t qv[NR][DW / 32];
   float qs[NR][GW];
+  // per row: the factor its scores take (the softmax scale in log2 units
+  // times the query's 2^k; d-slices: 2^k alone, on the slice's part)
+  float q_up[NR];
   const bool q_bf16 = a.q_dtype == DT_BF16;
   int qlen = 0;  // length of the sequence whose queries are loaded (RoPE positions)
   int qseq = 0;  // that sequence
@@ -445,7 +473,7 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
 #pragma unroll
       for (int c = 0; c < DW / 32; ++c) qv[r][c] = qp[16 * c + (lane & 15)];
     }
-    if constexpr (ROPE) qlen = seq_len(bq);
+    if constexpr (ROPE) qlen = WIN ? len_of(a, bq) : seq_len(bq);  // absolute positions
     qseq = bq;
   };
   auto finish_q = [&]() {
@@ -494,12 +522,26 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
     }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
+      // bf16 pairs are widened to fp32 and rounded to fp16 (rows at the
+      // fp16 range limit scaled by 2^-k first, q_range_scale); fp16 pairs
+      // pass through
+      float down = 1.0f, up = 1.0f;
+      if (q_bf16) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int c = 0; c < DW / 32; ++c) {
+          const uint32_t w = qv[r][c];
+          mx = fmaxf(mx, fmaxf(fabsf(__builtin_bit_cast(float, w << 16)),
+                               fabsf(__builtin_bit_cast(float, w & 0xffff0000u))));
+        }
+        down = q_range_scale(uniform_f32(row_allmax(mx)), up);
+      }
+      q_up[r] = DS > 1 ? up : a.scale_log2 * up;
 #pragma unroll
       for (int c = 0; c < DW / 32; ++c) {
-        // bf16 pairs are widened to fp32 and rounded to fp16; fp16 pairs pass through
         const uint32_t w = qv[r][c];
-        const half2_t hb = half2_t{(_Float16)__builtin_bit_cast(float, w << 16),
-                                   (_Float16)__builtin_bit_cast(float, w & 0xffff0000u)};
+        const half2_t hb = half2_t{(_Float16)(__builtin_bit_cast(float, w << 16) * down),
+                                   (_Float16)(__builtin_bit_cast(float, w & 0xffff0000u) * down)};
         qv[r][c] = q_bf16 ? h2_as_u32(hb) : w;
       }
       if constexpr (MODE == MODE_AFFINE) {
@@ -539,6 +581,9 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
     settle(vm[g]);
   }
   finish_q();
+#ifdef KRILL_WAVE_STAMPS
+  st_t1 = __builtin_amdgcn_s_memrealtime();
+#endif
 
   int i = i0;
   // Issue priority falls as the wave works through its range (3 in its
@@ -678,11 +723,11 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
         v = accg[r][0];
       }
       if constexpr (DS > 1) {
-        sc_lds[sbuf][wsl][r * 64 + lane] = v;  // this slice's part of the score
+        sc_lds[sbuf][wsl][r * 64 + lane] = v * q_up[r];  // this slice's part of the score
       } else {
         bool seen = tbase + lane < lim[r];
         if constexpr (WIN) seen = seen && tbase + lane >= lo[r];
-        s[r] = seen ? v * a.scale_log2 : -INFINITY;
+        s[r] = seen ? v * q_up[r] : -INFINITY;
       }
     }
     if constexpr (DS > 1) {
@@ -1060,6 +1105,9 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
       }
     }
     }
+#ifdef KRILL_WAVE_STAMPS
+    ++st_seg;
+#endif
     if (i >= iend_eff) break;
     // next sequence with blocks (empty ones get zeros from the merge)
     ++b;
@@ -1077,32 +1125,59 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
     }
     finish_q();
   }
+#ifdef KRILL_WAVE_STAMPS
+  {
+    const unsigned long long t2 = __builtin_amdgcn_s_memrealtime();
+    const unsigned hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);    // HW_REG_HW_ID
+    const unsigned xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);  // HW_REG_XCC_ID
+    const int64_t idx = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    if (lane == 0 && wsl == 0 && idx < kStampWaves) {
+      unsigned long long *o = g_wave_stamps + idx * 6;
+      o[0] = st_t0;
+      o[1] = st_t1;
+      o[2] = t2;
+      o[3] = 0;
+      o[4] = (unsigned long long)hw | ((unsigned long long)xcc << 32);
+      o[5] = (unsigned long long)(unsigned)(iend_eff - i0) | ((unsigned long long)(unsigned)st_seg << 32);
+    }
+  }
+#endif
 }
 
 template <int D, int MODE, int NR>
-static void launch_one(const AttnArgs &args, int B, dim3 grid, hipStream_t st) {
+static hipError_t launch_one(const AttnArgs &args, int B, dim3 grid, hipStream_t st) {
   const dim3 block(64 * d_slices<D>());
-  if (args.rope_cs)
+  if (args.rope_cs && args.window > 0) {
+    // sliding-window layers with RoPE: head_dim <= 256
+    if constexpr (D <= 256)
+      k_attn_valu<D, NR, MODE, 3><<<grid, block, 0, st>>>(args);
+    else
+      return hipErrorInvalidValue;
+  } else if (args.rope_cs) {
     k_attn_valu<D, NR, MODE, 1><<<grid, block, 0, st>>>(args);
-  else if (args.window > 0)
+  } else if (args.window > 0) {
     k_attn_valu<D, NR, MODE, 2><<<grid, block, 0, st>>>(args);
-  else
+  } else {
     k_attn_valu<D, NR, MODE, 0><<<grid, block, 0, st>>>(args);
+  }
+  return hipSuccess;
 }
 
 template <int D, int MODE>
 static hipError_t launch_valu_nr(const AttnArgs &args, int NR, int B, dim3 grid, hipStream_t st) {
+  hipError_t e;
   switch (NR) {
-    case 1: launch_one<D, MODE, 1>(args, B, grid, st); break;
-    case 2: launch_one<D, MODE, 2>(args, B, grid, st); break;
-    case 3: launch_one<D, MODE, 3>(args, B, grid, st); break;
-    case 4: launch_one<D, MODE, 4>(args, B, grid, st); break;
-    case 5: launch_one<D, MODE, 5>(args, B, grid, st); break;
-    case 6: launch_one<D, MODE, 6>(args, B, grid, st); break;
-    case 7: launch_one<D, MODE, 7>(args, B, grid, st); break;
-    case 8: launch_one<D, MODE, 8>(args, B, grid, st); break;
+    case 1: e = launch_one<D, MODE, 1>(args, B, grid, st); break;
+    case 2: e = launch_one<D, MODE, 2>(args, B, grid, st); break;
+    case 3: e = launch_one<D, MODE, 3>(args, B, grid, st); break;
+    case 4: e = launch_one<D, MODE, 4>(args, B, grid, st); break;
+    case 5: e = launch_one<D, MODE, 5>(args, B, grid, st); break;
+    case 6: e = launch_one<D, MODE, 6>(args, B, grid, st); break;
+    case 7: e = launch_one<D, MODE, 7>(args, B, grid, st); break;
+    case 8: e = launch_one<D, MODE, 8>(args, B, grid, st); break;
     default: return hipErrorInvalidValue;
   }
+  if (e != hipSuccess) return e;
   return hipGetLastError();
 }
 
@@ -1150,6 +1225,22 @@ int32_t valu_waves_per_cu(const PoolGeometry &g, int32_t NR) {
     c = n;
   }
   return c;
+}
+
+// Copies the stamps of the last decode launch (diagnostic build), up to
+// max_waves rows of 6 words; returns the rows copied, or -1 if this build
+// has no stamps.
+int32_t wave_stamps(unsigned long long *host, int32_t max_waves) {
+#ifdef KRILL_WAVE_STAMPS
+  const int32_t n = max_waves < kStampWaves ? max_waves : kStampWaves;
+  if (hipMemcpyFromSymbol(host, HIP_SYMBOL(g_wave_stamps), (size_t)n * 6 * 8, 0, hipMemcpyDeviceToHost) != hipSuccess)
+    return -2;
+  return n;
+#else
+  (void)host;
+  (void)max_waves;
+  return -1;
+#endif
 }
 
 hipError_t launch_attn_valu(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,

@@ -114,6 +114,17 @@ const char *krill_last_error(void) { return krill::g_last_error; }
 
 int32_t krill_abi_version(void) { return KRILL_ABI_VERSION; }
 
+int32_t krill_diag_wave_stamps(uint64_t *out, int32_t max_waves) {
+  return krill::guarded([&]() -> int32_t {
+    krill::clear_error();
+    if (!out || max_waves < 0) return fail(KRILL_E_INVAL, "out is NULL or max_waves < 0");
+    const int32_t n = krill::wave_stamps(reinterpret_cast<unsigned long long *>(out), max_waves);
+    if (n == -1) return fail(KRILL_E_UNSUPPORTED, "this build records no wave stamps (make stamps)");
+    if (n < 0) return fail(KRILL_E_HIP, "copy of the wave stamps failed");
+    return n;
+  });
+}
+
 int32_t krill_pool_create(const krill_pool_desc *desc, krill_stream_t stream, krill_pool_t *out) {
   return krill::guarded([&]() -> int32_t {
     krill::clear_error();
@@ -902,6 +913,62 @@ int32_t krill_window_workspace_size(krill_pool_t pool, int32_t B, int32_t Hq, in
   });
 }
 
+static int32_t run_windowed(krill_pool_t pool, int32_t layer, const void *dev_q, int32_t Lq,
+                            const int32_t *dev_block_tables, const int32_t *dev_seq_lens, const int32_t *dev_starts,
+                            int32_t window, int32_t B, int32_t max_blocks, int32_t max_seq_len, int32_t Hq,
+                            float scale, void *dev_out, int32_t out_dtype, void *dev_ws, size_t ws_bytes,
+                            krill_stream_t stream, const NewTokens &nt) {
+  if (int32_t rc = check_device_pool(pool, layer)) return rc;
+  if (B < 0 || max_blocks < 0 || max_seq_len < 0) return fail(KRILL_E_INVAL, "negative B, max_blocks or length");
+  if (B == 0) return KRILL_OK;
+  if (!dev_q || !dev_block_tables || !dev_seq_lens || !dev_out) return fail(KRILL_E_INVAL, "NULL device pointer");
+  if (out_dtype != KRILL_DTYPE_F32 && out_dtype != KRILL_DTYPE_F16 && out_dtype != KRILL_DTYPE_BF16)
+    return fail(KRILL_E_INVAL, "out_dtype %d", out_dtype);
+  if (!std::isfinite(scale)) return fail(KRILL_E_INVAL, "scale is not finite");
+  if ((int64_t)max_blocks * 64 < (int64_t)max_seq_len)
+    return fail(KRILL_E_RANGE, "max_seq_len %d exceeds the %d-block table width", max_seq_len, max_blocks);
+  if (B > 65535) return fail(KRILL_E_RANGE, "batch of %d sequences (at most 65535)", B);
+  krill::AttnPlan plan;
+  size_t total = 0;
+  if (int32_t rc = plan_windowed(pool, B, Hq, Lq, max_blocks, max_seq_len, window, &plan, &total)) return rc;
+  if (nt.k && plan.use_mfma)
+    return fail(KRILL_E_UNSUPPORTED, "the fused windowed step runs on the decode kernel: at most 8 query rows per "
+                "KV head (call krill_quantize_append, then krill_attention_windowed)");
+  if (nt.rope_cs && pool->geom.D > 256)
+    return fail(KRILL_E_UNSUPPORTED, "windowed RoPE step at head_dim %d (at most 256)", pool->geom.D);
+  if (ws_bytes < total || (total > 0 && !dev_ws))
+    return fail(KRILL_E_INVAL, "workspace of %zu bytes < %zu required", ws_bytes, total);
+  krill::AttnLaunch a;
+  a.q = dev_q;
+  a.tables = dev_block_tables;
+  a.lens = dev_seq_lens;
+  a.B = B;
+  a.max_blocks = max_blocks;
+  a.max_seq_len = (int32_t)std::min<int64_t>(max_seq_len, (int64_t)Lq + window + 62);
+  a.Hq = Hq;
+  a.Lq = Lq;
+  a.scale = scale;
+  a.out = dev_out;
+  a.out_dtype = out_dtype == KRILL_DTYPE_F32 ? krill::DT_F32 : out_dtype == KRILL_DTYPE_F16 ? krill::DT_F16
+                                                                                          : krill::DT_BF16;
+  a.ws = dev_ws;
+  a.ws_bytes = ws_bytes;
+  a.split_blocks = plan.split_blocks;
+  a.path = pool->opt_path;
+  a.k_new = nt.k;
+  a.v_new = nt.v;
+  a.kn_sb = nt.sb;
+  a.kn_sh = nt.sh;
+  a.rope_cs = nt.rope_cs;
+  a.rope_max_pos = nt.rope_max_pos;
+  DeviceGuard dg(pool->device);
+  hipStream_t st = pick_stream(pool, stream);
+  if (int32_t rc = flush_pending(pool, st)) return rc;
+  hipError_t e = krill::launch_attention_windowed(pool->geom, layer, a, plan, dev_starts, window, st);
+  if (e != hipSuccess) return hip_fail(e, "windowed attention launch");
+  return KRILL_OK;
+}
+
 int32_t krill_attention_windowed(krill_pool_t pool, int32_t layer, const void *dev_q, int32_t Lq,
                                  const int32_t *dev_block_tables, const int32_t *dev_seq_lens,
                                  const int32_t *dev_starts, int32_t window, int32_t B, int32_t max_blocks,
@@ -909,44 +976,34 @@ int32_t krill_attention_windowed(krill_pool_t pool, int32_t layer, const void *d
                                  void *dev_ws, size_t ws_bytes, krill_stream_t stream) {
   return krill::guarded([&]() -> int32_t {
     krill::clear_error();
-    if (int32_t rc = check_device_pool(pool, layer)) return rc;
-    if (B < 0 || max_blocks < 0 || max_seq_len < 0) return fail(KRILL_E_INVAL, "negative B, max_blocks or length");
-    if (B == 0) return KRILL_OK;
-    if (!dev_q || !dev_block_tables || !dev_seq_lens || !dev_out) return fail(KRILL_E_INVAL, "NULL device pointer");
-    if (out_dtype != KRILL_DTYPE_F32 && out_dtype != KRILL_DTYPE_F16 && out_dtype != KRILL_DTYPE_BF16)
-      return fail(KRILL_E_INVAL, "out_dtype %d", out_dtype);
-    if (!std::isfinite(scale)) return fail(KRILL_E_INVAL, "scale is not finite");
-    if ((int64_t)max_blocks * 64 < (int64_t)max_seq_len)
-      return fail(KRILL_E_RANGE, "max_seq_len %d exceeds the %d-block table width", max_seq_len, max_blocks);
-    if (B > 65535) return fail(KRILL_E_RANGE, "batch of %d sequences (at most 65535)", B);
-    krill::AttnPlan plan;
-    size_t total = 0;
-    if (int32_t rc = plan_windowed(pool, B, Hq, Lq, max_blocks, max_seq_len, window, &plan, &total)) return rc;
-    if (ws_bytes < total || (total > 0 && !dev_ws))
-      return fail(KRILL_E_INVAL, "workspace of %zu bytes < %zu required", ws_bytes, total);
-    krill::AttnLaunch a;
-    a.q = dev_q;
-    a.tables = dev_block_tables;
-    a.lens = dev_seq_lens;
-    a.B = B;
-    a.max_blocks = max_blocks;
-    a.max_seq_len = (int32_t)std::min<int64_t>(max_seq_len, (int64_t)Lq + window + 62);
-    a.Hq = Hq;
-    a.Lq = Lq;
-    a.scale = scale;
-    a.out = dev_out;
-    a.out_dtype = out_dtype == KRILL_DTYPE_F32 ? krill::DT_F32 : out_dtype == KRILL_DTYPE_F16 ? krill::DT_F16
-                                                                                            : krill::DT_BF16;
-    a.ws = dev_ws;
-    a.ws_bytes = ws_bytes;
-    a.split_blocks = plan.split_blocks;
-    a.path = pool->opt_path;
-    DeviceGuard dg(pool->device);
-    hipStream_t st = pick_stream(pool, stream);
-    if (int32_t rc = flush_pending(pool, st)) return rc;
-    hipError_t e = krill::launch_attention_windowed(pool->geom, layer, a, plan, dev_starts, window, st);
-    if (e != hipSuccess) return hip_fail(e, "windowed attention launch");
-    return KRILL_OK;
+    return run_windowed(pool, layer, dev_q, Lq, dev_block_tables, dev_seq_lens, dev_starts, window, B, max_blocks,
+                        max_seq_len, Hq, scale, dev_out, out_dtype, dev_ws, ws_bytes, stream, NewTokens{});
+  });
+}
+
+int32_t krill_decode_append_attention_windowed(krill_pool_t pool, int32_t layer, const void *dev_q,
+                                               const void *dev_k_new, const void *dev_v_new, int64_t stride_b,
+                                               int64_t stride_h, const int32_t *dev_block_tables,
+                                               const int32_t *dev_seq_lens, const int32_t *dev_starts,
+                                               int32_t window, int32_t B, int32_t max_blocks, int32_t max_seq_len,
+                                               int32_t Hq, float scale, const float *dev_cos_sin, int32_t max_pos,
+                                               void *dev_out, int32_t out_dtype, void *dev_ws, size_t ws_bytes,
+                                               krill_stream_t stream) {
+  return krill::guarded([&]() -> int32_t {
+    krill::clear_error();
+    if (B > 0 && (!dev_k_new || !dev_v_new)) return fail(KRILL_E_INVAL, "NULL new K/V pointer");
+    if (stride_b < 0 || stride_h < 0) return fail(KRILL_E_INVAL, "negative stride");
+    if (dev_cos_sin && (max_pos < 1 || max_pos < max_seq_len))
+      return fail(KRILL_E_INVAL, "RoPE table of %d positions does not cover max_seq_len %d", max_pos, max_seq_len);
+    NewTokens nt;
+    nt.k = dev_k_new;
+    nt.v = dev_v_new;
+    nt.sb = stride_b;
+    nt.sh = stride_h;
+    nt.rope_cs = dev_cos_sin;
+    nt.rope_max_pos = dev_cos_sin ? max_pos : 0;
+    return run_windowed(pool, layer, dev_q, 1, dev_block_tables, dev_seq_lens, dev_starts, window, B, max_blocks,
+                        max_seq_len, Hq, scale, dev_out, out_dtype, dev_ws, ws_bytes, stream, nt);
   });
 }
 

@@ -271,6 +271,25 @@ __device__ __forceinline__ float row_allsum(float v) {
   v += dpp_f32<0x128>(v);  // row_ror:8
   return v;
 }
+// Maximum over the 16 lanes of each DPP row, left in every lane of the row.
+__device__ __forceinline__ float row_allmax(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x124>(v));
+  v = fmaxf(v, dpp_f32<0x128>(v));
+  return v;
+}
+// Queries reach the matrix and dot-product instructions as fp16.  A bf16 row
+// whose largest |q| is at or above 65504 (where the fp16 rounding overflows)
+// is scaled by 2^-k first, k the smallest power that brings it below 2^15,
+// and its scores by 2^k; both are exact.  Returns 2^-k (1 for every other
+// row, non-finite maxima included) and sets `up` to 2^k.
+__device__ __forceinline__ float q_range_scale(float absmax, float &up) {
+  const int e = (int)((__builtin_bit_cast(uint32_t, absmax) >> 23) & 0xffu);  // biased exponent
+  const int k = (absmax >= 65504.0f && e < 255) ? e - 141 : 0;              // 2^15 has e = 142
+  up = __builtin_bit_cast(float, (uint32_t)(127 + k) << 23);
+  return __builtin_bit_cast(float, (uint32_t)(127 - k) << 23);
+}
 // A value known to be the same in every lane, moved to a scalar register.
 __device__ __forceinline__ float uniform_f32(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));

@@ -1187,7 +1187,13 @@ hipError_t launch_attention_shared_prefix(const PoolGeometry &g, int32_t layer, 
 hipError_t launch_attention_windowed(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
                                      const int32_t *starts, int32_t window, hipStream_t st) {
   if (a.B == 0) return hipSuccess;
-  if (window < 2 || a.k_new || a.rope_cs || a.len_const >= 0) return hipErrorInvalidValue;
+  if (window < 2 || a.len_const >= 0) return hipErrorInvalidValue;
+  // the decode step with the append (and RoPE) fused runs on the VALU
+  // kernel's window variants (the MFMA path has no RoPE of the queries, and
+  // its separate append launch reads absolute table columns the windowed
+  // plan does not cover)
+  if (a.rope_cs && (!a.k_new || g.D > 256)) return hipErrorInvalidValue;
+  if (a.k_new && (p.use_mfma || a.Lq != 1)) return hipErrorInvalidValue;
   AttnLaunch w = a;
   w.win_start = starts;
   w.window = window;

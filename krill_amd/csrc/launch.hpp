@@ -111,6 +111,9 @@ int32_t valu_waves_per_cu(const PoolGeometry &g, int32_t NR);
 // occupancy query on a device pool.
 int32_t mfma_groups_per_cu(const PoolGeometry &g, int32_t nrt, int32_t group_waves, int32_t token_split);
 
+// Per-wave timestamps of the last decode launch (diagnostic build only).
+int32_t wave_stamps(unsigned long long *host, int32_t max_waves);
+
 // Per-configuration kernels, defined in the attention translation units.
 hipError_t launch_attn_valu(const PoolGeometry &g, int32_t layer, const AttnLaunch &a, const AttnPlan &p,
                             hipStream_t st);

@@ -404,6 +404,52 @@ class KVPool:
             out.data_ptr(), code, ws.data_ptr(), ws.numel(), self._stream(stream)))
         return out
 
+    def decode_append_attention_windowed(self, layer: int, q, k_new, v_new, tables, lens, starts, window: int,
+                                         max_seq_len: int, scale: float, cos_sin=None, out_dtype=None, ws=None,
+                                         out=None, stream=None):
+        """The sliding layers' decode step in one launch: each sequence's newest
+        token (k_new / v_new [B, Hkv, 1, D], in_dtype) written at position
+        lens[b] - 1, then windowed attention of q [B, Hq, 1, D]; with cos_sin
+        (float32 [max_pos, D]) queries and new K rows turn by that position
+        first.  Same output and pool bytes as quantize_append(_rope) at the
+        reserved slots followed by attention_windowed."""
+        torch = _torch()
+        B, Hq, Lq, D = q.shape
+        if Lq != 1:
+            raise ValueError("the windowed decode step takes one query row per sequence")
+        self._check_dev("q", q, self.in_dtype)
+        Bt, mb = self._tables(tables, lens)
+        if Bt != B or D != self.head_dim:
+            raise ValueError("q batch/head_dim does not match the tables/pool")
+        H = self.num_kv_heads
+        for name, t in (("k_new", k_new), ("v_new", v_new)):
+            self._check_dev(name, t, self.in_dtype)
+            if t.numel() != B * H * D or t.shape[0] != B or t.shape[1] != H:
+                raise ValueError(f"{name} has shape {tuple(t.shape)}, expected [{B}, {H}, (1,) {D}]")
+        if starts is not None:
+            self._check_dev("starts", starts, torch.int32, (B,))
+        if cos_sin is not None:
+            self._check_dev("cos_sin", cos_sin, torch.float32)
+            if cos_sin.dim() != 2 or cos_sin.shape[1] != D:
+                raise ValueError(f"cos_sin must be [max_pos, {D}]")
+        out_dtype = torch.float32 if out_dtype is None else out_dtype
+        code = _dtype_code(out_dtype)
+        if out is None:
+            out = torch.empty((B, Hq, 1, D), dtype=out_dtype, device=q.device)
+        else:
+            self._check_dev("out", out, out_dtype, (B, Hq, 1, D))
+        need = ctypes.c_size_t()
+        L.check(L.lib().krill_window_workspace_size(self._h, B, Hq, 1, mb, max_seq_len, window, ctypes.byref(need)))
+        if ws is None or ws.numel() < need.value:
+            ws = torch.empty(max(need.value, 1), dtype=torch.uint8, device=q.device)
+        L.check(L.lib().krill_decode_append_attention_windowed(
+            self._h, layer, q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), H * D, D, tables.data_ptr(),
+            lens.data_ptr(), starts.data_ptr() if starts is not None else None, window, B, mb, max_seq_len, Hq,
+            float(scale), cos_sin.data_ptr() if cos_sin is not None else None,
+            int(cos_sin.shape[0]) if cos_sin is not None else 0, out.data_ptr(), code, ws.data_ptr(), ws.numel(),
+            self._stream(stream)))
+        return out
+
     def attention_shared_prefix(self, layer: int, q, prefix_table, suffix_tables, suffix_lens, max_suffix_len: int,
                                 scale: float, out_dtype=None, ws=None, out=None, stream=None, k_new=None,
                                 v_new=None):

@@ -221,3 +221,83 @@ def test_window_prefill_chunk_32_row_waves(mode):
     _check(pools, sl, W, Lq, mode, rng, R, tol_pair=1e-3)
     for p in pools:
         p.close()
+
+
+@pytest.mark.parametrize("rope", [False, True])
+@pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
+@pytest.mark.parametrize("D,R", [(128, 4), (256, 2)])
+def test_window_fused_decode_step(mode, D, R, rope):
+    """krill_decode_append_attention_windowed: the newest token written at
+    lens - 1 and windowed attention in one launch (with RoPE of the queries
+    and the new K row when rope) equals the two calls -- quantize-append
+    (_rope) at the reserved slot, then krill_attention_windowed on the
+    (oracle-rotated) queries -- in output and pool bytes, bit for bit, over
+    several steps with window trims; without RoPE also the oracle."""
+    from krill_amd.pool import rope_table
+
+    print(f"\ncase window_fused mode={mode} D={D} R={R} rope={rope}", flush=True)
+    W, H, B, steps = 100, 2, 3, 5
+    rng = np.random.default_rng(D + R + 7 * rope)
+    # two pools with the window option and the same block order
+    pools = []
+    for _ in range(2):
+        p = krill_amd.KVPool(1, H, D, 64, mode, DTS, free_list_seed=D)
+        p.set_option(krill_amd._lib.OPT_WINDOW, W)
+        pools.append(p)
+    fills = [[70, 64, 30], [5], [200, 3]]
+    sl = []
+    for pool in pools:
+        ss = Seqs(pool, B, 420, np.random.default_rng(7))
+        for b, chunks in enumerate(fills):
+            for L in chunks:
+                ss.append(b, L)
+        sl.append(ss)
+    cs = rope_table(512, D, 1.0e4)
+    csd = torch.from_numpy(cs).cuda()
+    scale = 1.0 / np.sqrt(D)
+    for step in range(steps):
+        q = rand_bits(rng, (B, H * R, 1, D), DTS)
+        pos = np.array([sl[0].len[b] for b in range(B)], np.int32)  # the new tokens' positions
+        # pool 0: two calls
+        p0, s0 = pools[0], sl[0]
+        slots = np.stack([p0.reserve_append(s0.seqs[b], 1) for b in range(B)]).astype(np.int32)
+        kn = np.stack([s0.k[b][:, pos[b]:pos[b] + 1] for b in range(B)])
+        vn = np.stack([s0.v[b][:, pos[b]:pos[b] + 1] for b in range(B)])
+        if rope:
+            p0.quantize_append_rope(0, to_dev(kn, DTS), to_dev(vn, DTS), i32(slots), i32(pos.reshape(B, 1)), csd)
+            qq = O.rope_rows(q, DT[DTS], np.broadcast_to(pos[:, None, None], (B, H * R, 1)), cs)
+        else:
+            p0.quantize_append(0, to_dev(kn, DTS), to_dev(vn, DTS), i32(slots))
+            qq = q
+        for b in range(B):
+            s0.len[b] += 1
+            s0.ops[b].append(("append", 1))
+        t0, n0, _ = s0.tables()
+        st0 = i32(p0.batch_starts(s0.seqs))
+        out_two = p0.attention_windowed(0, to_dev(qq, DTS), t0, n0, st0, W, int(max(s0.len)), scale)
+        # pool 1: the fused step
+        p1, s1 = pools[1], sl[1]
+        for b in range(B):
+            p1.reserve_append(s1.seqs[b], 1)
+            s1.len[b] += 1
+            s1.ops[b].append(("append", 1))
+        t1, n1, _ = s1.tables()
+        st1 = i32(p1.batch_starts(s1.seqs))
+        out_fused = p1.decode_append_attention_windowed(0, to_dev(q, DTS), to_dev(kn, DTS), to_dev(vn, DTS), t1, n1,
+                                                        st1, W, int(max(s1.len)), scale,
+                                                        cos_sin=csd if rope else None)
+        torch.cuda.synchronize()
+        assert torch.equal(out_two, out_fused), step
+        g0 = {k: v.cpu().numpy() for k, v in p0.gather(0, t0, n0, int(max(s0.len))).items()}
+        g1 = {k: v.cpu().numpy() for k, v in p1.gather(0, t1, n1, int(max(s1.len))).items()}
+        for k in g0:
+            np.testing.assert_array_equal(g0[k], g1[k])
+        if not rope:
+            got = out_fused.cpu().numpy()
+            for b in range(B):
+                total, start = O.rotating_retained_start(s1.ops[b], W)
+                want = _oracle_rows(s1, b, q[b], W, start, mode)
+                err = np.abs(got[b] - want).max()
+                assert err <= ATOL, (step, b, err)
+    for p in pools:
+        p.close()
