@@ -161,6 +161,8 @@ def parse():
     ap.add_argument("--workload", default="qwen3-14b-b32", choices=sorted(WORKLOADS))
     ap.add_argument("--quant", default="affine_g64", choices=["affine_g64", "ref_row"])
     ap.add_argument("--split-blocks", type=int, default=0)
+    ap.add_argument("--prefix-split", type=int, default=0,
+                    help="shared-prefix workload: prefix blocks per workgroup of the prefix pass (0 = automatic)")
     ap.add_argument("--wave-stamps", action="store_true",
                     help="add the last decode launch's wave timeline (needs KRILL_LIBRARY=libkrillhip_stamps.so)")
     ap.add_argument("--rope-fill", action="store_true",
@@ -212,6 +214,9 @@ class Env:
                                      free_list_seed=args.seed, **pool_kw)
         if args.split_blocks:
             self.pool.set_option(KL.OPT_SPLIT_BLOCKS, args.split_blocks)
+        if args.prefix_split:
+            self.pool.set_option(KL.OPT_PREFIX_SPLIT, args.prefix_split)
+
         self.lib = KL.lib()
         self.h = self.pool.handle
         self.stream = torch.cuda.current_stream()

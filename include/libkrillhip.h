@@ -72,6 +72,8 @@ extern "C" {
                                     sequence keeps its last window - 1 tokens and its blocks that hold none
                                     of them go back to the pool (RotatingKVCache.trimForAppend,
                                     RotatingKVCache.swift:70-75); for the pool of the sliding layers */
+#define KRILL_OPT_PREFIX_SPLIT 4 /* shared-prefix cascade: shared-prefix blocks per workgroup of its prefix
+                                    pass (1..64); 0 = automatic */
 
 typedef struct krill_pool *krill_pool_t;
 typedef void *krill_stream_t; /* hipStream_t */
@@ -126,8 +128,8 @@ int32_t krill_abi_version(void);
  * last decode-attention launch, from a library built with `make stamps`
  * (libkrillhip_stamps.so; the product build returns KRILL_E_UNSUPPORTED).
  * Copies up to max_waves rows of 6 words: realtime clock (100 MHz) at the
- * wave's start, first block ready, end, static part done; HW_ID | XCC_ID << 32;
- * static blocks | segments << 32.  Returns the rows copied. */
+ * wave's start, when its first block is in registers, and at its end; 0;
+ * HW_ID | XCC_ID << 32; blocks | segments << 32.  Returns the rows copied. */
 int32_t krill_diag_wave_stamps(uint64_t *out, int32_t max_waves);
 
 /* ---------------------------------------------------------------- pool */

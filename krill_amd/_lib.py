@@ -38,6 +38,7 @@ POOL_HOST_ONLY = 1
 OPT_SPLIT_BLOCKS = 1
 OPT_ATTN_PATH = 2
 OPT_WINDOW = 3
+OPT_PREFIX_SPLIT = 4
 
 _CODE_NAMES = {
     KRILL_E_INVAL: "KRILL_E_INVAL",

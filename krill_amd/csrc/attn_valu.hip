@@ -380,6 +380,14 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
     if (ss < iend) iend_eff = ss;  // the last sequence ends inside this range
   }
   const uint64_t tab_okm = __ballot(tab_ok);
+  // RoPE with the whole head in one wave: the cos/sin rows of the loaded
+  // sequence's query positions (row j: position qlen - Lq + j, Lq <= 8) are
+  // copied into LDS by direct loads issued right behind the queries, ahead of
+  // the first block's loads, so they land with that block instead of one
+  // memory round trip after it; finish_q and the newest token's RoPE read
+  // them there.
+  constexpr bool RSTAGE = ROPE && DS == 1;
+  __shared__ __attribute__((aligned(16))) float rope_lds[RSTAGE ? 8 * D : 1];
   __shared__ __attribute__((aligned(16))) uint8_t newrow_all[DS][2 * D];
   uint8_t *const newrow = newrow_all[wsl];  // the whole quantized row, per wave
   int patch_i = -1, patch_t = 0;  // flat block holding the segment's newest token, its position
@@ -392,12 +400,19 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
     if (!((tab_okm >> (f - i0)) & 1)) return;
     // RoPE turns the row by its absolute position (the window's view of a
     // sequence starts some whole blocks in)
+    // (staged: the token's position is the query position of this decode
+    // step, row 0 of the LDS copy; the queries of sequence bs are loaded)
     const int rpos = WIN ? len_of(a, bs) - 1 : len2 - 1;
+    const float *crow = nullptr;
+    if constexpr (ROPE) crow = RSTAGE ? rope_lds + (a.Lq - 1) * D : rope_row(a, rpos, D);
+    // the compiler does not order LDS reads after the direct loads into LDS
+    // (their data lands when vmcnt counts them done): wait for them here
+    if constexpr (RSTAGE) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (a.q_dtype == DT_BF16) {
-      if constexpr (ROPE) rope_row_lanes<D, DT_BF16>(rk, rope_row(a, rpos, D));
+      if constexpr (ROPE) rope_row_lanes<D, DT_BF16>(rk, crow);
       prepare_newest<D, MODE, DT_BF16>(rk, rv, newrow, pkm, pvm);
     } else {
-      if constexpr (ROPE) rope_row_lanes<D, DT_F16>(rk, rope_row(a, rpos, D));
+      if constexpr (ROPE) rope_row_lanes<D, DT_F16>(rk, crow);
       prepare_newest<D, MODE, DT_F16>(rk, rv, newrow, pkm, pvm);
     }
     patch_i = f;
@@ -474,16 +489,29 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
       for (int c = 0; c < DW / 32; ++c) qv[r][c] = qp[16 * c + (lane & 15)];
     }
     if constexpr (ROPE) qlen = WIN ? len_of(a, bq) : seq_len(bq);  // absolute positions
+    if constexpr (RSTAGE) {
+      const int64_t tb = (int64_t)a.rope_max_pos * D * 4;
+      const __amdgpu_buffer_rsrc_t rr =
+          block_rsrc(reinterpret_cast<const uint8_t *>(a.rope_cs), (int)(tb < INT32_MAX ? tb : INT32_MAX));
+      for (int j = 0; j < a.Lq; ++j) {
+        const int p = min(max(qlen - a.Lq + j, 0), a.rope_max_pos - 1);  // as rope_row clamps
+#pragma unroll
+        for (int c = 0; c < D / 64; ++c)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void_t *)(rope_lds + j * D + 64 * c), 4,
+                                                   (p * D + 64 * c + lane) * 4, 0, 0, 0);
+      }
+    }
     qseq = bq;
   };
   auto finish_q = [&]() {
     if constexpr (ROPE && DS == 1) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the staged cos/sin rows (see prepare)
       // row r (query position j = r / R, token qlen - Lq + j): pair words
       // 16 c + (lane & 15) of the first half turn with their partners
       // D/64 columns on
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
-        const float *crow = rope_row(a, qlen - a.Lq + r / a.R, D);
+        const float *crow = rope_lds + (r / a.R) * D;  // position qlen - Lq + r / R
 #pragma unroll
         for (int c = 0; c < D / 64; ++c) {
           const int d = 2 * (16 * c + (lane & 15));

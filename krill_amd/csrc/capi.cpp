@@ -27,6 +27,7 @@ struct krill_pool {
   bool host_only = false;
   int32_t opt_split_blocks = 0;
   int32_t opt_path = 0;
+  int32_t opt_prefix_split = 0;
   std::mutex flush_mu;
 };
 
@@ -284,6 +285,11 @@ int32_t krill_pool_set_option(krill_pool_t pool, int32_t option, int64_t value) 
       case KRILL_OPT_WINDOW:
         if (value < 0 || value > INT32_MAX / 4) return fail(KRILL_E_INVAL, "window %lld", static_cast<long long>(value));
         return pool->bm->set_window(static_cast<int32_t>(value));
+      case KRILL_OPT_PREFIX_SPLIT:
+        if (value < 0 || value > 64) return fail(KRILL_E_INVAL, "prefix split %lld", static_cast<long long>(value));
+        pool->opt_prefix_split = static_cast<int32_t>(value);
+        return KRILL_OK;
+
       default:
         return fail(KRILL_E_INVAL, "unknown option %d", option);
     }
@@ -746,8 +752,8 @@ static int32_t plan_shared_prefix(krill_pool_t pool, int32_t B, int32_t Hq, int3
                                   size_t *suffix_off, size_t *total) {
   if (B < 0 || prefix_blocks < 1 || max_suffix_len < 0) return fail(KRILL_E_INVAL, "bad B, prefix_blocks or length");
   if ((int64_t)prefix_blocks * 64 > INT32_MAX / 2) return fail(KRILL_E_RANGE, "prefix of %d blocks", prefix_blocks);
-  int32_t r = krill::plan_attention(pool->geom, 1, Hq, std::max(B, 1), prefix_blocks * 64, pool->opt_split_blocks, 0,
-                                    pp);
+  const int32_t psplit = pool->opt_prefix_split > 0 ? pool->opt_prefix_split : pool->opt_split_blocks;
+  int32_t r = krill::plan_attention(pool->geom, 1, Hq, std::max(B, 1), prefix_blocks * 64, psplit, 0, pp);
   if (r == 0)
     r = krill::plan_attention(pool->geom, B, Hq, 1, max_suffix_len, pool->opt_split_blocks, pool->opt_path, sp);
   if (r == -2) return fail(KRILL_E_UNSUPPORTED, "VALU path handles at most 8 query rows per KV head");

@@ -346,6 +346,12 @@ class KVPool:
         L.check(L.lib().krill_attention_workspace_size(self._h, B, Hq, Lq, max_seq_len, ctypes.byref(out)))
         return out.value
 
+    def shared_prefix_workspace_size(self, B: int, Hq: int, prefix_blocks: int, max_suffix_len: int) -> int:
+        out = ctypes.c_size_t()
+        L.check(L.lib().krill_shared_prefix_workspace_size(self._h, B, Hq, prefix_blocks, max_suffix_len,
+                                                           ctypes.byref(out)))
+        return out.value
+
     def attention(self, layer: int, q, tables, lens, max_seq_len: int, scale: float, out_dtype=None,
                   ws=None, out=None, stream=None):
         """q: [B, Hq, Lq, D] in in_dtype.  Lq == 1 is decode, Lq > 1 verify/chunked prefill."""

@@ -186,3 +186,61 @@ def test_shared_prefix_f16_inputs():
     got, single, ref = _case("affine_g64", 128, 2, 5, 200, [0, 9, 130], dt="f16", seed=17)
     assert np.abs(got - ref).max() <= ATOL
     assert np.abs(got - single).max() <= _single_tol(3, 5)
+
+
+@pytest.mark.parametrize("prefix_split", [0, 4, 8])
+def test_shared_prefix_prefix_split(prefix_split):
+    """KRILL_OPT_PREFIX_SPLIT (shared-prefix blocks per workgroup of the
+    prefix pass): the 65-block prefix of a Llama-3-8B-shaped batch over fewer,
+    longer workgroups gives the same output call after call and stays within
+    the oracle tolerance."""
+    print(f"\ncase shared_prefix_split prefix_split={prefix_split}", flush=True)
+    D, H, R, prefix_tokens, extra = 128, 8, 4, 4120, [0, 3, 64, 130, 900, 17, 1000, 2]
+    pool, rng, joined = _forked("affine_g64", D, H, prefix_tokens, extra, "bf16", seed=61)
+    P, B = prefix_tokens // 64, len(extra)
+    mb = (prefix_tokens + max(extra) + 63) // 64
+    ptab, stab, slen, smax = _split_tables(pool, joined.seqs, P, mb)
+    q = rand_bits(rng, (B, H * R, 1, D), "bf16")
+    qd = to_dev(q, "bf16")
+    L = krill_amd._lib
+    pool.set_option(L.OPT_PREFIX_SPLIT, prefix_split)
+    outs = []
+    for _ in range(2):
+        outs.append(pool.attention_shared_prefix(0, qd, ptab, stab, slen, smax, 0.1))
+        torch.cuda.synchronize()
+    ref = oracle_attention(pool, joined, 0, q, "bf16", 0.1)
+    pool.close()
+    assert torch.equal(outs[0], outs[1])
+    err = np.abs(outs[1].cpu().numpy() - ref).max()
+    print(f"max abs error {err:.3e}", flush=True)
+    assert err <= ATOL
+
+
+def test_shared_prefix_graph_replays_match_eager():
+    """A cascade call (prefix pass, suffix pass, merge) captured in a HIP
+    graph on a side stream and replayed three times, with eager work and
+    synchronizations between the replays: every replay equals the eager call
+    bit for bit."""
+    print("\ncase shared_prefix_graph", flush=True)
+    D, H, R, prefix_tokens, extra = 128, 4, 4, 1000, [5, 300, 0, 77]
+    pool, rng, joined = _forked("affine_g64", D, H, prefix_tokens, extra, "bf16", seed=67)
+    P, B = prefix_tokens // 64, len(extra)
+    mb = (prefix_tokens + max(extra) + 63) // 64
+    ptab, stab, slen, smax = _split_tables(pool, joined.seqs, P, mb)
+    qd = to_dev(rand_bits(rng, (B, H * R, 1, D), "bf16"), "bf16")
+    ws = torch.empty(max(pool.shared_prefix_workspace_size(B, H * R, P, smax), 1), dtype=torch.uint8, device="cuda")
+    out_e = pool.attention_shared_prefix(0, qd, ptab, stab, slen, smax, 0.1, ws=ws)
+    torch.cuda.synchronize()
+    out_g = torch.empty_like(out_e)
+    g = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    with torch.cuda.graph(g, stream=cap):
+        pool.attention_shared_prefix(0, qd, ptab, stab, slen, smax, 0.1, ws=ws, out=out_g)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        torch.randn(1 << 20, device="cuda").sum().item()
+        out_g.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, out_e), rep
+    pool.close()
