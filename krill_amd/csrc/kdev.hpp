@@ -395,15 +395,35 @@ __device__ __forceinline__ uint8_t affine_q(float w, float s, float bias) {
 // boundary of the step that follows (k + 1/2 for rint, k for truncation)
 // both round to the same integer; otherwise the exact division decides.
 // (About 2^-11 of uniformly spread quotients take the division.)
-__device__ __forceinline__ uint8_t affine_q_r(float w, float s, float bias, float r) {
-  const float a = w - bias;
-  const float y = a * r;
-  float n = rintf(y);
-  // y - n is exact (|y - n| <= 1/2 and n = rint(y))
-  if (!(fabsf(y) < 512.0f && fabsf(y - n) < 0.5f - 0x1p-12f)) n = rintf(a / s);
-  if (n > 255.0f) n = 255.0f;
-  if (n < 0.0f) n = 0.0f;
-  return (uint8_t)(uint32_t)n;
+
+// affine_q for four elements (byte e = element e of the word), with the
+// division y = (w - bias) / s done as (w - bias) * r, r = v_rcp_f32(s),
+// wherever that provably gives the same byte.  Off a rounding tie (ties sit
+// at k + 1/2, at distance |fract(y) - 1/2|) by more than 2^-12, rint(y) =
+// floor(y + 1/2), which v_cvt_rpi_i32_f32 gives as an integer in one step
+// (y + 1/2 is exact for |y| < 512), clamped as an integer.  No branch per
+// element: when any of the four is near a tie (or |y| >= 512, or NaN) all
+// four take the exact division, which gives the same bytes where the fast
+// path held.
+__device__ __forceinline__ uint32_t affine_q4(const float (&w)[4], float s, float bias, float r) {
+  float a[4];
+  int n[4];
+  int ok = 1;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    a[e] = w[e] - bias;
+    const float y = a[e] * r;
+    asm("v_cvt_rpi_i32_f32 %0, %1" : "=v"(n[e]) : "v"(y));
+    ok &= (int)(fabsf(y) < 512.0f) & (int)(fabsf(__builtin_amdgcn_fractf(y) - 0.5f) > 0x1p-12f);
+  }
+  if (!ok) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) n[e] = (int)rintf(a[e] / s);
+  }
+  uint32_t q = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) q |= (uint32_t)min(max(n[e], 0), 255) << (8 * e);
+  return q;
 }
 template <int DT>
 __device__ __forceinline__ uint8_t ref_q_r(float x, float mn, float safe, float r) {

@@ -197,13 +197,19 @@ __global__ __launch_bounds__(256) void k_quantize_append_blocks(LayerView lv, co
     if (r >= nrows || slot < 0 || (slot >> 6) >= lv.num_blocks) continue;
     if (ROPE && (unsigned)p >= (unsigned)rope.max_pos) continue;
     const int t = slot & 63;
-    // K with RoPE: the group's rotated elements from the LDS copy
-    const uint16_t *src = (ROPE && kv == 0)
-                              ? krot + r * D + g * GE
-                              : (kv ? v : k) + (int64_t)b * sb + (int64_t)h * sh + (int64_t)(l0 + r) * sl + g * GE;
+    // K with RoPE: the group's rotated elements from the LDS copy (a branch
+    // of its own, `kv` being the same for the whole wave: a pointer selected
+    // between LDS and global memory would make every load a flat load)
     uint4 raw[GE / 8];
+    if (ROPE && kv == 0) {
+      const uint16_t *src = krot + r * D + g * GE;
 #pragma unroll
-    for (int c = 0; c < GE / 8; ++c) raw[c] = *reinterpret_cast<const uint4 *>(src + 8 * c);
+      for (int c = 0; c < GE / 8; ++c) raw[c] = *reinterpret_cast<const uint4 *>(src + 8 * c);
+    } else {
+      const uint16_t *src = (kv ? v : k) + (int64_t)b * sb + (int64_t)h * sh + (int64_t)(l0 + r) * sl + g * GE;
+#pragma unroll
+      for (int c = 0; c < GE / 8; ++c) raw[c] = *reinterpret_cast<const uint4 *>(src + 8 * c);
+    }
     auto elem = [&](int e) -> float {
       const uint4 w = raw[e >> 3];
       const uint32_t u = ((e & 7) >> 1) == 0 ? w.x : ((e & 7) >> 1) == 1 ? w.y : ((e & 7) >> 1) == 2 ? w.z : w.w;
@@ -230,22 +236,37 @@ __global__ __launch_bounds__(256) void k_quantize_append_blocks(LayerView lv, co
       scale = safe;
       zero = mn + 0.0f;  // a zero minimum is stored as +0 (min over +-0 depends on order)
     } else {
-      float wmin = affine_w<DT>(elem(0)), wmax = wmin;
+      // The group's elements rounded to fp16 (affine_w) are fp16 values: kept
+      // as packed pairs (no second conversion for the quantize pass), their
+      // minimum and maximum taken two at a time.
+      half2_t wp[GE / 2];
 #pragma unroll
-      for (int e = 1; e < GE; ++e) {
-        const float w = affine_w<DT>(elem(e));
-        wmin = fminf(wmin, w);
-        wmax = fmaxf(wmax, w);
+      for (int c = 0; c < GE / 8; ++c) {
+        const uint32_t u4[4] = {raw[c].x, raw[c].y, raw[c].z, raw[c].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          wp[4 * c + j] = DT == DT_F16 ? u32_as_h2(u4[j])
+                                       : half2_t{(_Float16)__builtin_bit_cast(float, u4[j] << 16),
+                                                 (_Float16)__builtin_bit_cast(float, u4[j] & 0xffff0000u)};
       }
+      half2_t mn2 = wp[0], mx2 = wp[0];
+#pragma unroll
+      for (int i = 1; i < GE / 2; ++i) {
+        mn2 = __builtin_elementwise_min(mn2, wp[i]);
+        mx2 = __builtin_elementwise_max(mx2, wp[i]);
+      }
+      const float wmin = fminf((float)mn2[0], (float)mn2[1]), wmax = fmaxf((float)mx2[0], (float)mx2[1]);
+      // the packed values stay in registers for the second pass (the
+      // compiler would otherwise redo both conversions per element there)
+#pragma unroll
+      for (int i = 0; i < GE / 2; ++i) asm volatile("; keep %0" : "+v"(wp[i]));
       affine_params(wmin, wmax, scale, zero);
       const float rs = __builtin_amdgcn_rcpf(scale);
 #pragma unroll
       for (int c = 0; c < GE / 4; ++c) {
-        uint32_t wv = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          wv |= (uint32_t)affine_q_r(affine_w<DT>(elem(4 * c + e)), scale, zero, rs) << (8 * e);
-        qw[c] = wv;
+        const half2_t p0 = wp[2 * c], p1 = wp[2 * c + 1];
+        const float w4[4] = {(float)p0[0], (float)p0[1], (float)p1[0], (float)p1[1]};
+        qw[c] = affine_q4(w4, scale, zero, rs);
       }
     }
     uint8_t *reg = head_region(lv, slot >> 6, h);
@@ -259,11 +280,19 @@ __global__ __launch_bounds__(256) void k_quantize_append_blocks(LayerView lv, co
       // V: into the LDS image of the block's V region or straight to the block.
       // Offsets are taken relative to the V region (v_byte - v_offset, in
       // [0, 64 D)): an LDS pointer moved below its array would wrap in the
-      // 32-bit LDS address space before its conversion to a flat address.
-      uint8_t *vdst = fast ? img[r < nA ? 0 : 1] : reg + v_offset(D);
+      // 32-bit LDS address space.  The two destinations stay in separate
+      // branches (`fast` is uniform): one pointer selected between them would
+      // be a generic address, and every byte would go out as a flat store
+      // through the vector-memory path instead of an LDS write.
+      if (fast) {
+        uint8_t *vimg = img[r < nA ? 0 : 1];
 #pragma unroll
-      for (int e = 0; e < GE; ++e)
-        vdst[v_byte(D, t, d0 + e) - v_offset(D)] = (uint8_t)(qw[e >> 2] >> (8 * (e & 3)));
+        for (int e = 0; e < GE; ++e) vimg[v_byte(D, t, d0 + e) - v_offset(D)] = (uint8_t)(qw[e >> 2] >> (8 * (e & 3)));
+      } else {
+        uint8_t *vdst = reg + v_offset(D);
+#pragma unroll
+        for (int e = 0; e < GE; ++e) vdst[v_byte(D, t, d0 + e) - v_offset(D)] = (uint8_t)(qw[e >> 2] >> (8 * (e & 3)));
+      }
     }
     const uint32_t meta = (uint32_t)f32_to_f16_bits(scale) | ((uint32_t)f32_to_f16_bits(zero) << 16);
     *reinterpret_cast<uint32_t *>(reg + (kv ? vm_offset(D, G) : km_offset(D)) + ((t * G + g) << 2)) = meta;
