@@ -151,6 +151,35 @@ constexpr int valu_waves_per_simd() {
   return D <= 64 || (D == 128 && NR <= 5) ? 3 : 2;
 }
 
+// Sliding-window launches with the whole head in one wave (VAR 2 and 3,
+// head_dim <= 256): a window keeps every sequence short and about equally
+// long, so instead of the flat split each (sequence, KV head) gets one
+// workgroup whose waves split that sequence's blocks and combine their
+// partials in LDS after a barrier -- no merge launch.  Waves per workgroup:
+// what a compute unit holds of the kernel (8 at two waves per SIMD, 6 at
+// three, 8 at four), halved while the waves' LDS (scaled weights, V scale
+// pairs, the new row, the RoPE row, the partial) exceeds 64 KB; 0 for the
+// flat split.
+template <int D, int NR, int MODE, int VAR>
+constexpr int seq_waves() {
+  if constexpr (!(VAR == 2 || VAR == 3) || D > 256) {
+    return 0;
+  } else {
+    constexpr int GW = MODE == MODE_AFFINE ? D / 64 : 1;
+    constexpr int pwb = NR * GW * 64 * 4 + 2 * 64 * 2 + 2 * D + (VAR == 3 ? 4 * D : 0) + NR * (D + 4) * 4;
+    constexpr int wps = valu_waves_per_simd<D, NR>();
+    int w = wps == 3 ? 6 : 8;
+    while (w > 1 && w * pwb > 64 * 1024) w /= 2;
+    return w;
+  }
+}
+// Most blocks of one sequence a windowed workgroup's wave may read (one VGPR
+// of block-table entries per wave).
+template <int D, int NR, int MODE, int VAR>
+constexpr int seq_max_blocks() {
+  return 64 * seq_waves<D, NR, MODE, VAR>();
+}
+
 // LDS written and read by the lanes of one wave only: a wave's LDS
 // operations complete in order, so waiting for its outstanding ones (and
 // keeping the compiler from moving memory operations across) orders the
@@ -252,9 +281,14 @@ __device__ __forceinline__ void store_newest(const AttnArgs &a, int hk, int phys
 // [DW w, DW w + DW); the query rows of a KV head in row groups of NR rows
 // (blockIdx.z), each its own flat block order and partial slots.
 template <int D, int NR, int MODE, int VAR>
-__global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>())) void k_attn_valu(AttnArgs a) {
+__global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves<D, NR, MODE, VAR>() : d_slices<D>()),
+                             (valu_waves_per_simd<D, NR>())) void k_attn_valu(AttnArgs a) {
   constexpr bool ROPE = VAR == 1 || VAR == 3, WIN = VAR == 2 || VAR == 3;
   constexpr int DS = d_slices<D>();  // waves per workgroup, one per d-slice
+  // windowed: one workgroup per (sequence, KV head), partials merged in LDS
+  constexpr int SW = seq_waves<D, NR, MODE, VAR>();
+  constexpr bool SEQ = SW > 0;
+  constexpr int NWV = SEQ ? SW : DS;  // waves with LDS of their own
   constexpr int DW = D / DS;         // dims of one wave
   constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;    // scale groups per token (pool layout)
   constexpr int GW = MODE == MODE_AFFINE ? DW / 64 : 1;  // the wave's scale groups
@@ -267,15 +301,19 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
   constexpr bool PVM = pv_on_mfma<D, NR>();
   constexpr bool LOAD_TOGETHER = !PVM && valu_waves_per_simd<D, NR>() >= 3;  // next block's loads in one pass
 
-  __shared__ __attribute__((aligned(16))) float w_lds_all[DS][NR * GW * 64];
-  __shared__ __attribute__((aligned(16))) uint16_t sz_lds_all[DS][2 * 64];
+  __shared__ __attribute__((aligned(16))) float w_lds_all[NWV][NR * GW * 64];
+  __shared__ __attribute__((aligned(16))) uint16_t sz_lds_all[NWV][2 * 64];
+  // windowed: each wave's partial -- row r: o at r (D + 4), then m, l
+  constexpr int PST = D + 4;
+  __shared__ __attribute__((aligned(16))) float part_lds[SEQ ? SW : 1][SEQ ? NR * PST : 4];
   // the slices' partial scores, two buffers (block parity)
   __shared__ __attribute__((aligned(16))) float sc_lds[DS > 1 ? 2 : 1][DS][DS > 1 ? NR * 64 : 1];
 
-  const int lane = DS > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
+  const int lane = DS > 1 || SEQ ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
   const int wsl = DS > 1 ? (int)(threadIdx.x >> 6) : 0;  // this wave's d-slice
-  float *const w_lds = w_lds_all[wsl];
-  uint16_t *const sz_lds = sz_lds_all[wsl];
+  const int wid = SEQ ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;  // wave of the workgroup
+  float *const w_lds = w_lds_all[SEQ ? wid : wsl];
+  uint16_t *const sz_lds = sz_lds_all[SEQ ? wid : wsl];
   const int p0 = wsl * NP;                             // first K piece of the slice
   const int g0 = MODE == MODE_AFFINE ? wsl * GW : 0;   // first scale group of the slice
   const int rg = DS > 1 ? (int)blockIdx.z : 0;         // row group
@@ -316,11 +354,35 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
   // At most T waves take part, so every participating wave holds at least
   // one block (the merge relies on it: each wave between a sequence's first
   // and last writes that sequence's partial).
+  // Windowed (SEQ): the workgroup's sequence blockIdx.x, split evenly over
+  // its SW waves; a wave without blocks still leaves an (empty) partial.
+  int i0 = 0, iend = 0;
+  int b = -1, s = 0;  // sequence holding block i0 and the flat index of its first block
+  if constexpr (SEQ) {
+    const int bq = (int)blockIdx.x;
+    int carry = 0;
+    for (c0 = 0; c0 < a.B; c0 += 64) {
+      if (c0 > 0) {
+        const int bb = c0 + lane;
+        lenv = bb < a.B ? seq_len_view<WIN>(a, bb) : 0;
+        nbv = nblk(lenv);
+        incl = wave_incl_scan(nbv) + carry;
+      }
+      if (bq < c0 + 64) {
+        s = __builtin_amdgcn_readlane(incl - nbv, bq - c0);
+        break;
+      }
+      carry = __builtin_amdgcn_readlane(incl, 63);
+    }
+    b = bq;
+    const int nbq = nblk(__builtin_amdgcn_readlane(lenv, bq - c0));
+    i0 = s + (wid * nbq + SW - 1) / SW;
+    iend = s + ((wid + 1) * nbq + SW - 1) / SW;
+  } else {
   const int Wt = min(W, T);
   if (wv >= Wt) return;
-  const int i0 = (int)(((int64_t)wv * T + Wt - 1) / Wt);
-  const int iend = (int)(((int64_t)(wv + 1) * T + Wt - 1) / Wt);
-  int b = -1, s = 0;  // sequence holding block i0 and the flat index of its first block
+  i0 = (int)(((int64_t)wv * T + Wt - 1) / Wt);
+  iend = (int)(((int64_t)(wv + 1) * T + Wt - 1) / Wt);
   {
     int carry = 0;
     for (c0 = 0; c0 < a.B; c0 += 64) {
@@ -341,6 +403,7 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
     }
   }
   if (b < 0) return;
+  }
   auto seq_len = [&](int bs) -> int { return bs - c0 < 64 ? __builtin_amdgcn_readlane(lenv, bs - c0) : seq_len_view<WIN>(a, bs); };
 
   // Decode step with the append fused: the wave that reads a sequence's last
@@ -387,9 +450,11 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
   // memory round trip after it; finish_q and the newest token's RoPE read
   // them there.
   constexpr bool RSTAGE = ROPE && DS == 1;
-  __shared__ __attribute__((aligned(16))) float rope_lds[RSTAGE ? 8 * D : 1];
-  __shared__ __attribute__((aligned(16))) uint8_t newrow_all[DS][2 * D];
-  uint8_t *const newrow = newrow_all[wsl];  // the whole quantized row, per wave
+  // (windowed workgroups: one row per wave, the RoPE step being a decode step)
+  __shared__ __attribute__((aligned(16))) float rope_lds[RSTAGE ? (SEQ ? SW : 8) * D : 1];
+  float *const rope_w = rope_lds + (SEQ && RSTAGE ? wid * D : 0);
+  __shared__ __attribute__((aligned(16))) uint8_t newrow_all[NWV][2 * D];
+  uint8_t *const newrow = newrow_all[SEQ ? wid : wsl];  // the whole quantized row, per wave
   int patch_i = -1, patch_t = 0;  // flat block holding the segment's newest token, its position
   uint32_t pkm[G], pvm[G];
 #pragma unroll
@@ -404,7 +469,7 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
     // step, row 0 of the LDS copy; the queries of sequence bs are loaded)
     const int rpos = WIN ? len_of(a, bs) - 1 : len2 - 1;
     const float *crow = nullptr;
-    if constexpr (ROPE) crow = RSTAGE ? rope_lds + (a.Lq - 1) * D : rope_row(a, rpos, D);
+    if constexpr (ROPE) crow = RSTAGE ? rope_w + (a.Lq - 1) * D : rope_row(a, rpos, D);
     // the compiler does not order LDS reads after the direct loads into LDS
     // (their data lands when vmcnt counts them done): wait for them here
     if constexpr (RSTAGE) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -493,11 +558,11 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
       const int64_t tb = (int64_t)a.rope_max_pos * D * 4;
       const __amdgpu_buffer_rsrc_t rr =
           block_rsrc(reinterpret_cast<const uint8_t *>(a.rope_cs), (int)(tb < INT32_MAX ? tb : INT32_MAX));
-      for (int j = 0; j < a.Lq; ++j) {
+      for (int j = 0; j < (SEQ ? 1 : a.Lq); ++j) {
         const int p = min(max(qlen - a.Lq + j, 0), a.rope_max_pos - 1);  // as rope_row clamps
 #pragma unroll
         for (int c = 0; c < D / 64; ++c)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void_t *)(rope_lds + j * D + 64 * c), 4,
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void_t *)(rope_w + j * D + 64 * c), 4,
                                                    (p * D + 64 * c + lane) * 4, 0, 0, 0);
       }
     }
@@ -511,7 +576,7 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
       // D/64 columns on
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
-        const float *crow = rope_lds + (r / a.R) * D;  // position qlen - Lq + r / R
+        const float *crow = rope_w + (r / a.R) * D;  // position qlen - Lq + r / R
 #pragma unroll
         for (int c = 0; c < D / 64; ++c) {
           const int d = 2 * (16 * c + (lane & 15));
@@ -836,8 +901,11 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
       sz_lds[pos] = valid ? (uint16_t)(vm[0] & 0xffffu) : (uint16_t)0;
       sz_lds[64 + pos] = valid ? (uint16_t)(vm[0] >> 16) : (uint16_t)0;
     }
-    if constexpr (DS > 1)
-      wave_lds_sync();  // each wave has its own weights
+    // (each wave has its own weights; a workgroup barrier here would pair up
+    // with other waves' barriers once the waves of a windowed workgroup,
+    // whose block counts differ, leave the loop at different times)
+    if constexpr (DS > 1 || SEQ)
+      wave_lds_sync();
     else
       __syncthreads();
     if constexpr (PVM) {
@@ -1033,7 +1101,7 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
       km[g] = km_next[g];
       vm[g] = vm_next[g];
     }
-    if constexpr (DS > 1)
+    if constexpr (DS > 1 || SEQ)
       wave_lds_sync();
     else
       __syncthreads();
@@ -1079,11 +1147,11 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
     // 4 DPL consecutive d: d = DPL (16 k + q4 + j) + e for j < 4, e < DPL
     // (k counted over the whole row: the slice's tiles start at dt0).
     if (n < NR) {
-      const bool whole = !a.partial_only && s >= i0 && e <= iend;
+      const bool whole = !SEQ && !a.partial_only && s >= i0 && e <= iend;
       const float mul = !whole ? 1.0f : lsum_n > 0.0f ? 1.0f / lsum_n : 0.0f;
       const int64_t hslot = DS > 1 ? (int64_t)hk * a.row_groups + rg : (int64_t)hk;
       const int64_t pi = (hslot * (a.waves + a.B) + wv + b) * NR + n;
-      const int64_t ob = whole ? out_row_base(a, b, hk, r0 + n, D) : pi * D;
+      const int64_t ob = whole ? out_row_base(a, b, hk, r0 + n, D) : SEQ ? (int64_t)n * PST : pi * D;
 #pragma unroll
       for (int k = 0; k < ND / DPL; ++k) {
         float run[4 * DPL];
@@ -1091,10 +1159,17 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
         for (int j2 = 0; j2 < 4; ++j2)
 #pragma unroll
           for (int e2 = 0; e2 < DPL; ++e2) run[DPL * j2 + e2] = acc[DPL * k + e2][j2] * mul;
-        store_run<4 * DPL>(whole ? a.out : (void *)a.ws_o, ob + DPL * (16 * (dt0 / DPL + k) + q4), run,
-                           whole ? a.out_dtype : DT_F32);
+        store_run<4 * DPL>(SEQ ? (void *)part_lds[wid] : whole ? a.out : (void *)a.ws_o,
+                           ob + DPL * (16 * (dt0 / DPL + k) + q4), run, whole ? a.out_dtype : DT_F32);
       }
-      if (!whole && lane < 16 && wsl == 0) reinterpret_cast<float2 *>(a.ws_ml)[pi] = float2{m_n, lsum_n};
+      if constexpr (SEQ) {
+        if (lane < 16) {
+          part_lds[wid][n * PST + D] = m_n;
+          part_lds[wid][n * PST + D + 1] = lsum_n;
+        }
+      } else if (!whole && lane < 16 && wsl == 0) {
+        reinterpret_cast<float2 *>(a.ws_ml)[pi] = float2{m_n, lsum_n};
+      }
     }
     } else {
     // ---- end of the segment: the whole sequence in this wave -> output;
@@ -1114,7 +1189,17 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
 #pragma unroll
       for (int e2 = 0; e2 < DPL; ++e2) accv[r][e2] += cg;
     }
-    if (!a.partial_only && s >= i0 && e <= iend) {
+    if constexpr (SEQ) {
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+#pragma unroll
+        for (int e2 = 0; e2 < DPL; ++e2) part_lds[wid][r * PST + DPL * lane + e2] = accv[r][e2];
+        if (lane == 0) {
+          part_lds[wid][r * PST + D] = m_run[r];
+          part_lds[wid][r * PST + D + 1] = lsum[r];
+        }
+      }
+    } else if (!a.partial_only && s >= i0 && e <= iend) {
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
         const float inv = lsum[r] > 0.0f ? 1.0f / lsum[r] : 0.0f;
@@ -1153,12 +1238,36 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
     }
     finish_q();
   }
+  if constexpr (SEQ) {
+    // Every wave's partial of the sequence is in LDS: wave w combines rows
+    // w, w + SW, ... (the softmax merge of k_attn_merge_flat over the SW
+    // partials in wave order; a wave without blocks left m = -inf, l = 0)
+    // and writes them out.
+    __syncthreads();
+    for (int r = wid; r < NR; r += SW) {
+      const float mk = lane < SW ? part_lds[lane][r * PST + D] : -INFINITY;
+      const float lk = lane < SW ? part_lds[lane][r * PST + D + 1] : 0.0f;
+      const float M = uniform_f32(wave_allmax(mk));
+      const float wk = lane < SW && mk != -INFINITY ? fast_exp2(mk - M) : 0.0f;
+      const float L = uniform_f32(wave_allsum(wk * lk));
+      const float inv = (M == -INFINITY || !(L > 0.0f)) ? 0.0f : 1.0f / L;
+      const int64_t ob = out_row_base(a, b, hk, r, D);
+#pragma unroll
+      for (int e2 = 0; e2 < DPL; ++e2) {
+        const int d = lane + 64 * e2;
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < SW; ++k) acc += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k)) * part_lds[k][r * PST + d];
+        store_out(a.out, ob + d, acc * inv, a.out_dtype);
+      }
+    }
+  }
 #ifdef KRILL_WAVE_STAMPS
   {
     const unsigned long long t2 = __builtin_amdgcn_s_memrealtime();
     const unsigned hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);    // HW_REG_HW_ID
     const unsigned xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);  // HW_REG_XCC_ID
-    const int64_t idx = ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    const int64_t idx = (((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * (SEQ ? SW : 1) + wid;
     if (lane == 0 && wsl == 0 && idx < kStampWaves) {
       unsigned long long *o = g_wave_stamps + idx * 6;
       o[0] = st_t0;
@@ -1175,16 +1284,29 @@ __global__ __launch_bounds__(64 * d_slices<D>(), (valu_waves_per_simd<D, NR>()))
 template <int D, int MODE, int NR>
 static hipError_t launch_one(const AttnArgs &args, int B, dim3 grid, hipStream_t st) {
   const dim3 block(64 * d_slices<D>());
+  // windowed, whole head per wave: one workgroup of seq_waves per (sequence,
+  // KV head), each wave at most 64 of the sequence's blocks
+  auto seq_launch = [&](auto var) -> bool {
+    constexpr int SW = seq_waves<D, NR, MODE, decltype(var)::value>();
+    if constexpr (SW > 0) {
+      if (args.nb_cap > 64 * SW) return false;
+      k_attn_valu<D, NR, MODE, decltype(var)::value><<<dim3((unsigned)B, grid.y, 1), dim3(64 * SW), 0, st>>>(args);
+    } else {
+      k_attn_valu<D, NR, MODE, decltype(var)::value><<<grid, block, 0, st>>>(args);
+    }
+    return true;
+  };
   if (args.rope_cs && args.window > 0) {
     // sliding-window layers with RoPE: head_dim <= 256
-    if constexpr (D <= 256)
-      k_attn_valu<D, NR, MODE, 3><<<grid, block, 0, st>>>(args);
-    else
+    if constexpr (D <= 256) {
+      if (!seq_launch(std::integral_constant<int, 3>{})) return hipErrorInvalidValue;
+    } else {
       return hipErrorInvalidValue;
+    }
   } else if (args.rope_cs) {
     k_attn_valu<D, NR, MODE, 1><<<grid, block, 0, st>>>(args);
   } else if (args.window > 0) {
-    k_attn_valu<D, NR, MODE, 2><<<grid, block, 0, st>>>(args);
+    if (!seq_launch(std::integral_constant<int, 2>{})) return hipErrorInvalidValue;
   } else {
     k_attn_valu<D, NR, MODE, 0><<<grid, block, 0, st>>>(args);
   }
@@ -1253,6 +1375,29 @@ int32_t valu_waves_per_cu(const PoolGeometry &g, int32_t NR) {
     c = n;
   }
   return c;
+}
+
+// Longest windowed view (tokens) the decode kernel's per-sequence workgroups
+// take at head_dim <= 256 (64 blocks per wave); 0 where the flat split runs.
+template <int D, int MODE>
+static int32_t window_limit_nr(int NR, bool rope) {
+  switch (NR) {
+#define KRILL_WL(N)                                                                        \
+  case N:                                                                                  \
+    return 64 * (rope ? seq_max_blocks<D, N, MODE, 3>() : seq_max_blocks<D, N, MODE, 2>());
+    KRILL_WL(1) KRILL_WL(2) KRILL_WL(3) KRILL_WL(4) KRILL_WL(5) KRILL_WL(6) KRILL_WL(7) KRILL_WL(8)
+#undef KRILL_WL
+    default: return 0;
+  }
+}
+int32_t valu_window_limit(const PoolGeometry &g, int32_t NR, bool rope) {
+  const bool aff = g.mode == MODE_AFFINE;
+  switch (g.D) {
+    case 64: return aff ? window_limit_nr<64, MODE_AFFINE>(NR, rope) : window_limit_nr<64, MODE_REF>(NR, rope);
+    case 128: return aff ? window_limit_nr<128, MODE_AFFINE>(NR, rope) : window_limit_nr<128, MODE_REF>(NR, rope);
+    case 256: return aff ? window_limit_nr<256, MODE_AFFINE>(NR, rope) : window_limit_nr<256, MODE_REF>(NR, rope);
+    default: return 0;
+  }
 }
 
 // Copies the stamps of the last decode launch (diagnostic build), up to

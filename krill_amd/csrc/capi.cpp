@@ -942,6 +942,15 @@ static int32_t run_windowed(krill_pool_t pool, int32_t layer, const void *dev_q,
                 "KV head (call krill_quantize_append, then krill_attention_windowed)");
   if (nt.rope_cs && pool->geom.D > 256)
     return fail(KRILL_E_UNSUPPORTED, "windowed RoPE step at head_dim %d (at most 256)", pool->geom.D);
+  const int64_t view = std::min<int64_t>(max_seq_len, (int64_t)Lq + window + 62);
+  if (!plan.use_mfma && pool->geom.D <= 256) {
+    // the decode kernel's per-sequence workgroups: at most 64 blocks per wave
+    const int32_t lim = krill::valu_window_limit(pool->geom, plan.NR, nt.rope_cs != nullptr);
+    if (view > lim)
+      return fail(KRILL_E_UNSUPPORTED, "window of %d tokens: the windowed decode kernel reads at most %d tokens per "
+                  "sequence with %d query rows per KV head (KRILL_OPT_ATTN_PATH 2 runs the MFMA kernel instead)",
+                  window, lim, plan.NR);
+  }
   if (ws_bytes < total || (total > 0 && !dev_ws))
     return fail(KRILL_E_INVAL, "workspace of %zu bytes < %zu required", ws_bytes, total);
   krill::AttnLaunch a;
@@ -950,7 +959,7 @@ static int32_t run_windowed(krill_pool_t pool, int32_t layer, const void *dev_q,
   a.lens = dev_seq_lens;
   a.B = B;
   a.max_blocks = max_blocks;
-  a.max_seq_len = (int32_t)std::min<int64_t>(max_seq_len, (int64_t)Lq + window + 62);
+  a.max_seq_len = (int32_t)view;
   a.Hq = Hq;
   a.Lq = Lq;
   a.scale = scale;

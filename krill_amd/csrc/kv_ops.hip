@@ -1238,6 +1238,8 @@ hipError_t launch_attention(const PoolGeometry &g, int32_t layer, const AttnLaun
   }
   hipError_t e = p.use_mfma ? launch_attn_mfma(g, layer, a, p, st) : launch_attn_valu(g, layer, a, p, st);
   if (e != hipSuccess) return e;
+  // windowed decode kernel at head_dim <= 256: merged inside its workgroups
+  if (!p.use_mfma && a.window > 0 && g.D <= 256) return hipSuccess;
   return launch_attn_merge(g, layer, a, p, st);
 }
 

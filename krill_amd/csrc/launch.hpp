@@ -106,6 +106,9 @@ hipError_t launch_attention_shared_prefix(const PoolGeometry &g, int32_t layer, 
 // mode), from the runtime's occupancy query on a device pool, else the
 // register-budget design point.
 int32_t valu_waves_per_cu(const PoolGeometry &g, int32_t NR);
+// Longest windowed view (tokens) of the decode kernel's per-sequence
+// workgroups (head_dim <= 256; 0 elsewhere).
+int32_t valu_window_limit(const PoolGeometry &g, int32_t NR, bool rope);
 // Resident workgroups per compute unit of the MFMA kernel for (D, nrt,
 // group_waves, token_split, mode) (bound by its LDS ring or its registers), from the
 // occupancy query on a device pool.
