@@ -935,7 +935,9 @@ def run_window(args, w):
         "bound": "hbm",
         "kernel": ("windowed decode attention call" if args.unfused else
                    "fused " + ("RoPE + " if args.window_rope else "") + "append + windowed decode attention call")
-                  + " (k_attn_valu window variant + k_attn_merge_flat), one layer; bytes of the keys the rows see"
+                  + (" (k_attn_valu window variant, one workgroup per (sequence, KV head), partials merged in"
+                     " LDS)" if D <= 256 else " (k_attn_valu window variant + k_attn_merge_flat)")
+                  + ", one layer; bytes of the keys the rows see"
                   + ("" if args.unfused else ", q/o and the new token"),
         "achieved": round(launch_bytes / (attn_ms * 1e-3) / 1e9, 2),
         "peak": HBM_PEAK_GBS,

@@ -54,6 +54,12 @@ __host__ __device__ constexpr int mfma_stages(int D, int G, int W) {
   return W > 1 && 3 * mfma_stage_bytes(D, G) * (8 / W) <= 160 * 1024 ? 3 : 2;
 }
 
+// Two waves per SIMD for the 32-row, 4-wave, 128-d affine shape (chunked
+// prefill): left alone the register allocator lands a few registers past
+// the 256 that two waves may hold and the occupancy halves.
+template <int D, int MODE, int NRT, int W>
+constexpr int mfma_min_waves() { return D == 128 && MODE == MODE_AFFINE && NRT == 2 && W == 4 ? 2 : 1; }
+
 // VAR: 0 plain; 1 RoPE of the queries; 2 sliding window (keys below
 // max(win_start[b], position - window + 1) masked).
 // TS: 1 -- the W waves of a workgroup hold W row groups and every wave
@@ -62,7 +68,8 @@ __host__ __device__ constexpr int mfma_stages(int D, int G, int W) {
 // its own softmax state), so no byte is converted twice; at each segment
 // end the two states are combined through the ring stage just consumed.
 template <int D, int MODE, int NRT, int VAR, int W, int TS>
-__global__ __launch_bounds__(64 * W) void k_attn_mfma(AttnArgs a) {
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(mfma_min_waves<D, MODE, NRT, W>())))
+void k_attn_mfma(AttnArgs a) {
   constexpr bool ROPE = VAR == 1, WIN = VAR == 2;
   constexpr int G = MODE == MODE_AFFINE ? D / 64 : 1;
   constexpr int KS = D / 32;   // 32-d steps of Q.K^T

@@ -301,3 +301,43 @@ def test_window_fused_decode_step(mode, D, R, rope):
                 assert err <= ATOL, (step, b, err)
     for p in pools:
         p.close()
+
+
+def test_window_view_limit():
+    """Up to 8 rows per KV head at head_dim <= 256 the windowed call runs one
+    workgroup per (sequence, KV head), each wave reading at most 64 blocks:
+    at head_dim 256 with 8 rows, two waves, so a view (window + Lq + 62
+    tokens, capped at max_seq_len) of 8192 tokens is attended and one past it
+    is refused with KRILL_E_UNSUPPORTED; the MFMA path takes that call."""
+    from krill_amd._lib import KrillError, KRILL_E_UNSUPPORTED, OPT_ATTN_PATH
+    print("\ncase window_view_limit D=256 R=8", flush=True)
+    D, H, R, W = 256, 1, 8, 8200
+    pool = krill_amd.KVPool(1, H, D, 300, "affine_g64", DTS, free_list_seed=3)
+    pool.set_option(krill_amd._lib.OPT_WINDOW, W)
+    ss = Seqs(pool, 2, 8192, np.random.default_rng(11))
+    for b, L in enumerate([8192, 3000]):
+        for p in range(0, L, 1024):
+            ss.append(b, min(1024, L - p))
+    rng = np.random.default_rng(12)
+    q = rand_bits(rng, (2, H * R, 1, D), DTS)
+    qd = to_dev(q, DTS)
+    st = i32(pool.batch_starts(ss.seqs))
+    want = [_oracle_rows(ss, b, q[b], W, int(pool.batch_starts([ss.seqs[b]])[0]), "affine_g64") for b in range(2)]
+
+    def run(mb, msl):
+        t, n = pool.batch_tables(ss.seqs, mb)
+        out = pool.attention_windowed(0, qd, i32(t), i32(n), st, W, msl, 1.0 / np.sqrt(D))
+        torch.cuda.synchronize()
+        return out.cpu().numpy()
+
+    out = run(128, 8192)  # view 8192: the decode kernel's limit for this shape
+    for b in range(2):
+        assert np.abs(out[b] - want[b]).max() <= ATOL, b
+    with pytest.raises(KrillError) as e:
+        run(130, 8200)  # view min(8200, 8200 + 1 + 62) = 8200 > 8192
+    assert e.value.code == KRILL_E_UNSUPPORTED
+    pool.set_option(OPT_ATTN_PATH, 2)
+    out2 = run(130, 8200)
+    for b in range(2):
+        assert np.abs(out2[b] - want[b]).max() <= ATOL, b
+    pool.close()
