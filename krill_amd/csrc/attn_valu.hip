@@ -25,6 +25,10 @@
 //      q.k = s * (q.(u - 128)) + (z + 128 s) * sum q,
 //    so no element is dequantised.  Reference row mode dequantises exactly
 //    (f16(f16(u*s) + z), QuantizedKVCache.swift:200-204) before the dot.
+//    head_dim 512 (four d-slice waves, up to 8 rows each) takes the same
+//    fp16 operands to v_mfma_f32_16x16x32_f16 instead (S^T tiles of 16
+//    tokens x 16 rows, 16 MFMAs per block and wave in place of 512 dots) and
+//    returns the per-group sums to one token per lane through LDS;
 //  * online softmax in the log2 domain with a lazily raised running max: a
 //    block only pays for a wave reduction when some score exceeds the
 //    running max by more than 8 (a wave vote), so weights stay below 2^8;
@@ -127,8 +131,9 @@ __device__ __forceinline__ void ld_stream_words(__amdgpu_buffer_rsrc_t r, int of
 // workgroup, 128 dims each (a 512-byte K row per lane and 32 V tiles would not
 // fit one wave's registers).  Every wave holds its slice's query pairs, K
 // pieces, V tiles and output tiles, exactly the register set of the D = 128
-// kernel; the partial scores of the four slices meet in LDS (one barrier per
-// block), and every wave then runs the same softmax on the same sums.
+// kernel (the slice's scores on the matrix cores, MSC below); the partial
+// scores of the four slices meet in LDS (one barrier per block), and every
+// wave then runs the same softmax on the same sums.
 template <int D>
 constexpr int d_slices() {
   return D > 256 ? D / 128 : 1;
@@ -300,6 +305,16 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
   // the VALU (lane owns D / 64 rows of V^T, fp32 FMAs)
   constexpr bool PVM = pv_on_mfma<D, NR>();
   constexpr bool LOAD_TOGETHER = !PVM && valu_waves_per_simd<D, NR>() >= 3;  // next block's loads in one pass
+  // d-slices (head_dim 512): the scores on the matrix cores.  Lane l loads
+  // the 16-byte piece of token 16 j + (l & 15), chunk 4 c + (l >> 4) of the
+  // slice into kr[j KPN + c]; its two 8-byte halves are the A operands of two
+  // v_mfma_f32_16x16x32_f16 steps (the contraction runs over the slice's
+  // dims in that order, the query operand qB likewise), which leave S^T
+  // tiles per token tile j and 64-d chunk group c; the tiles go through LDS
+  // back to one token per lane for the scaling and the slices' exchange.
+  constexpr bool MSC = DS > 1;
+  constexpr int KPN = NP / 4;  // 64-d chunk groups of the slice (its scale groups in affine mode)
+  constexpr int ATS = 68;      // LDS row stride (floats) of the transposed score sums
 
   __shared__ __attribute__((aligned(16))) float w_lds_all[NWV][NR * GW * 64];
   __shared__ __attribute__((aligned(16))) uint16_t sz_lds_all[NWV][2 * 64];
@@ -308,6 +323,9 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
   __shared__ __attribute__((aligned(16))) float part_lds[SEQ ? SW : 1][SEQ ? NR * PST : 4];
   // the slices' partial scores, two buffers (block parity)
   __shared__ __attribute__((aligned(16))) float sc_lds[DS > 1 ? 2 : 1][DS][DS > 1 ? NR * 64 : 1];
+  // MSC, per wave: the per-group score sums [g][row][token] of the block,
+  // and at a segment's start the staging of the fp16 query words [row][64]
+  __shared__ __attribute__((aligned(16))) float msc_lds[MSC ? DS : 1][MSC ? GW * NR * ATS : 4];
 
   const int lane = DS > 1 || SEQ ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
   const int wsl = DS > 1 ? (int)(threadIdx.x >> 6) : 0;  // this wave's d-slice
@@ -504,19 +522,35 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
   auto v_tile_off = [](int gd, int tg, int h, int m) {
     return v_offset(D) + tg * 32 * D + (((2 * (gd % DPL) + h) * 64 + 16 * (gd / DPL) + m) << 4);
   };
+  // head_dim 512, affine (VRM): the rows of a stored tile span the slice's
+  // two scale groups (m < 8, m >= 8), so the wave regroups them: its tile
+  // vt = 4 gv + u, row rho, is row 8 gv + 4 (u >> 1) + (rho >> 2) of the
+  // slice's stored tile 4 (u & 1) + (rho & 3), i.e. d = DW wsl + 64 gv +
+  // 32 (u >> 1) + 8 (rho >> 2) + 4 (u & 1) + (rho & 3): every tile lies in
+  // group gv, and the four rows of an output quarter are consecutive d
+  constexpr bool VRM = DS > 1 && MODE == MODE_AFFINE;
+  static_assert(!VRM || (ND == 8 && GW == 2), "regrouping for two scale groups of 8 tiles");
+  auto vr_tile = [](int vt, int rho) { return VRM ? 4 * ((vt % 4) & 1) + (rho & 3) : vt; };
+  auto vr_row = [](int vt, int rho) { return VRM ? 8 * (vt / 4) + 4 * ((vt % 4) >> 1) + (rho >> 2) : rho; };
   const int gl = MODE == MODE_AFFINE ? (DPL * lane) / 64 : 0;  // VALU P.V: scale group of this lane's V rows
   constexpr int NV = PVM ? ND : 4 * DPL;  // 16-byte V pieces per lane
   uint4 kr[NP];
   uint4 vr[NV];
+  // byte offset of K register p's piece: one token per lane, or (MSC) the
+  // MFMA operand order
+  auto k_off = [&](int p) -> int {
+    return MSC ? k_byte(16 * (p / KPN) + (lane & 15), 16 * (p0 + 4 * (p % KPN) + (lane >> 4)))
+               : k_byte(lane, 16 * (p0 + p));
+  };
   auto load_k = [&](__amdgpu_buffer_rsrc_t r) {
 #pragma unroll
-    for (int p = 0; p < NP; ++p) kr[p] = ld_stream16(r, k_byte(lane, 16 * (p0 + p)));
+    for (int p = 0; p < NP; ++p) kr[p] = ld_stream16(r, k_off(p));
   };
   auto load_v = [&](__amdgpu_buffer_rsrc_t r) {
     if constexpr (PVM) {
       const int tg = lane >> 5, h = (lane >> 4) & 1, m = lane & 15;
 #pragma unroll
-      for (int dt = 0; dt < ND; ++dt) vr[dt] = ld_stream16(r, v_tile_off(dt0 + dt, tg, h, m));
+      for (int dt = 0; dt < ND; ++dt) vr[dt] = ld_stream16(r, v_tile_off(dt0 + vr_tile(dt, m), tg, h, vr_row(dt, m)));
     } else {
       // vr[tg 2 DPL + i]: d = DPL lane + i / 2, half i % 2 of token group tg
 #pragma unroll
@@ -538,6 +572,9 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
   // mode also needs the sum of each 64-d group of the fp16 query (pairs
   // 32g .. 32g+31 = columns 2g and 2g+1), reduced inside each 16-lane row.
   uint32_t qv[NR][DW / 32];
+  // MSC: lane (n, q4) holds, for chunk group c and half h, the fp16 words
+  // 32 c + 8 q4 + 4 h .. +3 of row n (zero for n >= NR)
+  half8_t qB[MSC ? KPN : 1][2];
   float qs[NR][GW];
   // per row: the factor its scores take (the softmax scale in log2 units
   // times the query's 2^k; d-slices: 2^k alone, on the slice's part)
@@ -648,6 +685,25 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
         for (int g = 0; g < GW; ++g) qs[r][g] = 0.0f;
       }
     }
+    if constexpr (MSC) {
+      // the query operands, through the wave's LDS (its lanes only)
+      uint32_t *const ql = reinterpret_cast<uint32_t *>(msc_lds[wsl]);
+      if (lane < 16) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+#pragma unroll
+          for (int c = 0; c < DW / 32; ++c) ql[r * 64 + 16 * c + lane] = qv[r][c];
+      }
+      const int n = lane & 15, q4 = lane >> 4;
+#pragma unroll
+      for (int c = 0; c < KPN; ++c)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          uint4 w = uint4{0u, 0u, 0u, 0u};
+          if (n < NR) w = *reinterpret_cast<const uint4 *>(ql + n * 64 + 32 * c + 8 * q4 + 4 * h);
+          qB[c][h] = __builtin_bit_cast(half8_t, w);
+        }
+    }
   };
 
   // Loads of block n+1 are issued in a fixed order inside the loop: K bytes
@@ -728,11 +784,23 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
     const __amdgpu_buffer_rsrc_t nrs = rsrc_of(i + 1);
     if (i == patch_i) {
       // the block holding the segment's newest token: its K row and both
-      // (scale, zero) words go to lane patch_t
+      // (scale, zero) words go to lane patch_t (MSC: its chunk 4 c + q4 to
+      // lane (patch_t & 15) + 16 q4, register (patch_t / 16) KPN + c)
+      if constexpr (MSC) {
+        const bool mine = (lane & 15) == (patch_t & 15);
 #pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        const uint4 x = *reinterpret_cast<const uint4 *>(newrow + 16 * (p0 + p));
-        if (lane == patch_t) kr[p] = x;
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int c = 0; c < KPN; ++c) {
+            const uint4 x = *reinterpret_cast<const uint4 *>(newrow + 16 * (p0 + 4 * c + (lane >> 4)));
+            if (mine && (patch_t >> 4) == j) kr[j * KPN + c] = x;
+          }
+      } else {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const uint4 x = *reinterpret_cast<const uint4 *>(newrow + 16 * (p0 + p));
+          if (lane == patch_t) kr[p] = x;
+        }
       }
 #pragma unroll
       for (int g = 0; g < GW; ++g) {
@@ -747,51 +815,116 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
     // pair of each dot comes from lane (pair & 15) of the lane's 16-lane row
     // through the DPP broadcast of v_dot2c.
     float accg[NR][GW];
+    if constexpr (MSC) {
+      float4_t sacc[4][GW];
 #pragma unroll
-    for (int r = 0; r < NR; ++r)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int g = 0; g < GW; ++g) accg[r][g] = 0.0f;
-    half2_t ks2 = m1024, kz2 = m1024;
-    if constexpr (MODE == MODE_REF) {
-      const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)(km[0] & 0xffffu));
-      const _Float16 z = __builtin_bit_cast(_Float16, (uint16_t)(km[0] >> 16));
-      ks2 = half2_t{s, s};
-      kz2 = half2_t{z, z};
-    }
+        for (int g = 0; g < GW; ++g) sacc[j][g] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      if (p > 0) order_after(kr[p], accg[NR - 1][MODE == MODE_AFFINE ? (p - 1) / PPG : 0]);
-      const uint32_t w4[4] = {kr[p].x, kr[p].y, kr[p].z, kr[p].w};
-      half2_t kp[8];
+      for (int j = 0; j < 4; ++j) {
+        half2_t ks2 = m1024, kz2 = m1024;
+        if constexpr (MODE == MODE_REF) {
+          // the (scale, zero) word of this lane's token of tile j
+          const uint32_t kmj = (uint32_t)__shfl((int)km[0], 16 * j + (lane & 15));
+          const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)(kmj & 0xffffu));
+          const _Float16 z = __builtin_bit_cast(_Float16, (uint16_t)(kmj >> 16));
+          ks2 = half2_t{s, s};
+          kz2 = half2_t{z, z};
+        }
+        half8_t A[KPN][2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        kp[2 * i] = bytes01_plus1024(w4[i]);
-        kp[2 * i + 1] = bytes23_plus1024(w4[i]);
+        for (int c = 0; c < KPN; ++c) {
+          const int p = j * KPN + c;
+          const uint32_t w4[4] = {kr[p].x, kr[p].y, kr[p].z, kr[p].w};
+          half2_t kp[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            kp[2 * e] = bytes01_plus1024(w4[e]);
+            kp[2 * e + 1] = bytes23_plus1024(w4[e]);
+          }
+          if constexpr (MODE == MODE_REF) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kp[e] = (kp[e] + m1024) * ks2 + kz2;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kp[e] = kp[e] + m1152;  // u - 128, exact
+          }
+          // the piece is converted: its register takes the next block's piece
+          kr[p] = ld_stream16(nrs, k_off(p));
+          A[c][0] = half8_t{kp[0][0], kp[0][1], kp[1][0], kp[1][1], kp[2][0], kp[2][1], kp[3][0], kp[3][1]};
+          A[c][1] = half8_t{kp[4][0], kp[4][1], kp[5][0], kp[5][1], kp[6][0], kp[6][1], kp[7][0], kp[7][1]};
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int c = 0; c < KPN; ++c) {
+            const int g = MODE == MODE_AFFINE ? c : 0;
+            sacc[j][g] = mfma16x16x32(A[c][h], qB[c][h], sacc[j][g]);
+          }
       }
+      // lane (n, q4) holds the sums of tokens 16 j + 4 q4 .. +3 for row n:
+      // back to one token per lane through the wave's LDS
+      float *const ml = msc_lds[wsl];
+      const int n = lane & 15, q4 = lane >> 4;
+      if (n < NR) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int g = 0; g < GW; ++g)
+            *reinterpret_cast<float4_t *>(ml + (g * NR + n) * ATS + 16 * j + 4 * q4) = sacc[j][g];
+      }
+#pragma unroll
+      for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int g = 0; g < GW; ++g) accg[r][g] = ml[(g * NR + r) * ATS + lane];
+    } else {
+#pragma unroll
+      for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int g = 0; g < GW; ++g) accg[r][g] = 0.0f;
+      half2_t ks2 = m1024, kz2 = m1024;
       if constexpr (MODE == MODE_REF) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) kp[i] = (kp[i] + m1024) * ks2 + kz2;
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) kp[i] = kp[i] + m1152;  // u - 128, exact
+        const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)(km[0] & 0xffffu));
+        const _Float16 z = __builtin_bit_cast(_Float16, (uint16_t)(km[0] >> 16));
+        ks2 = half2_t{s, s};
+        kz2 = half2_t{z, z};
       }
-      // the piece is converted: its register takes the next block's piece
-      if constexpr (!LOAD_TOGETHER) kr[p] = ld_stream16(nrs, k_byte(lane, 16 * (p0 + p)));
-      const int g = MODE == MODE_AFFINE ? p / PPG : 0;
-      // the last piece of a scale group finishes accg[.][g]
-      const bool tail = MODE == MODE_AFFINE ? (p + 1) % PPG == 0 : p == NP - 1;
 #pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        if (p & 1) {
-          if (tail)
-            dot8_bcast<8, true>(accg[r][g], qv[r][p >> 1], kp);
-          else
-            dot8_bcast<8, false>(accg[r][g], qv[r][p >> 1], kp);
+      for (int p = 0; p < NP; ++p) {
+        if (p > 0) order_after(kr[p], accg[NR - 1][MODE == MODE_AFFINE ? (p - 1) / PPG : 0]);
+        const uint32_t w4[4] = {kr[p].x, kr[p].y, kr[p].z, kr[p].w};
+        half2_t kp[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          kp[2 * i] = bytes01_plus1024(w4[i]);
+          kp[2 * i + 1] = bytes23_plus1024(w4[i]);
+        }
+        if constexpr (MODE == MODE_REF) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) kp[i] = (kp[i] + m1024) * ks2 + kz2;
         } else {
-          if (tail)
-            dot8_bcast<0, true>(accg[r][g], qv[r][p >> 1], kp);
-          else
-            dot8_bcast<0, false>(accg[r][g], qv[r][p >> 1], kp);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) kp[i] = kp[i] + m1152;  // u - 128, exact
+        }
+        // the piece is converted: its register takes the next block's piece
+        if constexpr (!LOAD_TOGETHER) kr[p] = ld_stream16(nrs, k_byte(lane, 16 * (p0 + p)));
+        const int g = MODE == MODE_AFFINE ? p / PPG : 0;
+        // the last piece of a scale group finishes accg[.][g]
+        const bool tail = MODE == MODE_AFFINE ? (p + 1) % PPG == 0 : p == NP - 1;
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          if (p & 1) {
+            if (tail)
+              dot8_bcast<8, true>(accg[r][g], qv[r][p >> 1], kp);
+            else
+              dot8_bcast<8, false>(accg[r][g], qv[r][p >> 1], kp);
+          } else {
+            if (tail)
+              dot8_bcast<0, true>(accg[r][g], qv[r][p >> 1], kp);
+            else
+              dot8_bcast<0, false>(accg[r][g], qv[r][p >> 1], kp);
+          }
         }
       }
     }
@@ -918,7 +1051,7 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
       const bool mine = (lane >> 4) == 2 * tg + (p >> 4);
 #pragma unroll
       for (int dt = 0; dt < ND; ++dt) {
-        const uint32_t nv = (uint32_t)newrow[D + tile_d(dt0 + dt, lane & 15)] << sh;
+        const uint32_t nv = (uint32_t)newrow[D + tile_d(dt0 + vr_tile(dt, lane & 15), vr_row(dt, lane & 15))] << sh;
         uint4 &x = vr[dt];
         if (mine) {
           if ((bp >> 2) == 0) x.x = (x.x & keep) | nv;
@@ -963,14 +1096,10 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
     // row l & 15 (rows beyond NR repeat the last one; their outputs are never
     // read), each binary32 weight as an fp16 high part and the fp16 rounding
     // of its remainder (about 2^-22 relative left), two MFMAs per tile.
-    if constexpr (DS > 1 && MODE == MODE_AFFINE) {
-      // head_dim 512: a tile's 16 rows d = 8 (16 k + m) + dt % 8 span two
-      // scale groups of the slice (rows m < 8 the first, m >= 8 the
-      // second), so each tile runs once per group with the other group's
-      // rows zeroed in A and that group's weights in B
+    if constexpr (VRM) {
+      // head_dim 512: each regrouped tile lies in one scale group, whose
+      // weights it takes in B
       const int nb = (lane & 15) < NR ? (lane & 15) : NR - 1, q = lane >> 4;
-      const bool upper = (lane & 15) >= 8;
-      const half8_t zero8 = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
       for (int sh = 0; sh < 2; ++sh) {
         half8_t bh[2], bl[2];
@@ -983,17 +1112,15 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
         for (int dt = 0; dt < ND; ++dt) {
           const uint4 v = vr[dt];
           const half8_t av = bytes8_centred(sh ? uint2{v.z, v.w} : uint2{v.x, v.y});
-          const half8_t a0 = upper ? zero8 : av, a1 = upper ? av : zero8;
-          acc[dt] = mfma16x16x32(a0, bh[0], acc[dt]);
-          acc[dt] = mfma16x16x32(a0, bl[0], acc[dt]);
-          acc[dt] = mfma16x16x32(a1, bh[1], acc[dt]);
-          acc[dt] = mfma16x16x32(a1, bl[1], acc[dt]);
+          const int g = dt / (ND / GW);
+          acc[dt] = mfma16x16x32(av, bh[g], acc[dt]);
+          acc[dt] = mfma16x16x32(av, bl[g], acc[dt]);
         }
       }
       // the tiles are consumed: their registers take the next block's
       const int tg = lane >> 5, h = (lane >> 4) & 1, m = lane & 15;
 #pragma unroll
-      for (int dt = 0; dt < ND; ++dt) vr[dt] = ld_stream16(nrs, v_tile_off(dt0 + dt, tg, h, m));
+      for (int dt = 0; dt < ND; ++dt) vr[dt] = ld_stream16(nrs, v_tile_off(dt0 + vr_tile(dt, m), tg, h, vr_row(dt, m)));
     } else {
       const int nb = (lane & 15) < NR ? (lane & 15) : NR - 1, q = lane >> 4;
 #pragma unroll
@@ -1134,15 +1261,8 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
         }
       }
     }
-    if constexpr (DS > 1 && MODE == MODE_AFFINE) {
-      // head_dim 512: output rows m = q4 + j < 8 are the slice's first group
-      const float cgl = lane >= 32 ? cg[1] : cg[0];
 #pragma unroll
-      for (int dt = 0; dt < ND; ++dt) acc[dt] += cgl;
-    } else {
-#pragma unroll
-      for (int dt = 0; dt < ND; ++dt) acc[dt] += cg[dt / (ND / GW)];
-    }
+    for (int dt = 0; dt < ND; ++dt) acc[dt] += cg[dt / (ND / GW)];
     // The lane's values of tiles DPL k .. DPL k + DPL - 1 form one run of
     // 4 DPL consecutive d: d = DPL (16 k + q4 + j) + e for j < 4, e < DPL
     // (k counted over the whole row: the slice's tiles start at dt0).
@@ -1152,15 +1272,32 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
       const int64_t hslot = DS > 1 ? (int64_t)hk * a.row_groups + rg : (int64_t)hk;
       const int64_t pi = (hslot * (a.waves + a.B) + wv + b) * NR + n;
       const int64_t ob = whole ? out_row_base(a, b, hk, r0 + n, D) : SEQ ? (int64_t)n * PST : pi * D;
+      if constexpr (VRM) {
+        // regrouped tiles: d = DW wsl + 64 gv + 32 uh + 8 (lane >> 4) + 4 ul + j
+        // for tile 4 gv + 2 uh + ul, element j -- four runs of 8
 #pragma unroll
-      for (int k = 0; k < ND / DPL; ++k) {
-        float run[4 * DPL];
+        for (int gv = 0; gv < 2; ++gv)
 #pragma unroll
-        for (int j2 = 0; j2 < 4; ++j2)
+          for (int uh = 0; uh < 2; ++uh) {
+            float run[8];
 #pragma unroll
-          for (int e2 = 0; e2 < DPL; ++e2) run[DPL * j2 + e2] = acc[DPL * k + e2][j2] * mul;
-        store_run<4 * DPL>(SEQ ? (void *)part_lds[wid] : whole ? a.out : (void *)a.ws_o,
-                           ob + DPL * (16 * (dt0 / DPL + k) + q4), run, whole ? a.out_dtype : DT_F32);
+            for (int ul = 0; ul < 2; ++ul)
+#pragma unroll
+              for (int j2 = 0; j2 < 4; ++j2) run[4 * ul + j2] = acc[4 * gv + 2 * uh + ul][j2] * mul;
+            store_run<8>(whole ? a.out : (void *)a.ws_o, ob + DW * wsl + 64 * gv + 32 * uh + 2 * q4, run,
+                         whole ? a.out_dtype : DT_F32);
+          }
+      } else {
+#pragma unroll
+        for (int k = 0; k < ND / DPL; ++k) {
+          float run[4 * DPL];
+#pragma unroll
+          for (int j2 = 0; j2 < 4; ++j2)
+#pragma unroll
+            for (int e2 = 0; e2 < DPL; ++e2) run[DPL * j2 + e2] = acc[DPL * k + e2][j2] * mul;
+          store_run<4 * DPL>(SEQ ? (void *)part_lds[wid] : whole ? a.out : (void *)a.ws_o,
+                             ob + DPL * (16 * (dt0 / DPL + k) + q4), run, whole ? a.out_dtype : DT_F32);
+        }
       }
       if constexpr (SEQ) {
         if (lane < 16) {
