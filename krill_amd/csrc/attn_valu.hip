@@ -312,7 +312,7 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
   // dims in that order, the query operand qB likewise), which leave S^T
   // tiles per token tile j and 64-d chunk group c; the tiles go through LDS
   // back to one token per lane for the scaling and the slices' exchange.
-  constexpr bool MSC = DS > 1;
+  constexpr bool MSC = DS > 1 || (D == 128 && PVM && !SEQ);
   constexpr int KPN = NP / 4;  // 64-d chunk groups of the slice (its scale groups in affine mode)
   constexpr int ATS = 68;      // LDS row stride (floats) of the transposed score sums
 
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
   __shared__ __attribute__((aligned(16))) float sc_lds[DS > 1 ? 2 : 1][DS][DS > 1 ? NR * 64 : 1];
   // MSC, per wave: the per-group score sums [g][row][token] of the block,
   // and at a segment's start the staging of the fp16 query words [row][64]
-  __shared__ __attribute__((aligned(16))) float msc_lds[MSC ? DS : 1][MSC ? GW * NR * ATS : 4];
+  __shared__ __attribute__((aligned(16))) float msc_lds[MSC ? NWV : 1][MSC ? GW * NR * ATS : 4];
 
   const int lane = DS > 1 || SEQ ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
   const int wsl = DS > 1 ? (int)(threadIdx.x >> 6) : 0;  // this wave's d-slice
@@ -687,7 +687,7 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
     }
     if constexpr (MSC) {
       // the query operands, through the wave's LDS (its lanes only)
-      uint32_t *const ql = reinterpret_cast<uint32_t *>(msc_lds[wsl]);
+      uint32_t *const ql = reinterpret_cast<uint32_t *>(msc_lds[SEQ ? wid : wsl]);
       if (lane < 16) {
 #pragma unroll
         for (int r = 0; r < NR; ++r)
@@ -865,7 +865,7 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
       }
       // lane (n, q4) holds the sums of tokens 16 j + 4 q4 .. +3 for row n:
       // back to one token per lane through the wave's LDS
-      float *const ml = msc_lds[wsl];
+      float *const ml = msc_lds[SEQ ? wid : wsl];
       const int n = lane & 15, q4 = lane >> 4;
       if (n < NR) {
 #pragma unroll
