@@ -181,6 +181,22 @@ def test_decode_attention_valu(mode, D, R):
     assert err <= ATOL, f"max abs error {err:.3e}"
 
 
+@pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
+@pytest.mark.parametrize("D,R,Lq,dt", [(128, 3, 1, "bf16"), (128, 6, 1, "f16"), (128, 7, 1, "bf16"),
+                                       (128, 2, 2, "f16"), (128, 1, 3, "bf16"), (128, 2, 3, "bf16"),
+                                       (512, 3, 1, "bf16"), (512, 6, 1, "f16")])
+def test_decode_attention_matrix_core_scores_rows(mode, D, R, Lq, dt):
+    """Every row count of the decode kernel's matrix-core scores (3-8 rows
+    per KV head at head_dim 128, 1-8 per row group at 512): the S^T tiles
+    carry 16 rows, the rows past R * Lq are zero operands, and the sums go
+    back to one token per lane through LDS; short query chunks (Lq > 1) mix
+    causal limits into the rows."""
+    print(f"\ncase decode_msc mode={mode} D={D} R={R} Lq={Lq} dt={dt}", flush=True)
+    got, ref = _attn_case(mode, D, 2, R, [Lq, 63, 64, 65, 300, 700], Lq=Lq, dt=dt, path=1, seed=D + 7 * R + Lq)
+    err = np.abs(got - ref).max()
+    assert err <= ATOL, f"max abs error {err:.3e}"
+
+
 @pytest.mark.parametrize("split_blocks", [1, 2, 3])
 def test_decode_attention_split_merge(split_blocks):
     print(f"\ncase decode_split sb={split_blocks}", flush=True)
