@@ -69,7 +69,7 @@ extern "C" {
                                     per split of one sequence on the MFMA path; 0 = automatic */
 #define KRILL_OPT_ATTN_PATH 2    /* 0 auto (VALU <= 8 query rows per KV head, else MFMA), 1 VALU, 2 MFMA;
                                     "VALU" names the decode kernel (one token per lane for the softmax; its
-                                    scores and P.V use the matrix cores at head_dim 64-128 with 3-8 rows and at
+                                    scores and P.V use the matrix cores at head_dim 128 with 3-8 rows and at
                                     head_dim 512), "MFMA" the row-tiled kernel of verify and prefill */
 #define KRILL_OPT_WINDOW 3       /* sliding window in tokens (0 none, else >= 2): before each append a
                                     sequence keeps its last window - 1 tokens and its blocks that hold none

@@ -25,9 +25,9 @@
 //      q.k = s * (q.(u - 128)) + (z + 128 s) * sum q,
 //    so no element is dequantised.  Reference row mode dequantises exactly
 //    (f16(f16(u*s) + z), QuantizedKVCache.swift:200-204) before the dot.
-//    Where P.V runs on the matrix cores (below) -- head_dim 64 and 128 with
-//    3-8 rows on the flat split, and head_dim 512 (four d-slice waves, up to
-//    8 rows each) -- the same fp16 operands go to v_mfma_f32_16x16x32_f16
+//    Where P.V runs on the matrix cores (below) -- head_dim 128 with 3-8
+//    rows on the flat split, and head_dim 512 (four d-slice waves, up to 8
+//    rows each) -- the same fp16 operands go to v_mfma_f32_16x16x32_f16
 //    instead (S^T tiles of 16 tokens x 16 rows, 16 MFMAs per block and wave
 //    in place of 64 v_dot2c per row and 128-d slice), and the per-group
 //    sums return to one token per lane through LDS;
@@ -307,15 +307,15 @@ __global__ __launch_bounds__(64 * (seq_waves<D, NR, MODE, VAR>() > 0 ? seq_waves
   // the VALU (lane owns D / 64 rows of V^T, fp32 FMAs)
   constexpr bool PVM = pv_on_mfma<D, NR>();
   constexpr bool LOAD_TOGETHER = !PVM && valu_waves_per_simd<D, NR>() >= 3;  // next block's loads in one pass
-  // MSC -- P.V on the matrix cores and a flat split (head_dim 64 and 128,
-  // 3-8 rows), or d-slices (head_dim 512): the scores there too.  Lane l loads
+  // MSC -- P.V on the matrix cores and a flat split (head_dim 128, 3-8
+  // rows), or d-slices (head_dim 512): the scores there too.  Lane l loads
   // the 16-byte piece of token 16 j + (l & 15), chunk 4 c + (l >> 4) of the
   // slice into kr[j KPN + c]; its two 8-byte halves are the A operands of two
   // v_mfma_f32_16x16x32_f16 steps (the contraction runs over the slice's
   // dims in that order, the query operand qB likewise), which leave S^T
   // tiles per token tile j and 64-d chunk group c; the tiles go through LDS
   // back to one token per lane for the scaling and the slices' exchange.
-  constexpr bool MSC = DS > 1 || (D <= 128 && PVM && !SEQ);
+  constexpr bool MSC = DS > 1 || (D == 128 && PVM && !SEQ);
   constexpr int KPN = NP / 4;  // 64-d chunk groups of the slice (its scale groups in affine mode)
   constexpr int ATS = 68;      // LDS row stride (floats) of the transposed score sums
 
