@@ -7,7 +7,7 @@ and the output against the oracle directly."""
 import numpy as np
 import pytest
 
-from kvutil import DT, Filled, i32, oracle_attention, rand_bits, to_dev
+from kvutil import DT, MODE, Filled, i32, oracle_attention, rand_bits, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -139,9 +139,10 @@ def test_fused_step_qwen3_14b_shape_against_oracle():
     _close(ctx)
 
 
+@pytest.mark.parametrize("mode", ["affine_g64", "ref_row"])
 @pytest.mark.parametrize("D,R,dt", [(128, 5, "bf16"), (64, 4, "f16"), (256, 2, "bf16"), (128, 16, "bf16"),
                                     (512, 8, "bf16"), (512, 16, "f16")])
-def test_fused_rope_step_matches_rope_append_and_rotated_queries(D, R, dt):
+def test_fused_rope_step_matches_rope_append_and_rotated_queries(mode, D, R, dt):
     """krill_decode_append_attention_rope against krill_quantize_append_rope at
     the reserved slots + decode attention on queries rotated by the oracle
     (R = 16: more than 8 rows per KV head, the MFMA path; at D = 512 two
@@ -149,8 +150,8 @@ def test_fused_rope_step_matches_rope_append_and_rotated_queries(D, R, dt):
     from krill_amd.pool import rope_table
     from oracle import oracle as O
 
-    print(f"\ncase fused_rope D={D} R={R} dt={dt}", flush=True)
-    H, mode, seed = 2, "affine_g64", 40 + D + R
+    print(f"\ncase fused_rope mode={mode} D={D} R={R} dt={dt}", flush=True)
+    H, seed = 2, 40 + D + R
     prefill = [70, 1, 200, 64, 517]
     B = len(prefill)
     blocks = sum((T + 64) // 64 for T in prefill) + 8
@@ -189,7 +190,7 @@ def test_fused_rope_step_matches_rope_append_and_rotated_queries(D, R, dt):
         assert np.array_equal(a.view(np.uint8), b_.view(np.uint8)), f"pool {name} differs"
     # and the new K bytes are the oracle's quantization of the rotated row
     kr = O.rope_rows(kn, DT[dt], np.broadcast_to(pos[:, None, None], (B, H, 1)), cs)
-    kq, _, _ = O.quantize(kr, DT[dt], 1)
+    kq, _, _ = O.quantize(kr, DT[dt], MODE[mode])
     got = snaps[1]["keys"].cpu().numpy()
     for b in range(B):
         np.testing.assert_array_equal(got[b, :, lens[b] - 1], kq[b, :, 0])
