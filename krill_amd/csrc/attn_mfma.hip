@@ -77,7 +77,13 @@ void k_attn_mfma(AttnArgs a) {
   constexpr int RR = 16 * NRT; // query rows of this wave
   constexpr int STAGE = mfma_stage_bytes(D, G);
   constexpr int NCH = STAGE / 1024;  // direct loads per block
-  constexpr int NST = mfma_stages(D, G, W);
+  // CVT (32-row waves in groups of four, affine, head_dim 128: chunked
+  // prefill): the four waves convert each staged block once, a quarter
+  // each, into fp16 K and V^T tiles in LDS that all four read, instead of
+  // every wave converting the whole block for its own rows; the tiles take
+  // the LDS of the third ring stage
+  constexpr bool CVT = W == 4 && TS == 1 && NRT == 2 && MODE == MODE_AFFINE && D == 128;
+  constexpr int NST = CVT ? 2 : mfma_stages(D, G, W);
   constexpr int NK = 64 * D / 1024;  // runs holding the K bytes
   // W > 1: the fewest runs of a stage any wave of the group issues
   constexpr int NCH_W = NCH / W;
@@ -89,6 +95,11 @@ void k_attn_mfma(AttnArgs a) {
   constexpr int NTG = 2 / TS;          // 32-token P.V groups per wave and block
   static_assert(TS == 1 || NRT * NDT * 64 * 16 + NRT * 64 * 8 <= STAGE, "combine buffer fits a stage");
   __shared__ __attribute__((aligned(1024))) uint8_t ring[NST * STAGE];
+  // CVT tiles: K [token][d] with rows KTS bytes apart, V^T [d][position] with
+  // rows VTS bytes apart (the padding puts the 16 rows a lane quarter reads
+  // in different banks)
+  constexpr int KTS = D * 2 + 16, VTS = 64 * 2 + 16;
+  __shared__ __attribute__((aligned(16))) uint8_t cvt_lds[CVT ? 64 * KTS + D * VTS : 16];
 
   const int lane = threadIdx.x & 63;
   const int wid = W > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;
@@ -345,6 +356,33 @@ void k_attn_mfma(AttnArgs a) {
         issue(i + NST - 1, (i + NST - 1 - i0) % NST, KRuns0{}, AllRuns{});
       }
       const uint8_t *st = ring + buf * STAGE;
+      if constexpr (CVT) {
+        // wave wid: K of tokens 16 wid .. +15 (lane: token 16 wid + lane / 4,
+        // dims 32 (lane % 4) .. +31) and V^T rows 32 wid .. +31 (lane: row
+        // 32 wid + lane / 2, token group lane % 2, its 32 positions), as exact
+        // fp16 u - 128; then every wave's part is in before any is read
+        {
+          const int tok = 16 * wid + (lane >> 2), d0 = 32 * (lane & 3);
+          const uint4 a = *reinterpret_cast<const uint4 *>(st + k_byte(tok, d0));
+          const uint4 b = *reinterpret_cast<const uint4 *>(st + k_byte(tok, d0 + 16));
+          uint8_t *o = cvt_lds + tok * KTS + d0 * 2;
+          *reinterpret_cast<half8_t *>(o) = bytes8_centred(uint2{a.x, a.y});
+          *reinterpret_cast<half8_t *>(o + 16) = bytes8_centred(uint2{a.z, a.w});
+          *reinterpret_cast<half8_t *>(o + 32) = bytes8_centred(uint2{b.x, b.y});
+          *reinterpret_cast<half8_t *>(o + 48) = bytes8_centred(uint2{b.z, b.w});
+        }
+        {
+          const int d = 32 * wid + (lane >> 1), tgv = lane & 1;
+          const uint4 a = *reinterpret_cast<const uint4 *>(st + v_pos_byte(D, tgv, d, 0));
+          const uint4 b = *reinterpret_cast<const uint4 *>(st + v_pos_byte(D, tgv, d, 16));
+          uint8_t *o = cvt_lds + 64 * KTS + d * VTS + 32 * tgv * 2;
+          *reinterpret_cast<half8_t *>(o) = bytes8_centred(uint2{a.x, a.y});
+          *reinterpret_cast<half8_t *>(o + 16) = bytes8_centred(uint2{a.z, a.w});
+          *reinterpret_cast<half8_t *>(o + 32) = bytes8_centred(uint2{b.x, b.y});
+          *reinterpret_cast<half8_t *>(o + 48) = bytes8_centred(uint2{b.z, b.w});
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      }
       const int tbase = (i - s) << 6;
       // some row of this group does not see every token of the block (causal
       // edge or the sequence's last block): only then are scores masked
@@ -374,16 +412,18 @@ void k_attn_mfma(AttnArgs a) {
           for (int g = 0; g < G; ++g) sacc[rt][g] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          const uint2 kb = *reinterpret_cast<const uint2 *>(st + k_byte(tokA, 32 * ks + 8 * q4));
           half8_t A;
-          if constexpr (MODE == MODE_REF) {
+          if constexpr (CVT) {
+            A = *reinterpret_cast<const half8_t *>(cvt_lds + tokA * KTS + (32 * ks + 8 * q4) * 2);
+          } else if constexpr (MODE == MODE_REF) {
+            const uint2 kb = *reinterpret_cast<const uint2 *>(st + k_byte(tokA, 32 * ks + 8 * q4));
             half2_t p0 = (bytes01_plus1024(kb.x) + m1024) * ks2 + kz2;
             half2_t p1 = (bytes23_plus1024(kb.x) + m1024) * ks2 + kz2;
             half2_t p2 = (bytes01_plus1024(kb.y) + m1024) * ks2 + kz2;
             half2_t p3 = (bytes23_plus1024(kb.y) + m1024) * ks2 + kz2;
             A = half8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
           } else {
-            A = bytes8_centred(kb);
+            A = bytes8_centred(*reinterpret_cast<const uint2 *>(st + k_byte(tokA, 32 * ks + 8 * q4)));
           }
           const int g = MODE == MODE_AFFINE ? ks / 2 : 0;
 #pragma unroll
@@ -548,8 +588,13 @@ void k_attn_mfma(AttnArgs a) {
           for (int t2 = 0; t2 < NDT / G; ++t2) {
             const int dt = g * (NDT / G) + t2;
             const int d = 16 * dt + n;
-            const uint2 vb = *reinterpret_cast<const uint2 *>(st + v_pos_byte(D, tg, d, 8 * q4));
-            const half8_t A = MODE == MODE_REF ? bytes8_dequant_ref(vb, sc4, zc4) : bytes8_centred(vb);
+            half8_t A;
+            if constexpr (CVT) {
+              A = *reinterpret_cast<const half8_t *>(cvt_lds + 64 * KTS + d * VTS + (32 * tg + 8 * q4) * 2);
+            } else {
+              const uint2 vb = *reinterpret_cast<const uint2 *>(st + v_pos_byte(D, tg, d, 8 * q4));
+              A = MODE == MODE_REF ? bytes8_dequant_ref(vb, sc4, zc4) : bytes8_centred(vb);
+            }
 #pragma unroll
             for (int rt = 0; rt < NRT; ++rt) {
               oacc[rt][dt] = mfma16x16x32(A, Bh[rt], oacc[rt][dt]);
