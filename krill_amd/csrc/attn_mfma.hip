@@ -77,12 +77,12 @@ void k_attn_mfma(AttnArgs a) {
   constexpr int RR = 16 * NRT; // query rows of this wave
   constexpr int STAGE = mfma_stage_bytes(D, G);
   constexpr int NCH = STAGE / 1024;  // direct loads per block
-  // CVT (32-row waves in groups of four, affine, head_dim 128: chunked
-  // prefill): the four waves convert each staged block once, a quarter
-  // each, into fp16 K and V^T tiles in LDS that all four read, instead of
-  // every wave converting the whole block for its own rows; the tiles take
-  // the LDS of the third ring stage
-  constexpr bool CVT = W == 4 && TS == 1 && NRT == 2 && MODE == MODE_AFFINE && D == 128;
+  // CVT (four-wave groups, affine, head_dim 128: chunked prefill, the
+  // cascade's prefix pass): the four waves convert each staged block once,
+  // a quarter each, into fp16 K and V^T tiles in LDS that all four read,
+  // instead of every wave converting the whole block for its own rows; the
+  // tiles take the LDS of the third ring stage
+  constexpr bool CVT = W == 4 && TS == 1 && MODE == MODE_AFFINE && D == 128;
   constexpr int NST = CVT ? 2 : mfma_stages(D, G, W);
   constexpr int NK = 64 * D / 1024;  // runs holding the K bytes
   // W > 1: the fewest runs of a stage any wave of the group issues
